@@ -1,0 +1,239 @@
+"""Benchmark of the quantized-weight hot path on one MI355X.
+
+Headline (`value`): W4A16 dequant-fused GEMV at M=1 over one LLaMA-7B decoder block quantized
+INT4 asymmetric g128.  One step = one launch that multiplies the block's 7
+projections (Wq/Wk/Wv/Wo 4096x4096, W_gate/W_up 11008x4096, W_down 4096x11008) by bf16
+activations.  Steps rotate over `--copies` distinct copies of the packed block so the working
+set (16 x 105 MB) exceeds the 256 MB MALL and every step streams from HBM.
+
+Also reported (`components`): quantize GB/s (INT4 g128 and INT8 per-channel over the f32
+block), W4A16 GEMV at M=8/16, W8A16 GEMV at M=1 (config 1) and NF4 GEMV at M=1 (config 3).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+METRIC = "quantize GB/s; W4A16 GEMV GB/s (%HBM peak) at M=1; FP8 GEMM TFLOPS at M=4096"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=16)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-headline", action="store_true",
+                    help="time only the headline kernel (for profiler runs)")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the quantized "
+              "GEMV/GEMM shards by output rows with no collective; see DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from castforge_amd import ffi, ops, synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ffi.lib()
+    log(f"[bench] {ffi.version()} on {torch.cuda.get_device_name(dev)}")
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    def time_steps(fn, steps, warmup):
+        """Whole-job time per step (ms) and average per-launch time (ms) from event pairs."""
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        s, e = ev(), ev()
+        s.record()
+        for i in range(steps):
+            fn(i)
+        e.record()
+        e.synchronize()
+        per_step = s.elapsed_time(e) / steps
+        pairs = [(ev(), ev()) for _ in range(steps)]
+        for i in range(steps):
+            pairs[i][0].record()
+            fn(i)
+            pairs[i][1].record()
+        torch.cuda.synchronize()
+        per_launch = sum(a.elapsed_time(b) for a, b in pairs) / steps
+        return per_step, per_launch
+
+    # ---------------------------------------------------------------- block weights ----
+    t0 = time.time()
+    block_f32 = []
+    for tid, (name, n, k) in enumerate(synth.LLAMA7B_BLOCK):
+        block_f32.append(torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32) * 0.02)
+    packed0 = [ops.quantize_int4g(w, 128) for w in block_f32]
+    torch.cuda.synchronize()
+    log(f"[bench] generated + quantized block in {time.time() - t0:.1f}s")
+
+    # activations: bf16 N(0,1) with 1% of K channels x20 (host-generated, seeded)
+    def x_for(m, k, tid):
+        xb = synth.activations_bf16(0, 100 + tid, m, k)
+        return torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+
+    def w4_bytes(m):
+        tot = 0
+        for (_, n, k) in synth.LLAMA7B_BLOCK:
+            g = (k + 127) // 128
+            tot += n * k // 2 + n * g * 2 + n * ((g + 7) // 8) * 4 + 2 * m * k + 2 * m * n
+        return tot
+
+    copies = [packed0] + [[ops.Int4Packed(p.codes.clone(), p.scales.clone(), p.zeros.clone(),
+                                          p.n, p.k, p.group) for p in packed0]
+                          for _ in range(args.copies - 1)]
+
+    def gemv_case(m):
+        xs = [x_for(m, k, tid) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)]
+        ys = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
+        return lambda i: ops.gemv_w4a16_batched(xs, copies[i % len(copies)], ys)
+
+    components = {}
+    ms_step, ms_launch = time_steps(gemv_case(1), args.steps, args.warmup)
+    bytes_m1 = w4_bytes(1)
+    value = bytes_m1 / (ms_step * 1e-3) / 1e9
+    achieved = bytes_m1 / (ms_launch * 1e-3) / 1e9
+    log(f"[bench] W4A16 GEMV M=1: {ms_step * 1e3:.1f} us/step, {ms_launch * 1e3:.1f} us/launch, "
+        f"{value:.0f} GB/s (launch-only {achieved:.0f} GB/s)")
+
+    if not args.only_headline:
+        for m in (8, 16):
+            st, la = time_steps(gemv_case(m), max(20, args.steps // 4), 5)
+            components[f"w4a16_gemv_m{m}_GBps"] = round(w4_bytes(m) / (st * 1e-3) / 1e9, 1)
+            log(f"[bench] W4A16 GEMV M={m}: {st * 1e3:.1f} us/step {components[f'w4a16_gemv_m{m}_GBps']} GB/s")
+
+        # quantize over the f32 block (809 MB in, > MALL)
+        nel = sum(n * k for (_, n, k) in synth.LLAMA7B_BLOCK)
+        nrows = sum(n for (_, n, k) in synth.LLAMA7B_BLOCK)
+        ngroups = sum(n * ((k + 127) // 128) for (_, n, k) in synth.LLAMA7B_BLOCK)
+        st, _ = time_steps(lambda i: [ops.quantize_int4g(w, 128) for w in block_f32], 10, 2)
+        q4_bytes = nel * 4 + nel // 2 + ngroups * 2 + sum(n * (((k + 127) // 128 + 7) // 8) * 4
+                                                           for (_, n, k) in synth.LLAMA7B_BLOCK)
+        components["quantize_int4g128_GBps"] = round(q4_bytes / (st * 1e-3) / 1e9, 1)
+        st, _ = time_steps(lambda i: [ops.quantize_int8(w, 8, "channel", "half_even") for w in block_f32], 10, 2)
+        components["quantize_int8_channel_GBps"] = round((nel * 5 + nrows * 4) / (st * 1e-3) / 1e9, 1)
+        log(f"[bench] quantize int4g {components['quantize_int4g128_GBps']} GB/s, "
+            f"int8 {components['quantize_int8_channel_GBps']} GB/s")
+
+        # W8A16 GEMV M=1 over rotating copies of the INT8 block (config 1)
+        q8 = [ops.quantize_int8(w, 8, "channel", "half_even") for w in block_f32]
+        q8c = [q8] + [[(q.clone(), s.clone()) for q, s in q8] for _ in range(7)]
+        xs8 = [x_for(1, k, tid) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)]
+        ys8 = [torch.empty((1, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
+
+        def w8_step(i):
+            for x, (q, s), y in zip(xs8, q8c[i % len(q8c)], ys8):
+                ffi.call("castforge_hip_gemv_w8a16", x.data_ptr(), 1, q.shape[0], q.shape[1], q.data_ptr(),
+                         s.data_ptr(), ffi.GRAN_CHANNEL, y.data_ptr(), ffi.DTYPE_BF16,
+                         torch.cuda.current_stream().cuda_stream)
+        st, _ = time_steps(w8_step, 50, 5)
+        w8_bytes = nel + nrows * 4 + sum(2 * k + 2 * n for (_, n, k) in synth.LLAMA7B_BLOCK)
+        components["w8a16_gemv_m1_GBps"] = round(w8_bytes / (st * 1e-3) / 1e9, 1)
+        del q8, q8c
+
+        # NF4 b64 GEMV M=1 over W_gate/W_up/W_down (config 3)
+        nf = [ops.quantize_nf4(w, 64) for w in block_f32[4:]]
+        nfc = [nf] + [[ops.Nf4Packed(p.codes.clone(), p.absmax.clone(), p.n, p.k, p.block) for p in nf]
+                      for _ in range(15)]
+        xsn = [x_for(1, p.k, 4 + j) for j, p in enumerate(nf)]
+        ysn = [torch.empty((1, p.n), dtype=torch.bfloat16, device=dev) for p in nf]
+
+        def nf_step(i):
+            for x, p, y in zip(xsn, nfc[i % len(nfc)], ysn):
+                ffi.call("castforge_hip_gemv_nf4", x.data_ptr(), 1, p.n, p.k, p.block, p.codes.data_ptr(),
+                         p.absmax.data_ptr(), y.data_ptr(), ffi.DTYPE_BF16,
+                         torch.cuda.current_stream().cuda_stream)
+        st, _ = time_steps(nf_step, 50, 5)
+        nf_bytes = sum(p.nbytes() + 2 * p.k + 2 * p.n for p in nf)
+        components["nf4_gemv_m1_GBps"] = round(nf_bytes / (st * 1e-3) / 1e9, 1)
+        log(f"[bench] W8A16 M=1 {components['w8a16_gemv_m1_GBps']} GB/s, NF4 M=1 {components['nf4_gemv_m1_GBps']} GB/s")
+
+    components["w4a16_gemv_m1_GBps"] = round(value, 1)
+    components["w4a16_gemv_m1_pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBPS, 1)
+
+    # ---------------------------------------------------------------- CPU baseline ----
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(ROOT / "tests"))
+        import oracle_lib as O
+
+        host = [(p.codes.cpu().numpy().view(np.uint32), p.scales.cpu().numpy().view(np.uint16),
+                 p.zeros.cpu().numpy().view(np.uint32), p.n, p.k) for p in packed0]
+        xh = [synth.activations_bf16(0, 100 + tid, 1, k) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)]
+        passes, t_cpu = 0, 0.0
+        while t_cpu < 10.0 and passes < 8:
+            t1 = time.perf_counter()
+            for (c, s, z, n, k), x in zip(host, xh):
+                O.gemm_w4a16(x, c, s, z, n, k, 128)
+            t_cpu += time.perf_counter() - t1
+            passes += 1
+        cpu = {"value": round(bytes_m1 * passes / t_cpu / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port",
+               "sample": f"{passes} pass(es) of the full block W4A16 GEMV at M=1 with the oracle's "
+                         f"evaluator semantics (dequantize to f32, then the m,n,k f32 loop of "
+                         f"eval.rs:1465-1507), single thread, {t_cpu:.1f} s"}
+        log(f"[bench] cpu baseline {cpu['value']} GB/s over {passes} passes ({t_cpu:.1f}s)")
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_w4a16_gemv_m1.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4xbf16",
+        "data": "synthetic (N(0,0.02) weights, bf16 N(0,1) activations with 1% x20 channels)",
+        "config": {"workload": "llama7b_block_int4g128_w4a16_gemv_m1", "m": 1, "group": 128,
+                   "matrices": 7, "rotating_copies": len(copies),
+                   "value_is": "W4A16 GEMV GB/s at M=1 (algorithmic bytes / whole-job time per step)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": "skinny_qgemm_kernel<FMT_INT4>", "bytes_per_launch": bytes_m1,
+                     "us_per_launch": round(ms_launch * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "components": components,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

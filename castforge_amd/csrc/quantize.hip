@@ -1,0 +1,612 @@
+// Quantize / dequantize kernels for gfx950 and their C-ABI entry points.
+//
+// All kernels are HBM-bound streaming passes: 16-byte loads, wave64 butterfly reductions
+// for absmax/min/max, packed stores (4 int8 codes or 8 nibble codes per 32-bit store).
+// The arithmetic is the exact f32 sequence of the CPU reference: correctly rounded f32
+// division (hipcc's default), no contraction (this file is built with -ffp-contract=off),
+// round-half-even via rintf or half-away via roundf, NaN -> 0 as in Rust's `as i8`.
+#include "../../include/castforge_hip.h"
+#include "cfh_common.hpp"
+
+namespace cfh {
+namespace {
+
+constexpr int kBlock = 256;  // 4 waves
+
+__device__ __forceinline__ float round_sel(float x, int mode) {
+    return mode == CFH_ROUND_HALF_EVEN ? rintf(x) : roundf(x);
+}
+
+// formats.rs:676: (v / scale).round().clamp(qmin, qmax) as i8 — NaN maps to 0.
+__device__ __forceinline__ uint32_t quant_sym_byte(float v, float scale, float qmin, float qmax,
+                                                   int mode) {
+    float r = round_sel(v / scale, mode);
+    if (r != r) return 0u;
+    r = fminf(fmaxf(r, qmin), qmax);
+    return static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+}
+
+// Block-wide max of non-negative values (fmaxf ignores NaN like Rust's f32::max).
+__device__ __forceinline__ float block_max(float v, float *red) {
+    v = wave_max<64>(v);
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / 64; ++i) r = fmaxf(r, red[i]);
+    return r;
+}
+
+struct F32x4Src {
+    const float *p;
+    __device__ __forceinline__ float4 load4(int64_t i) const {
+        return reinterpret_cast<const float4 *>(p)[i];
+    }
+    __device__ __forceinline__ float load1(int64_t i) const { return p[i]; }
+};
+
+struct Bf16x4Src {
+    const uint16_t *p;
+    __device__ __forceinline__ float4 load4(int64_t i) const {
+        uint2 u = reinterpret_cast<const uint2 *>(p)[i];
+        return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                           __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+    }
+    __device__ __forceinline__ float load1(int64_t i) const { return bf16_to_f32(p[i]); }
+};
+
+// Encoders: how one value becomes one byte, given the row's absmax.
+struct SymEnc {
+    float qmin, qmax;
+    int mode;
+    __device__ __forceinline__ float scale_of(float amax) const {
+        return amax < 1e-12f ? 1.0f : amax / qmax;
+    }
+    __device__ __forceinline__ uint32_t enc(float v, float scale) const {
+        return quant_sym_byte(v, scale, qmin, qmax, mode);
+    }
+};
+
+struct Fp8Enc {
+    __device__ __forceinline__ float scale_of(float amax) const {
+        return amax < 1e-12f ? 1.0f : amax / 448.0f;
+    }
+    __device__ __forceinline__ uint32_t enc(float v, float scale) const {
+        return f32_to_e4m3fn(v / scale);
+    }
+};
+
+__device__ __forceinline__ float amax4(float a, float4 v) {
+    a = fmaxf(a, fabsf(v.x));
+    a = fmaxf(a, fabsf(v.y));
+    a = fmaxf(a, fabsf(v.z));
+    a = fmaxf(a, fabsf(v.w));
+    return a;
+}
+
+// One workgroup per row; the row stays in registers (VPT float4 per thread), so HBM sees
+// each input byte once.  Requires cols % 4 == 0 and 16-byte aligned rows.
+template <int VPT, class Src, class Enc>
+__global__ __launch_bounds__(kBlock) void rows_quant_reg_kernel(Src src, int64_t cols, Enc e,
+                                                                 uint8_t *__restrict__ codes,
+                                                                 float *__restrict__ scales) {
+    __shared__ float red[kBlock / 64];
+    const int64_t row = blockIdx.x;
+    const int64_t nv = cols >> 2;
+    const int64_t base = row * nv;
+    float4 v[VPT];
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
+        if (idx < nv) {
+            v[i] = src.load4(base + idx);
+            am = amax4(am, v[i]);
+        }
+    }
+    am = block_max(am, red);
+    const float scale = e.scale_of(am);
+    uint32_t *out = reinterpret_cast<uint32_t *>(codes + row * cols);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
+        if (idx < nv) {
+            out[idx] = e.enc(v[i].x, scale) | (e.enc(v[i].y, scale) << 8) |
+                       (e.enc(v[i].z, scale) << 16) | (e.enc(v[i].w, scale) << 24);
+        }
+    }
+    if (threadIdx.x == 0) scales[row] = scale;
+}
+
+// Any row length / alignment: two passes over the row (the second pass hits L2/MALL).
+template <class Src, class Enc>
+__global__ __launch_bounds__(kBlock) void rows_quant_generic_kernel(Src src, int64_t cols, Enc e,
+                                                                     uint8_t *__restrict__ codes,
+                                                                     float *__restrict__ scales) {
+    __shared__ float red[kBlock / 64];
+    const int64_t row = blockIdx.x;
+    const int64_t base = row * cols;
+    float am = 0.0f;
+    for (int64_t i = threadIdx.x; i < cols; i += kBlock) am = fmaxf(am, fabsf(src.load1(base + i)));
+    am = block_max(am, red);
+    const float scale = e.scale_of(am);
+    for (int64_t i = threadIdx.x; i < cols; i += kBlock)
+        codes[base + i] = static_cast<uint8_t>(e.enc(src.load1(base + i), scale));
+    if (threadIdx.x == 0) scales[row] = scale;
+}
+
+template <class Src, class Enc>
+void launch_rows_quant(Src src, bool vec_ok, int64_t rows, int64_t cols, Enc e, uint8_t *codes,
+                       float *scales, hipStream_t st) {
+    if (rows == 0) return;
+    require(rows <= 0x7fffffff, "too many rows for one launch");
+    const int64_t nv = cols / 4;
+    dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
+    if (vec_ok && nv <= 1 * kBlock)
+        rows_quant_reg_kernel<1><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    else if (vec_ok && nv <= 2 * kBlock)
+        rows_quant_reg_kernel<2><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    else if (vec_ok && nv <= 4 * kBlock)
+        rows_quant_reg_kernel<4><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    else if (vec_ok && nv <= 8 * kBlock)
+        rows_quant_reg_kernel<8><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    else if (vec_ok && nv <= 12 * kBlock)
+        rows_quant_reg_kernel<12><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    else if (vec_ok && nv <= 16 * kBlock)
+        rows_quant_reg_kernel<16><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    else
+        rows_quant_generic_kernel<<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    check_launch("rows_quant");
+}
+
+// ---- per-tensor (reference QuantizeWeightsPass) -----------------------------------------
+// The absmax accumulates into scales[0] viewed as a u32 (non-negative floats order like
+// their bit patterns); the quantize kernel derives the scale from it; a last one-thread
+// kernel replaces the absmax by the scale.
+__global__ void fill_u32_kernel(uint32_t *p, uint32_t v) { *p = v; }
+
+__global__ __launch_bounds__(kBlock) void tensor_absmax_kernel(const float *__restrict__ src,
+                                                               int64_t n, uint32_t *acc) {
+    __shared__ float red[kBlock / 64];
+    float am = 0.0f;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+        const int64_t nv = n >> 2;
+        for (int64_t i = t; i < nv; i += stride)
+            am = amax4(am, reinterpret_cast<const float4 *>(src)[i]);
+        for (int64_t i = (nv << 2) + t; i < n; i += stride) am = fmaxf(am, fabsf(src[i]));
+    } else {
+        for (int64_t i = t; i < n; i += stride) am = fmaxf(am, fabsf(src[i]));
+    }
+    am = block_max(am, red);
+    if (threadIdx.x == 0) atomicMax(acc, __float_as_uint(am));
+}
+
+__global__ __launch_bounds__(kBlock) void tensor_quant_kernel(const float *__restrict__ src,
+                                                              int64_t n, SymEnc e,
+                                                              const uint32_t *acc,
+                                                              uint8_t *__restrict__ codes) {
+    const float scale = e.scale_of(__uint_as_float(*acc));
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) &&
+                     ((reinterpret_cast<uintptr_t>(codes) & 3u) == 0);
+    int64_t done = 0;
+    if (vec) {
+        const int64_t nv = n >> 2;
+        for (int64_t i = t; i < nv; i += stride) {
+            float4 v = reinterpret_cast<const float4 *>(src)[i];
+            reinterpret_cast<uint32_t *>(codes)[i] =
+                e.enc(v.x, scale) | (e.enc(v.y, scale) << 8) | (e.enc(v.z, scale) << 16) |
+                (e.enc(v.w, scale) << 24);
+        }
+        done = nv << 2;
+    }
+    for (int64_t i = done + t; i < n; i += stride) codes[i] = static_cast<uint8_t>(e.enc(src[i], scale));
+}
+
+__global__ void tensor_scale_finalize_kernel(float *scales, SymEnc e) {
+    scales[0] = e.scale_of(scales[0]);
+}
+
+int grid_for(int64_t items, int per_block, int cap) {
+    int64_t g = (items + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return static_cast<int>(g);
+}
+
+// ---- INT4 asymmetric group-wise ------------------------------------------------------------
+// A task is (row, zero-word) = up to 8 groups; each thread owns one code word (8 elements),
+// so a task has GROUP threads and a group has GROUP/8 adjacent lanes.
+__device__ __forceinline__ uint16_t int4_scale_bits(float mx, float mn) {
+    const float range = mx - mn;
+    uint16_t h = range >= 1e-12f ? f32_to_f16_rne(range / 15.0f) : static_cast<uint16_t>(0x3C00);
+    if (h == 0) h = 0x0001;
+    if (h == 0x7C00) h = 0x7BFF;
+    return h;
+}
+
+template <int GROUP>
+__global__ __launch_bounds__(kBlock) void int4g_quant_kernel(const float *__restrict__ src,
+                                                             int64_t rows, int64_t cols,
+                                                             uint32_t *__restrict__ codes,
+                                                             uint16_t *__restrict__ scales,
+                                                             uint32_t *__restrict__ zeros) {
+    constexpr int T = GROUP;          // threads per task
+    constexpr int TPB = kBlock / T;   // tasks per block
+    constexpr int TPG = GROUP / 8;    // threads per group
+    __shared__ uint32_t zpart[kBlock / 64];
+    const int64_t KW = cols >> 3, G = (cols + GROUP - 1) / GROUP, ZW = (G + 7) >> 3;
+    const int64_t task = static_cast<int64_t>(blockIdx.x) * TPB + threadIdx.x / T;
+    const int t = threadIdx.x % T;
+    const int64_t row = task / ZW, zw = task - row * ZW;
+    const bool task_ok = row < rows;
+    const int64_t w = zw * T + t;
+    const bool ok = task_ok && w < KW;
+    float x[8];
+    float mx = -INFINITY, mn = INFINITY;
+    if (ok) {
+        const float4 *p = reinterpret_cast<const float4 *>(src + row * cols + w * 8);
+        float4 a = p[0], b = p[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, x[i]); mn = fminf(mn, x[i]); }
+    }
+    mx = wave_max<TPG>(mx);
+    mn = wave_min<TPG>(mn);
+    const uint16_t h = int4_scale_bits(mx, mn);
+    const float s = f16_to_f32(h);
+    float zf = rintf(-mn / s);
+    if (zf != zf) zf = 0.0f;
+    zf = fminf(fmaxf(zf, 0.0f), 15.0f);
+    const int gi = t / TPG;  // group within the task
+    uint32_t zn = 0;
+    if (ok) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float r = rintf(x[i] / s);
+            if (r != r) r = 0.0f;
+            const float qf = fminf(fmaxf(r + zf, 0.0f), 15.0f);
+            word |= static_cast<uint32_t>(qf) << (4 * i);
+        }
+        codes[row * KW + w] = word;
+        if (t % TPG == 0) {
+            scales[row * G + zw * 8 + gi] = h;
+            zn = static_cast<uint32_t>(zf) << (4 * gi);
+        }
+    }
+    if constexpr (T <= 64) {
+        zn = wave_or<T>(zn);
+        if (t == 0 && task_ok) zeros[row * ZW + zw] = zn;
+    } else {
+        zn = wave_or<64>(zn);
+        if ((threadIdx.x & 63) == 0) zpart[threadIdx.x >> 6] = zn;
+        __syncthreads();
+        if (t == 0 && task_ok) {
+            uint32_t z = 0;
+            const int w0 = (threadIdx.x >> 6);
+#pragma unroll
+            for (int i = 0; i < T / 64; ++i) z |= zpart[w0 + i];
+            zeros[row * ZW + zw] = z;
+        }
+    }
+}
+
+// ---- NF4 block-wise ------------------------------------------------------------------------
+__constant__ float kNf4Table[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+// code = #{i : x > 0.5f*(T[i]+T[i+1])}; NaN -> 7.  The midpoints are exact f32 constants.
+__device__ __forceinline__ uint32_t nf4_code(float x) {
+    if (x != x) return 7u;
+    constexpr float m0 = 0.5f * (-1.0f + -0.6961928009986877f);
+    constexpr float m1 = 0.5f * (-0.6961928009986877f + -0.5250730514526367f);
+    constexpr float m2 = 0.5f * (-0.5250730514526367f + -0.39491748809814453f);
+    constexpr float m3 = 0.5f * (-0.39491748809814453f + -0.28444138169288635f);
+    constexpr float m4 = 0.5f * (-0.28444138169288635f + -0.18477343022823334f);
+    constexpr float m5 = 0.5f * (-0.18477343022823334f + -0.09105003625154495f);
+    constexpr float m6 = 0.5f * (-0.09105003625154495f + 0.0f);
+    constexpr float m7 = 0.5f * (0.0f + 0.07958029955625534f);
+    constexpr float m8 = 0.5f * (0.07958029955625534f + 0.16093020141124725f);
+    constexpr float m9 = 0.5f * (0.16093020141124725f + 0.24611230194568634f);
+    constexpr float m10 = 0.5f * (0.24611230194568634f + 0.33791524171829224f);
+    constexpr float m11 = 0.5f * (0.33791524171829224f + 0.44070982933044434f);
+    constexpr float m12 = 0.5f * (0.44070982933044434f + 0.5626170039176941f);
+    constexpr float m13 = 0.5f * (0.5626170039176941f + 0.7229568362236023f);
+    constexpr float m14 = 0.5f * (0.7229568362236023f + 1.0f);
+    uint32_t c = (x > m0) + (x > m1) + (x > m2) + (x > m3) + (x > m4) + (x > m5) + (x > m6) +
+                 (x > m7) + (x > m8) + (x > m9) + (x > m10) + (x > m11) + (x > m12) + (x > m13) +
+                 (x > m14);
+    return c;
+}
+
+template <int BLOCK>
+__global__ __launch_bounds__(kBlock) void nf4_quant_kernel(const float *__restrict__ src,
+                                                           int64_t rows, int64_t cols,
+                                                           uint32_t *__restrict__ codes,
+                                                           float *__restrict__ absmax) {
+    constexpr int TPG = BLOCK / 8;  // threads per quantization block
+    const int64_t KW = cols >> 3, B = (cols + BLOCK - 1) / BLOCK, KWp = B * TPG;
+    const int64_t gt = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t row = gt / KWp, w = gt - row * KWp;
+    const bool ok = row < rows && w < KW;
+    float x[8];
+    float am = 0.0f;
+    if (ok) {
+        const float4 *p = reinterpret_cast<const float4 *>(src + row * cols + w * 8);
+        float4 a = p[0], b = p[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(x[i]));
+    }
+    am = wave_max<TPG>(am);
+    const float st = am < 1e-12f ? 1.0f : am;
+    if (ok) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) word |= nf4_code(x[i] / st) << (4 * i);
+        codes[row * KW + w] = word;
+        if (w % TPG == 0) absmax[row * B + w / TPG] = st;
+    }
+}
+
+// ---- dequantize (TensorStore::resolve_f32_attr for the packed backings) -------------------
+__global__ void dequant_int8_kernel(const int8_t *__restrict__ q, const float *__restrict__ scales,
+                                    int64_t rows, int64_t cols, int per_row,
+                                    float *__restrict__ out) {
+    const int64_t n = rows * cols;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const float s = per_row ? scales[i / cols] : scales[0];
+        out[i] = static_cast<float>(static_cast<int32_t>(q[i])) * s;
+    }
+}
+
+__global__ void dequant_int4g_kernel(const uint32_t *__restrict__ codes,
+                                     const uint16_t *__restrict__ scales,
+                                     const uint32_t *__restrict__ zeros, int64_t rows, int64_t cols,
+                                     int64_t group, float *__restrict__ out) {
+    const int64_t KW = cols >> 3, G = (cols + group - 1) / group, ZW = (G + 7) >> 3;
+    const int64_t nw = rows * KW;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nw; i += stride) {
+        const int64_t r = i / KW, w = i - r * KW;
+        const uint32_t word = codes[i];
+        for (int j = 0; j < 8; ++j) {
+            const int64_t k = w * 8 + j, g = k / group;
+            const int32_t z = static_cast<int32_t>((zeros[r * ZW + (g >> 3)] >> (4 * (g & 7))) & 15u);
+            const int32_t q = static_cast<int32_t>((word >> (4 * j)) & 15u);
+            out[r * cols + k] = static_cast<float>(q - z) * f16_to_f32(scales[r * G + g]);
+        }
+    }
+}
+
+__global__ void dequant_nf4_kernel(const uint32_t *__restrict__ codes,
+                                   const float *__restrict__ absmax, int64_t rows, int64_t cols,
+                                   int64_t block, float *__restrict__ out) {
+    const int64_t KW = cols >> 3, B = (cols + block - 1) / block;
+    const int64_t nw = rows * KW;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nw; i += stride) {
+        const int64_t r = i / KW, w = i - r * KW;
+        const uint32_t word = codes[i];
+        for (int j = 0; j < 8; ++j) {
+            const int64_t k = w * 8 + j;
+            out[r * cols + k] = kNf4Table[(word >> (4 * j)) & 15u] * absmax[r * B + k / block];
+        }
+    }
+}
+
+__global__ void dequant_fp8_kernel(const uint8_t *__restrict__ q, const float *__restrict__ scales,
+                                   int64_t rows, int64_t cols, float *__restrict__ out) {
+    const int64_t n = rows * cols;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = e4m3fn_to_f32(q[i]) * scales[i / cols];
+}
+
+constexpr int kGridCap = 256 * 64;
+
+bool pow2_in(int64_t v, int64_t lo, int64_t hi) {
+    return v >= lo && v <= hi && (v & (v - 1)) == 0;
+}
+
+void check_shape(int64_t rows, int64_t cols) {
+    require(rows >= 0 && cols >= 0, "rows and cols must be non-negative");
+    require(cols == 0 || rows <= INT64_MAX / cols, "rows * cols overflows");
+}
+
+}  // namespace
+}  // namespace cfh
+
+using namespace cfh;
+
+extern "C" {
+
+int32_t castforge_hip_quantize_int8(const float *src, int64_t rows, int64_t cols, int32_t bits,
+                                    int32_t granularity, int32_t round_mode, int8_t *codes,
+                                    float *scales, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(granularity == CFH_GRAN_TENSOR || granularity == CFH_GRAN_CHANNEL,
+                "granularity must be CFH_GRAN_TENSOR or CFH_GRAN_CHANNEL");
+        require(round_mode == CFH_ROUND_HALF_AWAY || round_mode == CFH_ROUND_HALF_EVEN,
+                "round_mode must be CFH_ROUND_HALF_AWAY or CFH_ROUND_HALF_EVEN");
+        require(scales != nullptr, "scales must not be NULL");
+        const int64_t n = rows * cols;
+        require(n == 0 || (src && codes), "src and codes must not be NULL");
+        // formats.rs:654-660: bits == 4 -> [-8, 7], anything else -> [-128, 127]
+        SymEnc e{bits == 4 ? -8.0f : -128.0f, bits == 4 ? 7.0f : 127.0f, round_mode};
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        if (granularity == CFH_GRAN_CHANNEL) {
+            const bool vec = (cols % 4 == 0) && aligned(src, 16) && aligned(codes, 4);
+            launch_rows_quant(F32x4Src{src}, vec, rows, cols, e,
+                              reinterpret_cast<uint8_t *>(codes), scales, st);
+            return;
+        }
+        uint32_t *acc = reinterpret_cast<uint32_t *>(scales);
+        fill_u32_kernel<<<1, 1, 0, st>>>(acc, 0u);
+        check_launch("fill_u32");
+        if (n > 0) {
+            tensor_absmax_kernel<<<grid_for(n / 4 + 1, kBlock, kGridCap), kBlock, 0, st>>>(src, n, acc);
+            check_launch("tensor_absmax");
+            tensor_quant_kernel<<<grid_for(n / 4 + 1, kBlock, kGridCap), kBlock, 0, st>>>(
+                src, n, e, acc, reinterpret_cast<uint8_t *>(codes));
+            check_launch("tensor_quant");
+        }
+        tensor_scale_finalize_kernel<<<1, 1, 0, st>>>(scales, e);
+        check_launch("tensor_scale_finalize");
+    });
+}
+
+int32_t castforge_hip_dequantize_int8(const int8_t *codes, const float *scales, int64_t rows,
+                                      int64_t cols, int32_t granularity, float *out, void *stream,
+                                      char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(granularity == CFH_GRAN_TENSOR || granularity == CFH_GRAN_CHANNEL,
+                "granularity must be CFH_GRAN_TENSOR or CFH_GRAN_CHANNEL");
+        const int64_t n = rows * cols;
+        if (n == 0) return;
+        require(codes && scales && out, "codes, scales and out must not be NULL");
+        dequant_int8_kernel<<<grid_for(n, kBlock, kGridCap), kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+            codes, scales, rows, cols, granularity == CFH_GRAN_CHANNEL, out);
+        check_launch("dequant_int8");
+    });
+}
+
+int32_t castforge_hip_quantize_int4g(const float *src, int64_t rows, int64_t cols, int64_t group,
+                                     uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros,
+                                     void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(pow2_in(group, 8, 256), "group must be a power of two in [8, 256]");
+        require(cols % 8 == 0, "cols must be a multiple of 8 (8 codes per 32-bit word)");
+        if (rows == 0 || cols == 0) return;
+        require(src && codes && scales_f16 && zeros, "buffers must not be NULL");
+        require(aligned(src, 16), "src must be 16-byte aligned");
+        require(aligned(codes, 4) && aligned(scales_f16, 2) && aligned(zeros, 4),
+                "codes/zeros must be 4-byte and scales 2-byte aligned");
+        const int64_t G = (cols + group - 1) / group, ZW = (G + 7) / 8;
+        const int64_t tasks = rows * ZW, tpb = kBlock / group;
+        const int64_t blocks = (tasks + tpb - 1) / tpb;
+        require(blocks <= 0x7fffffff, "tensor too large for one launch");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        dim3 g(static_cast<unsigned>(blocks)), b(kBlock);
+        switch (group) {
+        case 8: int4g_quant_kernel<8><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
+        case 16: int4g_quant_kernel<16><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
+        case 32: int4g_quant_kernel<32><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
+        case 64: int4g_quant_kernel<64><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
+        case 128: int4g_quant_kernel<128><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
+        default: int4g_quant_kernel<256><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
+        }
+        check_launch("int4g_quant");
+    });
+}
+
+int32_t castforge_hip_dequantize_int4g(const uint32_t *codes, const uint16_t *scales_f16,
+                                       const uint32_t *zeros, int64_t rows, int64_t cols,
+                                       int64_t group, float *out, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(group >= 8 && group % 8 == 0, "group must be a positive multiple of 8");
+        require(cols % 8 == 0, "cols must be a multiple of 8");
+        if (rows == 0 || cols == 0) return;
+        require(codes && scales_f16 && zeros && out, "buffers must not be NULL");
+        dequant_int4g_kernel<<<grid_for(rows * (cols / 8), kBlock, kGridCap), kBlock, 0,
+                               static_cast<hipStream_t>(stream)>>>(codes, scales_f16, zeros, rows,
+                                                                   cols, group, out);
+        check_launch("dequant_int4g");
+    });
+}
+
+int32_t castforge_hip_quantize_nf4(const float *src, int64_t rows, int64_t cols, int64_t block,
+                                   uint32_t *codes, float *absmax, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(pow2_in(block, 8, 512), "block must be a power of two in [8, 512]");
+        require(cols % 8 == 0, "cols must be a multiple of 8 (8 codes per 32-bit word)");
+        if (rows == 0 || cols == 0) return;
+        require(src && codes && absmax, "buffers must not be NULL");
+        require(aligned(src, 16) && aligned(codes, 4) && aligned(absmax, 4),
+                "src must be 16-byte aligned, codes/absmax 4-byte aligned");
+        const int64_t B = (cols + block - 1) / block, KWp = B * (block / 8);
+        const int64_t threads = rows * KWp, blocks = (threads + kBlock - 1) / kBlock;
+        require(blocks <= 0x7fffffff, "tensor too large for one launch");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        dim3 g(static_cast<unsigned>(blocks)), b(kBlock);
+        switch (block) {
+        case 8: nf4_quant_kernel<8><<<g, b, 0, st>>>(src, rows, cols, codes, absmax); break;
+        case 16: nf4_quant_kernel<16><<<g, b, 0, st>>>(src, rows, cols, codes, absmax); break;
+        case 32: nf4_quant_kernel<32><<<g, b, 0, st>>>(src, rows, cols, codes, absmax); break;
+        case 64: nf4_quant_kernel<64><<<g, b, 0, st>>>(src, rows, cols, codes, absmax); break;
+        case 128: nf4_quant_kernel<128><<<g, b, 0, st>>>(src, rows, cols, codes, absmax); break;
+        case 256: nf4_quant_kernel<256><<<g, b, 0, st>>>(src, rows, cols, codes, absmax); break;
+        default: nf4_quant_kernel<512><<<g, b, 0, st>>>(src, rows, cols, codes, absmax); break;
+        }
+        check_launch("nf4_quant");
+    });
+}
+
+int32_t castforge_hip_dequantize_nf4(const uint32_t *codes, const float *absmax, int64_t rows,
+                                     int64_t cols, int64_t block, float *out, void *stream,
+                                     char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(block >= 8 && block % 8 == 0, "block must be a positive multiple of 8");
+        require(cols % 8 == 0, "cols must be a multiple of 8");
+        if (rows == 0 || cols == 0) return;
+        require(codes && absmax && out, "buffers must not be NULL");
+        dequant_nf4_kernel<<<grid_for(rows * (cols / 8), kBlock, kGridCap), kBlock, 0,
+                             static_cast<hipStream_t>(stream)>>>(codes, absmax, rows, cols, block, out);
+        check_launch("dequant_nf4");
+    });
+}
+
+int32_t castforge_hip_quantize_fp8(const void *src, int32_t src_dtype, int64_t rows, int64_t cols,
+                                   uint8_t *codes, float *scales, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(src_dtype == CFH_DTYPE_F32 || src_dtype == CFH_DTYPE_BF16,
+                "src_dtype must be CFH_DTYPE_F32 or CFH_DTYPE_BF16");
+        if (rows == 0) return;
+        require(scales != nullptr, "scales must not be NULL");
+        require(cols == 0 || (src && codes), "src and codes must not be NULL");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        if (src_dtype == CFH_DTYPE_F32) {
+            const bool vec = (cols % 4 == 0) && aligned(src, 16) && aligned(codes, 4);
+            launch_rows_quant(F32x4Src{static_cast<const float *>(src)}, vec, rows, cols, Fp8Enc{},
+                              codes, scales, st);
+        } else {
+            const bool vec = (cols % 4 == 0) && aligned(src, 8) && aligned(codes, 4);
+            launch_rows_quant(Bf16x4Src{static_cast<const uint16_t *>(src)}, vec, rows, cols,
+                              Fp8Enc{}, codes, scales, st);
+        }
+    });
+}
+
+int32_t castforge_hip_dequantize_fp8(const uint8_t *codes, const float *scales, int64_t rows,
+                                     int64_t cols, float *out, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        const int64_t n = rows * cols;
+        if (n == 0) return;
+        require(codes && scales && out, "buffers must not be NULL");
+        dequant_fp8_kernel<<<grid_for(n, kBlock, kGridCap), kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+            codes, scales, rows, cols, out);
+        check_launch("dequant_fp8");
+    });
+}
+
+}  // extern "C"

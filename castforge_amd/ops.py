@@ -1,0 +1,212 @@
+"""Torch-tensor front end over the C ABI: allocates outputs on the input's device and enqueues
+the HIP kernels on torch's current stream.  PyTorch is only used for device memory and
+streams; every computation happens in libcastforge_hip.so.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ffi
+from .ffi import DTYPE_BF16, DTYPE_F32, GRAN_CHANNEL, GRAN_TENSOR, ROUND_HALF_AWAY, ROUND_HALF_EVEN
+
+_ROUND = {"half_away": ROUND_HALF_AWAY, "half_even": ROUND_HALF_EVEN}
+_GRAN = {"tensor": GRAN_TENSOR, "channel": GRAN_CHANNEL}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dev(t: torch.Tensor) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError("castforge_amd kernels take device tensors (HIP); got a CPU tensor")
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return t
+
+
+def _out_dtype(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return DTYPE_F32
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise ValueError(f"output dtype must be float32 or bfloat16, got {dtype}")
+
+
+# ---------------------------------------------------------------------------- INT8 ----
+def quantize_int8(w: torch.Tensor, bits: int = 8, granularity: str = "channel",
+                  round: str = "half_even") -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric absmax INT8 (or INT4-in-int8 when bits=4). Returns (codes i8, scales f32)."""
+    w = _dev(w)
+    if w.dtype != torch.float32:
+        raise ValueError("quantize_int8 takes float32 weights")
+    rows, cols = (w.shape[0], w[0].numel()) if w.dim() >= 2 else (1, w.numel())
+    codes = torch.empty(w.shape, dtype=torch.int8, device=w.device)
+    scales = torch.empty(rows if granularity == "channel" else 1, dtype=torch.float32, device=w.device)
+    if granularity == "tensor":
+        rows, cols = 1, w.numel()
+    ffi.call("castforge_hip_quantize_int8", _ptr(w), rows, cols, bits, _GRAN[granularity],
+             _ROUND[round], _ptr(codes), _ptr(scales), _stream(w))
+    return codes, scales
+
+
+def dequantize_int8(codes: torch.Tensor, scales: torch.Tensor, granularity: str = "channel") -> torch.Tensor:
+    codes = _dev(codes)
+    rows = codes.shape[0] if codes.dim() >= 2 else 1
+    cols = codes.numel() // max(rows, 1) if rows else 0
+    out = torch.empty(codes.shape, dtype=torch.float32, device=codes.device)
+    ffi.call("castforge_hip_dequantize_int8", _ptr(codes), _ptr(_dev(scales)), rows, cols,
+             _GRAN[granularity], _ptr(out), _stream(codes))
+    return out
+
+
+# --------------------------------------------------------------------------- INT4g ----
+@dataclass
+class Int4Packed:
+    """INT4 asymmetric group-wise weights: codes u32 [N, K/8], scales f16 [N, G], zeros u32 [N, ceil(G/8)]."""
+    codes: torch.Tensor
+    scales: torch.Tensor
+    zeros: torch.Tensor
+    n: int
+    k: int
+    group: int
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.codes, self.scales, self.zeros))
+
+
+def quantize_int4g(w: torch.Tensor, group: int = 128) -> Int4Packed:
+    w = _dev(w)
+    if w.dtype != torch.float32 or w.dim() != 2:
+        raise ValueError("quantize_int4g takes a 2-D float32 [N, K] weight")
+    n, k = w.shape
+    g = (k + group - 1) // group
+    codes = torch.empty((n, k // 8), dtype=torch.int32, device=w.device)
+    scales = torch.empty((n, g), dtype=torch.float16, device=w.device)
+    zeros = torch.empty((n, (g + 7) // 8), dtype=torch.int32, device=w.device)
+    ffi.call("castforge_hip_quantize_int4g", _ptr(w), n, k, group, _ptr(codes), _ptr(scales),
+             _ptr(zeros), _stream(w))
+    return Int4Packed(codes, scales, zeros, n, k, group)
+
+
+def dequantize_int4g(p: Int4Packed) -> torch.Tensor:
+    out = torch.empty((p.n, p.k), dtype=torch.float32, device=p.codes.device)
+    ffi.call("castforge_hip_dequantize_int4g", _ptr(p.codes), _ptr(p.scales), _ptr(p.zeros), p.n,
+             p.k, p.group, _ptr(out), _stream(p.codes))
+    return out
+
+
+# ----------------------------------------------------------------------------- NF4 ----
+@dataclass
+class Nf4Packed:
+    codes: torch.Tensor
+    absmax: torch.Tensor
+    n: int
+    k: int
+    block: int
+
+    def nbytes(self) -> int:
+        return self.codes.numel() * 4 + self.absmax.numel() * 4
+
+
+def quantize_nf4(w: torch.Tensor, block: int = 64) -> Nf4Packed:
+    w = _dev(w)
+    if w.dtype != torch.float32 or w.dim() != 2:
+        raise ValueError("quantize_nf4 takes a 2-D float32 [N, K] weight")
+    n, k = w.shape
+    nb = (k + block - 1) // block
+    codes = torch.empty((n, k // 8), dtype=torch.int32, device=w.device)
+    absmax = torch.empty((n, nb), dtype=torch.float32, device=w.device)
+    ffi.call("castforge_hip_quantize_nf4", _ptr(w), n, k, block, _ptr(codes), _ptr(absmax), _stream(w))
+    return Nf4Packed(codes, absmax, n, k, block)
+
+
+def dequantize_nf4(p: Nf4Packed) -> torch.Tensor:
+    out = torch.empty((p.n, p.k), dtype=torch.float32, device=p.codes.device)
+    ffi.call("castforge_hip_dequantize_nf4", _ptr(p.codes), _ptr(p.absmax), p.n, p.k, p.block,
+             _ptr(out), _stream(p.codes))
+    return out
+
+
+# ----------------------------------------------------------------------------- FP8 ----
+def quantize_fp8(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row E4M3FN with scale absmax/448; v is float32 or bfloat16 [R, C]."""
+    v = _dev(v)
+    if v.dim() != 2:
+        raise ValueError("quantize_fp8 takes a 2-D [rows, cols] tensor")
+    if v.dtype == torch.float32:
+        dt = DTYPE_F32
+    elif v.dtype == torch.bfloat16:
+        dt = DTYPE_BF16
+    else:
+        raise ValueError("quantize_fp8 takes float32 or bfloat16")
+    r, c = v.shape
+    codes = torch.empty((r, c), dtype=torch.uint8, device=v.device)
+    scales = torch.empty(r, dtype=torch.float32, device=v.device)
+    ffi.call("castforge_hip_quantize_fp8", _ptr(v), dt, r, c, _ptr(codes), _ptr(scales), _stream(v))
+    return codes, scales
+
+
+def dequantize_fp8(codes: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    codes = _dev(codes)
+    r, c = codes.shape
+    out = torch.empty((r, c), dtype=torch.float32, device=codes.device)
+    ffi.call("castforge_hip_dequantize_fp8", _ptr(codes), _ptr(_dev(scales)), r, c, _ptr(out),
+             _stream(codes))
+    return out
+
+
+# ------------------------------------------------------------------- fused matmuls ----
+def _check_x(x: torch.Tensor, k: int) -> torch.Tensor:
+    x = _dev(x)
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != k:
+        raise ValueError(f"x must be bfloat16 [M, {k}]")
+    return x
+
+
+def gemm_w4a16(x: torch.Tensor, p: Int4Packed, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    x = _check_x(x, p.k)
+    y = torch.empty((x.shape[0], p.n), dtype=out_dtype, device=x.device)
+    ffi.call("castforge_hip_gemv_w4a16", _ptr(x), x.shape[0], p.n, p.k, p.group, _ptr(p.codes),
+             _ptr(p.scales), _ptr(p.zeros), _ptr(y), _out_dtype(out_dtype), _stream(x))
+    return y
+
+
+def gemm_w8a16(x: torch.Tensor, codes: torch.Tensor, scales: torch.Tensor,
+               granularity: str = "channel", out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    n, k = codes.shape
+    x = _check_x(x, k)
+    y = torch.empty((x.shape[0], n), dtype=out_dtype, device=x.device)
+    ffi.call("castforge_hip_gemv_w8a16", _ptr(x), x.shape[0], n, k, _ptr(_dev(codes)),
+             _ptr(_dev(scales)), _GRAN[granularity], _ptr(y), _out_dtype(out_dtype), _stream(x))
+    return y
+
+
+def gemm_nf4(x: torch.Tensor, p: Nf4Packed, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    x = _check_x(x, p.k)
+    y = torch.empty((x.shape[0], p.n), dtype=out_dtype, device=x.device)
+    ffi.call("castforge_hip_gemv_nf4", _ptr(x), x.shape[0], p.n, p.k, p.block, _ptr(p.codes),
+             _ptr(p.absmax), _ptr(y), _out_dtype(out_dtype), _stream(x))
+    return y
+
+
+def gemv_w4a16_batched(xs: list[torch.Tensor], ps: list[Int4Packed], ys: list[torch.Tensor]) -> None:
+    """One launch for several W4A16 problems with the same M (1..16); outputs preallocated."""
+    if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
+        raise ValueError("xs, ps, ys must have the same length <= 8")
+    m = xs[0].shape[0]
+    arr = (ffi.W4A16Problem * max(1, len(ps)))()
+    for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
+        _check_x(x, p.k)
+        if x.shape[0] != m or y.shape != (m, p.n):
+            raise ValueError("all problems must share M and y must be [M, n]")
+        arr[i] = ffi.W4A16Problem(_ptr(x), _ptr(p.codes), _ptr(p.scales), _ptr(p.zeros), _ptr(y),
+                                  p.n, p.k, p.group)
+    yd = _out_dtype(ys[0].dtype)
+    ffi.call("castforge_hip_gemv_w4a16_batched", arr, len(ps), m, yd, _stream(xs[0]))

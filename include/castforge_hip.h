@@ -1,0 +1,148 @@
+/*
+ * CastForge MI355X quantized-weight hot path — C ABI (`include/castforge_hip.h`).
+ *
+ * Sits beside the unchanged `include/castforge.h` of sungdomo/CastForge and follows the
+ * conventions of its FFI (src/ffi.rs:13-215, include/castforge.h:18-52):
+ *   - every entry point returns int32_t: 0 success, 1 error (message in *out_error),
+ *     2 internal exception caught; nothing throws or aborts across the ABI;
+ *   - *out_error (may be NULL) is cleared on entry and, when set, is a heap string the caller
+ *     frees with castforge_hip_free_string (ffi.rs:25-31);
+ *   - the caller owns every buffer; the library allocates no device memory;
+ *   - buffers named src/codes/scales/zeros/absmax/x/y are DEVICE pointers; `stream` is a
+ *     hipStream_t (NULL = the null stream); work is enqueued asynchronously on it;
+ *   - shapes are int64 element counts; weights are row-major [N, K] with K contiguous, the
+ *     `packed_rhs` layout of the reference (passes/weights/fold.rs:549-554);
+ *   - calls on different streams are independent; no global mutable state.
+ *
+ * Packed formats (new in this library; the reference stores one i8 per element):
+ *   INT8  : codes i8 [N, K]; scales f32 [N] (per channel) or [1] (per tensor).
+ *   INT4g : codes u32 [N, K/8], element k in bits 4*(k%8); scales f16 bits [N, G];
+ *           zeros u32 [N, ceil(G/8)], group g in bits 4*(g%8); G = ceil(K/group).
+ *           dequant = (q - z) * f32(scale).
+ *   NF4   : codes u32 [N, K/8] (same packing); absmax f32 [N, ceil(K/block)].
+ *           dequant = NF4_TABLE[q] * absmax.
+ *   FP8   : codes u8 [R, C] OCP E4M3FN; scales f32 [R]; dequant = e4m3(q) * scale.
+ */
+#ifndef CASTFORGE_HIP_H
+#define CASTFORGE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CASTFORGE_HIP_ABI_VERSION 1
+#define CFH_MAX_BATCH 8
+
+/* Rounding rule of the integer quantizers.  HALF_AWAY is Rust's f32::round used by the
+ * reference (formats.rs:676, schemes.rs:546); HALF_EVEN is IEEE round-to-nearest-even. */
+enum { CFH_ROUND_HALF_AWAY = 0, CFH_ROUND_HALF_EVEN = 1 };
+/* Scale granularity of the symmetric INT8/INT4 quantizer. */
+enum { CFH_GRAN_TENSOR = 0, CFH_GRAN_CHANNEL = 1 };
+/* Element types of activations / outputs. */
+enum { CFH_DTYPE_F32 = 0, CFH_DTYPE_BF16 = 1 };
+
+/* ---- library ---------------------------------------------------------------------------- */
+
+/* Mirrors castforge_version (castforge.h:18-21, ffi.rs:13-23): static string, do not free. */
+const char *castforge_hip_version(void);
+
+/* Mirrors castforge_free_string (castforge.h:23-26, ffi.rs:25-31). NULL is ignored. */
+void castforge_hip_free_string(char *ptr);
+
+/* Device name, CU count, HBM size and arch of the current device as a JSON heap string. */
+int32_t castforge_hip_device_info(char **out_json, char **out_error);
+
+/* ---- quantize / dequantize --------------------------------------------------------------- */
+
+/* Symmetric absmax quantization of f32 [rows, cols] to i8 codes.
+ * Replaces quantize_symmetric_f32 (passes/quantize/formats.rs:664-698) as called by
+ * QuantizeWeightsPass::run (passes/quantize/schemes.rs:324-452): amax = NaN-ignoring max |v|,
+ * scale = amax < 1e-12 ? 1 : amax / qmax, q = clamp(round(v / scale), qmin, qmax), NaN -> 0;
+ * bits == 4 -> [-8, 7], anything else -> [-128, 127] (formats.rs:654-660).
+ * CFH_GRAN_TENSOR writes scales[0] (the reference); CFH_GRAN_CHANNEL writes scales[rows]. */
+int32_t castforge_hip_quantize_int8(const float *src, int64_t rows, int64_t cols, int32_t bits,
+                                    int32_t granularity, int32_t round_mode, int8_t *codes,
+                                    float *scales, void *stream, char **out_error);
+
+/* (q - 0) * scale to f32.  Replaces TensorStore::resolve_f32_attr for QuantizedI8
+ * (ir/tensor_store.rs:323-331) and the evaluator's dequant (codegen/eval.rs:305-319). */
+int32_t castforge_hip_dequantize_int8(const int8_t *codes, const float *scales, int64_t rows,
+                                      int64_t cols, int32_t granularity, float *out, void *stream,
+                                      char **out_error);
+
+/* INT4 asymmetric group-wise along K, fp16 scale and u4 zero point, 8 codes per u32.
+ * New scheme behind quantize(bits=4,group=..) (registry/families.rs:133-137); the reference's
+ * group-wise pass (passes/quantize/schemes.rs:532-549) is symmetric and keeps no codes.
+ * group: power of two in [8, 256]; cols % 8 == 0; src 16-byte aligned.
+ * Per group: h = f16_rne((max - min) / 15) (range < 1e-12 -> 1.0; 0 -> 0x0001; Inf -> 0x7BFF),
+ * s = f32(h), z = clamp(rne(-min / s), 0, 15), q = clamp(rne(v / s) + z, 0, 15), NaN -> z. */
+int32_t castforge_hip_quantize_int4g(const float *src, int64_t rows, int64_t cols, int64_t group,
+                                     uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros,
+                                     void *stream, char **out_error);
+
+int32_t castforge_hip_dequantize_int4g(const uint32_t *codes, const uint16_t *scales_f16,
+                                       const uint32_t *zeros, int64_t rows, int64_t cols,
+                                       int64_t group, float *out, void *stream, char **out_error);
+
+/* NF4 block-wise along K (QLoRA normal-float table), f32 absmax per block, 8 codes per u32.
+ * New scheme (claimed by the reference README.md:68, absent from its code).
+ * block: power of two in [8, 512]; cols % 8 == 0.  stored = absmax < 1e-12 ? 1 : absmax;
+ * code = #{i : v / stored > (T[i] + T[i+1]) / 2}, NaN -> 7. */
+int32_t castforge_hip_quantize_nf4(const float *src, int64_t rows, int64_t cols, int64_t block,
+                                   uint32_t *codes, float *absmax, void *stream, char **out_error);
+
+int32_t castforge_hip_dequantize_nf4(const uint32_t *codes, const float *absmax, int64_t rows,
+                                     int64_t cols, int64_t block, float *out, void *stream,
+                                     char **out_error);
+
+/* FP8 E4M3FN per row (weights: per output channel; activations: per token, dynamic):
+ * scale = absmax < 1e-12 ? 1 : absmax / 448, code = f32_to_fp8_e4m3fn(v / scale) bit-exact
+ * with the reference codec (passes/serving/mutable_loads.rs:367-411).  src_dtype F32 or BF16. */
+int32_t castforge_hip_quantize_fp8(const void *src, int32_t src_dtype, int64_t rows, int64_t cols,
+                                   uint8_t *codes, float *scales, void *stream, char **out_error);
+
+/* fp8_e4m3fn_to_f32 (mutable_loads.rs:415-432) times the row scale. */
+int32_t castforge_hip_dequantize_fp8(const uint8_t *codes, const float *scales, int64_t rows,
+                                     int64_t cols, float *out, void *stream, char **out_error);
+
+/* ---- dequant-fused matmul ----------------------------------------------------------------- */
+/* y[m, n] = sum_k x[m, k] * dequant(W)[n, k]; x bf16 [M, K]; y f32 or bf16 [M, N].
+ * Replaces the evaluation of `castforge.fused_qmatmul` (passes/fuse/epilogue.rs:10-94,
+ * codegen/eval.rs:1145-1179 -> eval_matmul_2d eval.rs:1465-1507, packed_rhs) and the HIP text
+ * the reference emits for it (codegen/targets/gpu_c.rs:208-292, passes/loops/lower.rs:226-247).
+ * M <= 16 runs the MFMA decode kernel; larger M runs the prefill GEMM. */
+int32_t castforge_hip_gemv_w4a16(const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
+                                 const uint32_t *codes, const uint16_t *scales_f16,
+                                 const uint32_t *zeros, void *y, int32_t y_dtype, void *stream,
+                                 char **out_error);
+
+int32_t castforge_hip_gemv_w8a16(const uint16_t *x, int64_t m, int64_t n, int64_t k,
+                                 const int8_t *codes, const float *scales, int32_t granularity,
+                                 void *y, int32_t y_dtype, void *stream, char **out_error);
+
+int32_t castforge_hip_gemv_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t block,
+                               const uint32_t *codes, const float *absmax, void *y, int32_t y_dtype,
+                               void *stream, char **out_error);
+
+/* Several W4A16 problems with the same M (1..16) in ONE launch, e.g. the 7 projections of a
+ * decoder block; each needs k % 128 == 0, group % 128 == 0 and 16-byte aligned x / codes. */
+typedef struct cfh_w4a16_problem_t {
+    const uint16_t *x;          /* bf16 [M, k] */
+    const uint32_t *codes;      /* u32 [n, k/8] */
+    const uint16_t *scales_f16; /* f16 [n, G] */
+    const uint32_t *zeros;      /* u32 [n, ceil(G/8)] */
+    void *y;                    /* [M, n] */
+    int64_t n, k, group;
+} cfh_w4a16_problem_t;
+
+int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, int32_t count,
+                                         int64_t m, int32_t y_dtype, void *stream,
+                                         char **out_error);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CASTFORGE_HIP_H */

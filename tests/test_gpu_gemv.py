@@ -1,0 +1,107 @@
+"""GPU parity of the dequant-fused GEMV / skinny GEMM kernels against the oracle's evaluator
+semantics (dequantize to f32, then eval_matmul_2d): |y - ref| <= 1e-3 + 1e-2 * |ref|, the
+north-star tolerance for bf16 accumulation."""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from castforge_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 1e-3
+
+
+def _close(y, ref):
+    y = y.float().cpu().numpy()
+    err = np.abs(y - ref)
+    bound = ATOL + RTOL * np.abs(ref)
+    bad = err > bound
+    assert not bad.any(), f"{bad.sum()} / {bad.size} outside tol; max err {err.max():.3e}"
+
+
+def _x(seed, m, k, dev):
+    xb = synth.activations_bf16(seed, 7, m, k)
+    return xb, torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+@pytest.mark.parametrize("m", [1, 2, 8, 16])
+@pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (64, 11008), (4096, 4096)])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_w4a16_skinny(cuda, m, n, k, out):
+    w = synth.weight(51, 1, n, k)
+    codes, scales, zeros = O.quantize_int4g(w, 128)
+    xb, x = _x(52, m, k, cuda)
+    p = ops.Int4Packed(torch.from_numpy(codes.view(np.int32)).to(cuda),
+                       torch.from_numpy(scales.view(np.float16)).to(cuda),
+                       torch.from_numpy(zeros.view(np.int32)).to(cuda), n, k, 128)
+    y = ops.gemm_w4a16(x, p, out)
+    torch.cuda.synchronize()
+    _close(y, O.gemm_w4a16(xb, codes, scales, zeros, n, k, 128))
+
+
+@pytest.mark.parametrize("m,group,k", [(3, 64, 512), (20, 128, 256), (1, 32, 1000), (5, 256, 512)])
+def test_w4a16_generic_paths(cuda, m, group, k):
+    n = 37
+    w = synth.weight(53, 1, n, k)
+    xb, x = _x(54, m, k, cuda)
+    p = ops.quantize_int4g(torch.from_numpy(w).to(cuda), group)
+    y = ops.gemm_w4a16(x, p, torch.float32)
+    ref = O.gemm_w4a16(xb, p.codes.cpu().numpy().view(np.uint32), p.scales.cpu().numpy().view(np.uint16),
+                       p.zeros.cpu().numpy().view(np.uint32), n, k, group)
+    _close(y, ref)
+
+
+@pytest.mark.parametrize("m", [1, 5, 16])
+@pytest.mark.parametrize("gran", ["channel", "tensor"])
+@pytest.mark.parametrize("n,k", [(40, 192), (4096, 4096), (33, 11008)])
+def test_w8a16(cuda, m, gran, n, k):
+    w = synth.weight(61, 1, n, k)
+    xb, x = _x(62, m, k, cuda)
+    q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, gran, "half_even")
+    y = ops.gemm_w8a16(x, q, s, gran, torch.float32)
+    sc = s.cpu().numpy()
+    sc = sc if gran == "channel" else np.full(n, sc[0], np.float32)
+    _close(y, O.gemm_w8a16(xb, q.cpu().numpy(), sc))
+
+
+@pytest.mark.parametrize("m", [1, 16, 40])
+@pytest.mark.parametrize("block", [64, 32, 16])
+def test_nf4(cuda, m, block):
+    n, k = 96, 1024
+    w = synth.weight(71, 1, n, k)
+    xb, x = _x(72, m, k, cuda)
+    p = ops.quantize_nf4(torch.from_numpy(w).to(cuda), block)
+    y = ops.gemm_nf4(x, p, torch.float32)
+    ref = O.gemm_nf4(xb, p.codes.cpu().numpy().view(np.uint32), p.absmax.cpu().numpy(), n, k, block)
+    _close(y, ref)
+
+
+def test_w4a16_batched_block_m1(cuda):
+    """The bench's single launch: 7 projections of one LLaMA-7B block at M=1."""
+    xs, ps, ys, refs = [], [], [], []
+    for tid, (name, n, k) in enumerate(synth.LLAMA7B_BLOCK):
+        w = synth.weight(0, tid, n, k)
+        codes, scales, zeros = O.quantize_int4g(w, 128)
+        xb, x = _x(100 + tid, 1, k, cuda)
+        ps.append(ops.Int4Packed(torch.from_numpy(codes.view(np.int32)).to(cuda),
+                                 torch.from_numpy(scales.view(np.float16)).to(cuda),
+                                 torch.from_numpy(zeros.view(np.int32)).to(cuda), n, k, 128))
+        xs.append(x)
+        ys.append(torch.empty((1, n), dtype=torch.bfloat16, device=cuda))
+        refs.append(O.gemm_w4a16(xb, codes, scales, zeros, n, k, 128))
+    ops.gemv_w4a16_batched(xs, ps, ys)
+    torch.cuda.synchronize()
+    for y, ref in zip(ys, refs):
+        _close(y, ref)
+
+
+def test_empty_and_degenerate(cuda):
+    p = ops.quantize_int4g(torch.zeros((0, 256), device=cuda), 128)
+    x = torch.zeros((1, 256), dtype=torch.bfloat16, device=cuda)
+    assert ops.gemm_w4a16(x, p).shape == (1, 0)
+    w = torch.zeros((16, 256), device=cuda)
+    p = ops.quantize_int4g(w, 128)
+    y = ops.gemm_w4a16(torch.ones((1, 256), dtype=torch.bfloat16, device=cuda), p, torch.float32)
+    assert torch.all(y == 0)

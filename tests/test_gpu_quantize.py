@@ -1,0 +1,172 @@
+"""GPU parity of the quantize / dequantize kernels against the CPU oracle: bit-exact codes,
+scales and zero points on the same seeded inputs, edge cases, and the BASELINE block shapes."""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from castforge_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+SPECIALS = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-30, -1e-38, 3.0e38], np.float32)
+
+
+def _w(seed, n, k, std=0.02, specials=False):
+    w = synth.weight(seed, 1, n, k, std)
+    if specials and w.size >= 64:
+        flat = w.reshape(-1)
+        r = synth.rng(seed, 2)
+        idx = r.choice(flat.size, size=min(len(SPECIALS) * 2, flat.size // 4), replace=False)
+        flat[idx] = np.resize(SPECIALS, idx.size)
+    return w
+
+
+def _u32(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+# --------------------------------------------------------------------------- INT8 ----
+@pytest.mark.parametrize("n,k", [(64, 96), (7, 13), (33, 4096), (3, 70000), (1, 4), (5, 11008)])
+@pytest.mark.parametrize("mode", ["half_away", "half_even"])
+def test_int8_per_channel_bit_exact(cuda, n, k, mode):
+    w = _w(11, n, k, specials=(n * k >= 200))
+    q_ref, s_ref = O.quantize_int8_rows(w, 8, 0 if mode == "half_away" else 1)
+    q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, "channel", mode)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_int8_ties_exact(cuda):
+    # v/scale lands exactly on .5 (scale = 1 with amax 127)
+    w = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -2.5, -126.5, 126.5]], np.float32)
+    for mode, m in (("half_away", 0), ("half_even", 1)):
+        q_ref, _ = O.quantize_int8_rows(w, 8, m)
+        q, _ = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, "channel", mode)
+        assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("shape", [(2, 2), (1, 1), (4096, 4096), (1, 1001), (3, 5, 7)])
+def test_int8_per_tensor_bit_exact(cuda, shape):
+    w = synth.weight(12, 3, int(np.prod(shape[:-1])), shape[-1]).reshape(shape)
+    q_ref, s_ref = O.quantize_symmetric(w, 8, 0)
+    q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, "tensor", "half_away")
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert s.cpu().numpy()[0].view(np.uint32) == np.float32(s_ref).view(np.uint32)
+
+
+def test_int8_reference_known_answer(cuda):
+    w = torch.tensor([[0.5, -0.25], [0.75, 0.5]], device=cuda)
+    q, s = ops.quantize_int8(w, 8, "tensor", "half_away")
+    assert q.cpu().flatten().tolist() == [85, -42, 127, 85]
+    assert s.cpu().numpy().view(np.uint32)[0] == 0x3BC18306
+
+
+def test_int4_symmetric_bits4(cuda):
+    w = _w(13, 16, 256)
+    q_ref, s_ref = O.quantize_int8_rows(w, 4, 0)
+    q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), 4, "channel", "half_away")
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_int8_dequant_matches_oracle(cuda):
+    w = _w(14, 32, 100)
+    q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, "channel", "half_even")
+    d = ops.dequantize_int8(q, s, "channel").cpu().numpy()
+    ref = q.cpu().numpy().astype(np.float32) * s.cpu().numpy()[:, None]
+    assert np.array_equal(d, ref)
+
+
+# -------------------------------------------------------------------------- INT4g ----
+@pytest.mark.parametrize("group", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("n,k", [(16, 1024), (5, 200), (3, 11008), (1, 8)])
+def test_int4g_bit_exact(cuda, group, n, k):
+    w = _w(21, n, k, specials=(n * k >= 1024))
+    c_ref, s_ref, z_ref = O.quantize_int4g(w, group)
+    p = ops.quantize_int4g(torch.from_numpy(w).to(cuda), group)
+    assert np.array_equal(_u32(p.codes), c_ref)
+    assert np.array_equal(p.scales.cpu().numpy().view(np.uint16), s_ref)
+    assert np.array_equal(_u32(p.zeros), z_ref)
+    d = ops.dequantize_int4g(p).cpu().numpy()
+    d_ref = O.dequantize_int4g(c_ref, s_ref, z_ref, n, k, group)
+    assert np.array_equal(d.view(np.uint32), d_ref.view(np.uint32))
+
+
+def test_int4g_edge_groups(cuda):
+    w = np.zeros((4, 256), np.float32)
+    w[1, :] = 0.25
+    w[2, :5] = np.nan
+    w[2, 5:] = np.linspace(-1, 1, 251, dtype=np.float32)
+    w[3, :128] = 1e-9  # tiny range -> guarded scales
+    w[3, 128:] = np.linspace(-70000, 70000, 128, dtype=np.float32)  # fp16 scale saturates
+    c_ref, s_ref, z_ref = O.quantize_int4g(w, 128)
+    p = ops.quantize_int4g(torch.from_numpy(w).to(cuda), 128)
+    assert np.array_equal(_u32(p.codes), c_ref)
+    assert np.array_equal(p.scales.cpu().numpy().view(np.uint16), s_ref)
+    assert np.array_equal(_u32(p.zeros), z_ref)
+
+
+# ---------------------------------------------------------------------------- NF4 ----
+@pytest.mark.parametrize("block", [8, 32, 64, 128, 512])
+@pytest.mark.parametrize("n,k", [(16, 1024), (7, 200), (2, 11008)])
+def test_nf4_bit_exact(cuda, block, n, k):
+    w = _w(31, n, k, specials=(n * k >= 1024))
+    c_ref, a_ref = O.quantize_nf4(w, block)
+    p = ops.quantize_nf4(torch.from_numpy(w).to(cuda), block)
+    assert np.array_equal(_u32(p.codes), c_ref)
+    assert np.array_equal(p.absmax.cpu().numpy().view(np.uint32), a_ref.view(np.uint32))
+    d = ops.dequantize_nf4(p).cpu().numpy()
+    assert np.array_equal(d.view(np.uint32), O.dequantize_nf4(c_ref, a_ref, n, k, block).view(np.uint32))
+
+
+# ---------------------------------------------------------------------------- FP8 ----
+QUIRK = np.array([0x3CFFFFFE, 0x3CFFFFFF, 0x3D7FFFFE, 0x3D7FFFFF, 0x3DFFFFFF, 0x3E7FFFFF,
+                  0x40FFFFFF, 0x417FFFFF, 0x41FFFFFE, 0x41FFFFFF, 0x427FFFFE, 0x427FFFFF,
+                  0x42FFFFFE, 0x42FFFFFF, 0x437FFFFE, 0x437FFFFF], np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("r,c", [(16, 300), (5, 4096), (3, 7), (2, 70000)])
+def test_fp8_rows_f32_bit_exact(cuda, r, c):
+    v = synth.fp8_inputs(41, 1, r, c)
+    c_ref, s_ref = O.quantize_fp8_rows(v)
+    codes, scales = ops.quantize_fp8(torch.from_numpy(v).to(cuda))
+    assert np.array_equal(codes.cpu().numpy(), c_ref)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_fp8_reference_quirk_inputs(cuda):
+    # rows with amax 448 have scale exactly 1, so v/scale = v hits the 16 quirk magnitudes
+    row = np.concatenate([[448.0], QUIRK, -QUIRK, [np.nan, 0.0, -0.0, 1e-3, 2.0 ** -10]]).astype(np.float32)
+    v = np.stack([row, row[::-1].copy()])
+    c_ref, s_ref = O.quantize_fp8_rows(v)
+    codes, scales = ops.quantize_fp8(torch.from_numpy(v).to(cuda))
+    assert np.array_equal(codes.cpu().numpy(), c_ref)
+    assert s_ref[0] == 1.0
+
+
+@pytest.mark.parametrize("r,c", [(16, 512), (4096, 4096 // 8), (3, 11)])
+def test_fp8_rows_bf16_bit_exact(cuda, r, c):
+    x = synth.activations_bf16(42, 1, r, c)
+    c_ref, s_ref = O.quantize_fp8_rows(x)
+    codes, scales = ops.quantize_fp8(torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(cuda))
+    assert np.array_equal(codes.cpu().numpy(), c_ref)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    d = ops.dequantize_fp8(codes, scales).cpu().numpy()
+    dec = torch.from_numpy(c_ref).view(torch.float8_e4m3fn).float().numpy() * s_ref[:, None]
+    assert np.array_equal(d, dec)
+
+
+# ------------------------------------------------------------- BASELINE block shapes ----
+@pytest.mark.parametrize("name,n,k", synth.LLAMA7B_BLOCK)
+def test_block_int8_channel_and_int4g128_full_size(cuda, name, n, k):
+    tid = [b[0] for b in synth.LLAMA7B_BLOCK].index(name)
+    w = synth.weight(0, tid, n, k)
+    wd = torch.from_numpy(w).to(cuda)
+    q_ref, s_ref = O.quantize_int8_rows(w, 8, 1)
+    q, s = ops.quantize_int8(wd, 8, "channel", "half_even")
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+    c_ref, sc_ref, z_ref = O.quantize_int4g(w, 128)
+    p = ops.quantize_int4g(wd, 128)
+    assert np.array_equal(_u32(p.codes), c_ref)
+    assert np.array_equal(p.scales.cpu().numpy().view(np.uint16), sc_ref)
+    assert np.array_equal(_u32(p.zeros), z_ref)
