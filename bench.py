@@ -177,6 +177,28 @@ def main():
         nf_bytes = sum(p.nbytes() + 2 * p.k + 2 * p.n for p in nf)
         components["nf4_gemv_m1_GBps"] = round(nf_bytes / (st * 1e-3) / 1e9, 1)
         log(f"[bench] W8A16 M=1 {components['w8a16_gemv_m1_GBps']} GB/s, NF4 M=1 {components['nf4_gemv_m1_GBps']} GB/s")
+        del nf, nfc
+
+        # FP8 E4M3 W8A8 GEMM at M=4096 (config 4): N(0,1) inputs with 0.5% outliers x30
+        for (m, n, k) in ((4096, 11008, 4096), (4096, 4096, 11008)):
+            a = torch.randn((m, k), generator=gen, device=dev)
+            a[torch.rand((m, k), generator=gen, device=dev) < 0.005] *= 30
+            w = torch.randn((n, k), generator=gen, device=dev)
+            w[torch.rand((n, k), generator=gen, device=dev) < 0.005] *= 30
+            a16 = a.to(torch.bfloat16)
+            del a
+            qw, sw = ops.quantize_fp8(w)
+            qa, sa = ops.quantize_fp8(a16)
+            y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            _, la = time_steps(lambda i: ops.gemm_fp8(qa, sa, qw, sw, y), 30, 3)
+            tag = f"m{m}_n{n}_k{k}"
+            components[f"fp8_gemm_{tag}_TFLOPs"] = round(2.0 * m * n * k / (la * 1e-3) / 1e12, 1)
+            components[f"fp8_gemm_{tag}_pct_fp8_peak"] = round(100 * 2.0 * m * n * k / (la * 1e-3) / 5.0e15, 1)
+            _, lq = time_steps(lambda i: ops.quantize_fp8(a16), 20, 3)
+            components[f"fp8_act_quant_{tag}_GBps"] = round((m * k * 3 + m * 4) / (lq * 1e-3) / 1e9, 1)
+            log(f"[bench] FP8 GEMM {tag}: {la * 1e3:.1f} us, {components[f'fp8_gemm_{tag}_TFLOPs']} TFLOP/s; "
+                f"act quant {components[f'fp8_act_quant_{tag}_GBps']} GB/s")
+            del w, a16, qw, sw, qa, sa, y
 
     components["w4a16_gemv_m1_GBps"] = round(value, 1)
     components["w4a16_gemv_m1_pct_hbm_peak"] = round(100.0 * value / HBM_PEAK_GBPS, 1)

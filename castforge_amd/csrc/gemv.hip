@@ -6,15 +6,20 @@
 // row-major (packed_rhs layout, fold.rs:549-554).
 //
 // Decode is HBM-bound on the packed weight stream.  Design:
-//   * a workgroup (4 waves) owns 16 weight rows; the 4 waves split K;
-//   * each lane streams 16 B of one row per load (lane%16 = row, lane/16 = 16-byte part), so a
-//     wave-wide load covers 64 B of each of 16 rows: one 128-element INT4 group per row;
-//   * codes become exact f16 values (q - z) with the magic-exponent trick (or an LDS table
-//     for NF4) and feed v_mfma_f32_16x16x32_f16 as the B operand; the activation rows are
-//     the A operand, converted once per workgroup from bf16 to f16 in LDS, in the permuted
-//     order the nibble extraction produces, so M = 1..16 costs the same MFMA count;
-//   * INT4 group scales (one per row per 128-k chunk) multiply the fp32 chunk result;
-//     NF4 block scales (64 k) are folded into the f16 operand; INT8 scales are per row.
+//   * a workgroup (4 waves) owns 16*R weight rows; the 4 waves interleave over K "chunks";
+//   * a chunk is what one wave-wide load brings for 16 rows: lane%16 = row, lane/16 = part,
+//     each lane loads LW bytes (16, 8 or 4), so one chunk spans exactly one quantization
+//     group / NF4 block per row and its scale multiplies the fp32 MFMA result (no rounding of
+//     the scale into the f16 operand);
+//   * codes become exact f16 operands: INT4 (q - z) and INT8 q by the magic-exponent trick,
+//     NF4 table values as an exact f16 hi + lo pair (two MFMAs) from an LDS table;
+//   * v_mfma_f32_16x16x32_f16 with dequantized W rows as B and the activation rows as A; x is
+//     converted once per workgroup from bf16 to f16 in LDS, in the permuted order the nibble
+//     extraction produces, so M = 1..16 costs the same MFMA count;
+//   * 8 chunks (8 KB per wave) are in flight before the x staging starts; problems with the
+//     longest K are dispatched first so no long workgroup forms a tail.
+#include <algorithm>
+
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
 
@@ -52,14 +57,11 @@ struct Batch {
     int32_t y_bf16;
 };
 
-// Chunk = the K span one wave-wide 16-byte-per-lane load covers for each of the 16 rows.
-template <int FMT> struct FmtTraits;
-template <> struct FmtTraits<FMT_INT4> { static constexpr int kChunk = 128; };
-template <> struct FmtTraits<FMT_NF4> { static constexpr int kChunk = 128; };
-template <> struct FmtTraits<FMT_INT8> { static constexpr int kChunk = 64; };
+template <int FMT> constexpr int codes_per_byte() { return FMT == FMT_INT8 ? 1 : 2; }
 
 // Position, within each 8-element k-run, of the element the extraction places in f16 slot i.
-// INT4: (n0,n4),(n1,n5),(n2,n6),(n3,n7); INT8 (two words): (b0,b2),(b1,b3) of each word.
+// INT4: (n0,n4),(n1,n5),(n2,n6),(n3,n7); INT8 (two words): (b0,b2),(b1,b3) of each word;
+// NF4: the table gives natural-order pairs.
 __device__ __forceinline__ int perm_src(int fmt, int i) {
     if (fmt == FMT_INT4) return (i >> 1) + ((i & 1) << 2);
     if (fmt == FMT_INT8) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
@@ -70,18 +72,16 @@ __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast
 __device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
 // INT4 word -> 4 f16 pairs of exact (q - z).  zc1024 = -(1024+z) splat, zc64 = -(64+z) splat.
+// (w & 0x000F000F) | 0x6400_6400 is the f16 pair (1024 + n0, 1024 + n4); the 0x00F0 nibbles
+// give 1024 + 16 n, scaled back by 1/16.  Every intermediate is an exact f16.
 __device__ __forceinline__ void int4_word_to_h(uint32_t w, half2_t zc1024, half2_t zc64,
                                                uint32_t out[4]) {
     const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
     const uint32_t w8 = w >> 8;
-    half2_t lo0 = as_h2((w & 0x000F000Fu) | 0x64006400u) + zc1024;
-    half2_t hi0 = as_h2((w & 0x00F000F0u) | 0x64006400u) * sixteenth + zc64;
-    half2_t lo1 = as_h2((w8 & 0x000F000Fu) | 0x64006400u) + zc1024;
-    half2_t hi1 = as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth + zc64;
-    out[0] = as_u(lo0);
-    out[1] = as_u(hi0);
-    out[2] = as_u(lo1);
-    out[3] = as_u(hi1);
+    out[0] = as_u(as_h2((w & 0x000F000Fu) | 0x64006400u) + zc1024);
+    out[1] = as_u(as_h2((w & 0x00F000F0u) | 0x64006400u) * sixteenth + zc64);
+    out[2] = as_u(as_h2((w8 & 0x000F000Fu) | 0x64006400u) + zc1024);
+    out[3] = as_u(as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth + zc64);
 }
 
 // INT8 word (4 signed codes) -> 2 f16 pairs of exact q.
@@ -93,8 +93,7 @@ __device__ __forceinline__ void int8_word_to_h(uint32_t w, uint32_t out[2]) {
 }
 
 __device__ __forceinline__ half8_t pack8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    uint4 v = make_uint4(a, b, c, d);
-    return __builtin_bit_cast(half8_t, v);
+    return __builtin_bit_cast(half8_t, make_uint4(a, b, c, d));
 }
 
 __constant__ float kNf4[16] = {
@@ -103,14 +102,28 @@ __constant__ float kNf4[16] = {
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
-template <int FMT>
-__global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
-    using Tr = FmtTraits<FMT>;
-    extern __shared__ __align__(16) _Float16 xs[];  // [M][KC], permuted per 8-run
-    __shared__ floatx4 red[kWaves - 1][64];
-    __shared__ uint32_t nf4_lut[FMT == FMT_NF4 ? 256 : 1];
+template <int LW>
+__device__ __forceinline__ void load_words(const uint8_t *p, uint32_t *w) {
+    if constexpr (LW == 16) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(p);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (LW == 8) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        w[0] = v.x; w[1] = v.y;
+    } else {
+        w[0] = *reinterpret_cast<const uint32_t *>(p);
+    }
+}
 
-    // locate the problem of this workgroup
+template <int FMT, int LW, int R>
+__global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
+    constexpr int WPL = LW / 4;                         // 32-bit code words per lane per chunk
+    constexpr int CK = 4 * LW * codes_per_byte<FMT>();  // K elements per chunk
+    constexpr int NB = R == 1 ? 8 : 2;                  // chunks in flight per wave
+    extern __shared__ __align__(16) _Float16 xs[];      // [M][KC], permuted per 8-run
+    __shared__ floatx4 red[kWaves - 1][R][64];
+    __shared__ uint2 lut[FMT == FMT_NF4 ? 256 : 1];
+
     int pi = 0;
 #pragma unroll
     for (int i = 1; i < kMaxProblems; ++i)
@@ -118,36 +131,84 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const Problem &P = b.p[pi];
     const int M = b.m;
     const int64_t N = P.n, K = P.k;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x - P.tile_begin) * 16;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x - P.tile_begin) * 16 * R;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, part = lane >> 4;
-    const int64_t nrow = n0 + lr;
-    const bool row_ok = nrow < N;
+    int64_t nrow[R];
+    bool rok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        nrow[r] = n0 + 16 * r + lr;
+        rok[r] = nrow[r] < N;
+    }
+    const int64_t row_bytes = K / codes_per_byte<FMT>();
+    const uint8_t *codes = static_cast<const uint8_t *>(P.codes);
+    const int64_t G = FMT == FMT_INT4 ? (K + P.group - 1) / P.group : 0;
+    const int64_t ZW = (G + 7) / 8;
+    const int64_t NBLK = FMT == FMT_NF4 ? (K + P.group - 1) / P.group : 0;
+
+    uint32_t wq[NB][R][WPL];
+    float sc[NB][R];
+    uint32_t zq[NB][R];
+
+    // loads chunks c0, c0 + 4, ... (< cend) of this wave
+    auto load_batch = [&](int c0, int cend) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int c = c0 + j * kWaves;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                sc[j][r] = 0.f;
+                zq[j][r] = 0;
+#pragma unroll
+                for (int t = 0; t < WPL; ++t) wq[j][r][t] = 0;
+                if (c < cend && rok[r]) {
+                    const int64_t kk = static_cast<int64_t>(c) * CK;
+                    load_words<LW>(codes + nrow[r] * row_bytes + kk / codes_per_byte<FMT>() + part * LW, wq[j][r]);
+                    if constexpr (FMT == FMT_INT4) {
+                        const int64_t g = kk / P.group;
+                        sc[j][r] = f16_to_f32(static_cast<const uint16_t *>(P.scales)[nrow[r] * G + g]);
+                        zq[j][r] = (P.zeros[nrow[r] * ZW + (g >> 3)] >> (4 * (g & 7))) & 15u;
+                    } else if constexpr (FMT == FMT_NF4) {
+                        sc[j][r] = static_cast<const float *>(P.scales)[nrow[r] * NBLK + kk / P.group];
+                    }
+                }
+            }
+        }
+    };
+
+    const int KC = P.kc;
+    const int nchunks = static_cast<int>(K / CK);
+    const int cps = KC / CK;  // chunks per LDS stage
+    // first batch goes out before the activation staging
+    load_batch(wave, cps < nchunks ? cps : nchunks);
+    bool have = true;
 
     if constexpr (FMT == FMT_NF4) {
         for (int i = tid; i < 256; i += kThreads) {
-            half2_t v = {static_cast<_Float16>(kNf4[i & 15]), static_cast<_Float16>(kNf4[i >> 4])};
-            nf4_lut[i] = as_u(v);
+            const _Float16 h0 = static_cast<_Float16>(kNf4[i & 15]), h1 = static_cast<_Float16>(kNf4[i >> 4]);
+            const _Float16 l0 = static_cast<_Float16>(kNf4[i & 15] - static_cast<float>(h0));
+            const _Float16 l1 = static_cast<_Float16>(kNf4[i >> 4] - static_cast<float>(h1));
+            half2_t hi = {h0, h1}, lo = {l0, l1};
+            lut[i] = make_uint2(as_u(hi), as_u(lo));
         }
     }
 
-    const int64_t row_bytes = (FMT == FMT_INT8) ? K : K / 2;
-    const uint8_t *wrow = static_cast<const uint8_t *>(P.codes) + (row_ok ? nrow : 0) * row_bytes;
-    const int64_t G = (FMT == FMT_INT4) ? (K + P.group - 1) / P.group : 0;
-    const int64_t ZW = (G + 7) / 8;
+    floatx4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    const int KC = P.kc;
-
-    for (int64_t k0 = 0; k0 < K; k0 += KC) {
-        const int kc = static_cast<int>((K - k0) < KC ? (K - k0) : KC);
+    for (int cs = 0; cs < nchunks; cs += cps) {
+        const int ce = cs + cps < nchunks ? cs + cps : nchunks;
+        const int64_t k0 = static_cast<int64_t>(cs) * CK;
+        const int kc = (ce - cs) * CK;
         // ---- stage x[:, k0:k0+kc] as permuted f16 ----
         __syncthreads();
         const int runs = kc >> 3;
         for (int it = tid; it < M * runs; it += kThreads) {
-            const int m = it / runs, r = it - m * runs;
-            const uint4 raw = *reinterpret_cast<const uint4 *>(P.x + static_cast<int64_t>(m) * K + k0 + r * 8);
+            const int m = it / runs, rr = it - m * runs;
+            const uint4 raw = *reinterpret_cast<const uint4 *>(P.x + static_cast<int64_t>(m) * K + k0 + rr * 8);
             const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
             uint32_t o[4];
 #pragma unroll
@@ -158,82 +219,76 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
                 half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
                 o[i] = as_u(h);
             }
-            *reinterpret_cast<uint4 *>(xs + m * KC + r * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4 *>(xs + m * KC + rr * 8) = make_uint4(o[0], o[1], o[2], o[3]);
         }
         __syncthreads();
 
-        // ---- stream this stage's chunks; wave w takes chunks w, w+4, ... ----
-        const int nchunks = kc / Tr::kChunk;
-        constexpr int NB = 4;  // chunks in flight per wave
-        for (int cb = wave; cb < nchunks; cb += kWaves * NB) {
-            uint4 wq[NB];
-            float sc[NB];
-            uint32_t zw[NB];
+        for (int cb = cs + wave; cb < ce; cb += kWaves * NB) {
+            if (!have) load_batch(cb, ce);
+            have = false;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 const int c = cb + j * kWaves;
-                wq[j] = make_uint4(0, 0, 0, 0);
-                sc[j] = 0.f;
-                zw[j] = 0;
-                if (c < nchunks && row_ok) {
-                    const int64_t kk = k0 + static_cast<int64_t>(c) * Tr::kChunk;
-                    const int64_t boff = (FMT == FMT_INT8 ? kk : kk / 2) + part * 16;
-                    wq[j] = *reinterpret_cast<const uint4 *>(wrow + boff);
-                    if constexpr (FMT == FMT_INT4) {
-                        const int64_t g = kk / P.group;
-                        sc[j] = f16_to_f32(static_cast<const uint16_t *>(P.scales)[nrow * G + g]);
-                        zw[j] = (P.zeros[nrow * ZW + (g >> 3)] >> (4 * (g & 7))) & 15u;
-                    } else if constexpr (FMT == FMT_NF4) {
-                        const int64_t nb = (K + P.group - 1) / P.group;
-                        sc[j] = static_cast<const float *>(P.scales)[nrow * nb + (kk + part * 32) / P.group];
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int c = cb + j * kWaves;
-                if (c >= nchunks) break;
-                const uint32_t ww[4] = {wq[j].x, wq[j].y, wq[j].z, wq[j].w};
-                const int xoff = c * Tr::kChunk + part * (Tr::kChunk / 4);
-                floatx4 part_acc = {0.f, 0.f, 0.f, 0.f};
+                if (c >= ce) break;
+                const int xoff = (c - cs) * CK + part * (CK / 4);
+                const _Float16 *xa = xs + lr * KC + xoff;
                 if constexpr (FMT == FMT_INT4) {
-                    const _Float16 z1024 = static_cast<_Float16>(-1024.0f - static_cast<float>(zw[j]));
-                    const _Float16 z64 = static_cast<_Float16>(-64.0f - static_cast<float>(zw[j]));
-                    const half2_t zc1024 = {z1024, z1024}, zc64 = {z64, z64};
+                    floatx4 pacc[R];
+                    half2_t zc1024[R], zc64[R];
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        uint32_t hb[4];
-                        int4_word_to_h(ww[t], zc1024, zc64, hb);
-                        half8_t bop = pack8(hb[0], hb[1], hb[2], hb[3]);
-                        half8_t aop = {};
-                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xs + lr * KC + xoff + t * 8);
-                        part_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, part_acc, 0, 0, 0);
+                    for (int r = 0; r < R; ++r) {
+                        pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+                        const _Float16 a = static_cast<_Float16>(-1024.0f - static_cast<float>(zq[j][r]));
+                        const _Float16 s = static_cast<_Float16>(-64.0f - static_cast<float>(zq[j][r]));
+                        zc1024[r] = half2_t{a, a};
+                        zc64[r] = half2_t{s, s};
                     }
-                    acc += part_acc * sc[j];
-                } else if constexpr (FMT == FMT_INT8) {
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        uint32_t h0[2], h1[2];
-                        int8_word_to_h(ww[2 * t], h0);
-                        int8_word_to_h(ww[2 * t + 1], h1);
-                        half8_t bop = pack8(h0[0], h0[1], h1[0], h1[1]);
+                    for (int t = 0; t < WPL; ++t) {
                         half8_t aop = {};
-                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xs + lr * KC + xoff + t * 8);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc, 0, 0, 0);
+                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            uint32_t hb[4];
+                            int4_word_to_h(wq[j][r][t], zc1024[r], zc64[r], hb);
+                            pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(hb[0], hb[1], hb[2], hb[3]),
+                                                                            pacc[r], 0, 0, 0);
+                        }
                     }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r] += pacc[r] * sc[j][r];
+                } else if constexpr (FMT == FMT_NF4) {
+                    floatx4 pacc[R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 0; t < WPL; ++t) {
+                        half8_t aop = {};
+                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const uint32_t w = wq[j][r][t];
+                            const uint2 e0 = lut[w & 255u], e1 = lut[(w >> 8) & 255u];
+                            const uint2 e2 = lut[(w >> 16) & 255u], e3 = lut[w >> 24];
+                            pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.x, e1.x, e2.x, e3.x), pacc[r], 0, 0, 0);
+                            pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.y, e1.y, e2.y, e3.y), pacc[r], 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < R; ++r) acc[r] += pacc[r] * sc[j][r];
                 } else {
-                    const _Float16 s16 = static_cast<_Float16>(sc[j]);
-                    const half2_t s2 = {s16, s16};
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const uint32_t w = ww[t];
-                        uint32_t hb[4];
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) hb[q] = as_u(as_h2(nf4_lut[(w >> (8 * q)) & 255u]) * s2);
-                        half8_t bop = pack8(hb[0], hb[1], hb[2], hb[3]);
+                    for (int t = 0; t < WPL / 2; ++t) {
                         half8_t aop = {};
-                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xs + lr * KC + xoff + t * 8);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, bop, acc, 0, 0, 0);
+                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            uint32_t h0[2], h1[2];
+                            int8_word_to_h(wq[j][r][2 * t], h0);
+                            int8_word_to_h(wq[j][r][2 * t + 1], h1);
+                            acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]),
+                                                                           acc[r], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -241,26 +296,29 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     }
 
     // ---- reduce the 4 waves' partial tiles and store ----
-    if (wave > 0) red[wave - 1][lane] = acc;
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) red[wave - 1][r][lane] = acc[r];
+    }
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
-        for (int w = 0; w < kWaves - 1; ++w) acc += red[w][lane];
-        if constexpr (FMT == FMT_INT8) {
-            if (row_ok) {
-                const float *s = static_cast<const float *>(P.scales);
-                acc *= P.scale_per_row ? s[nrow] : s[0];
-            }
-        }
-        if (row_ok) {
+        for (int r = 0; r < R; ++r) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = part * 4 + r;
+            for (int w = 0; w < kWaves - 1; ++w) acc[r] += red[w][r][lane];
+            if (!rok[r]) continue;
+            if constexpr (FMT == FMT_INT8) {
+                const float *s = static_cast<const float *>(P.scales);
+                acc[r] *= P.scale_per_row ? s[nrow[r]] : s[0];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = part * 4 + q;
                 if (m < M) {
                     if (b.y_bf16)
-                        static_cast<uint16_t *>(P.y)[static_cast<int64_t>(m) * N + nrow] = f32_to_bf16_rne(acc[r]);
+                        static_cast<uint16_t *>(P.y)[static_cast<int64_t>(m) * N + nrow[r]] = f32_to_bf16_rne(acc[r][q]);
                     else
-                        static_cast<float *>(P.y)[static_cast<int64_t>(m) * N + nrow] = acc[r];
+                        static_cast<float *>(P.y)[static_cast<int64_t>(m) * N + nrow[r]] = acc[r][q];
                 }
             }
         }
@@ -276,7 +334,7 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
     const int64_t K = P.k, N = P.n;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     const int64_t G = (FMT == FMT_INT4) ? (K + P.group - 1) / P.group : 0, ZW = (G + 7) / 8;
-    const int64_t NB = (FMT == FMT_NF4) ? (K + P.group - 1) / P.group : 0;
+    const int64_t NBLK = (FMT == FMT_NF4) ? (K + P.group - 1) / P.group : 0;
     for (int64_t k = lane; k < K; k += 64) {
         float w;
         if constexpr (FMT == FMT_INT8) {
@@ -290,7 +348,7 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
                 w = static_cast<float>(static_cast<int32_t>(q) - z) *
                     f16_to_f32(static_cast<const uint16_t *>(P.scales)[n * G + g]);
             } else {
-                w = kNf4[q] * static_cast<const float *>(P.scales)[n * NB + k / P.group];
+                w = kNf4[q] * static_cast<const float *>(P.scales)[n * NBLK + k / P.group];
             }
         }
 #pragma unroll
@@ -316,36 +374,62 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
     }
 }
 
-template <int FMT>
-bool skinny_ok(const Problem &p, int64_t m) {
-    using Tr = FmtTraits<FMT>;
-    if (m < 1 || m > 16) return false;
-    if (p.k % Tr::kChunk != 0) return false;
-    if (!aligned(p.x, 16) || !aligned(p.codes, 16)) return false;
-    if (FMT == FMT_INT4 && (p.group % 128 != 0)) return false;
-    if (FMT == FMT_NF4 && (p.group % 32 != 0)) return false;
-    return true;
+// Bytes each lane loads per chunk for this format / group (0 = no MFMA path).
+int lw_for(int fmt, int64_t group) {
+    if (fmt == FMT_INT8) return 16;
+    if (group % 128 == 0) return 16;
+    if (group == 64) return 8;
+    if (group == 32) return 4;
+    return 0;
 }
 
-template <int FMT>
-int32_t kc_for(int64_t k, int64_t m) {
-    using Tr = FmtTraits<FMT>;
+int chunk_k(int fmt, int lw) { return 4 * lw * (fmt == FMT_INT8 ? 1 : 2); }
+
+bool skinny_ok(int fmt, const Problem &p, int64_t m) {
+    if (m < 1 || m > 16) return false;
+    const int lw = lw_for(fmt, p.group);
+    if (lw == 0) return false;
+    if (p.k % chunk_k(fmt, lw) != 0) return false;
+    return aligned(p.x, 16) && aligned(p.codes, 16);
+}
+
+int32_t kc_for(int64_t k, int64_t m, int ck) {
     int64_t kc = (kLdsBytesMax / 2) / m;
-    kc = (kc / Tr::kChunk) * Tr::kChunk;
-    if (kc < Tr::kChunk) kc = Tr::kChunk;
+    kc = (kc / ck) * ck;
+    if (kc < ck) kc = ck;
     return static_cast<int32_t>(kc < k ? kc : k);
 }
 
-// Launch a batch of problems that share M; all must pass skinny_ok.
-template <int FMT>
-void launch_skinny(Problem *ps, int count, int64_t m, int y_bf16, hipStream_t st) {
+template <int FMT, int LW, int R>
+void launch_one(const Batch &b, int64_t tiles, int64_t lds, hipStream_t st) {
+    skinny_qgemm_kernel<FMT, LW, R><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
+                                      static_cast<size_t>(lds), st>>>(b);
+}
+
+template <int FMT, int R>
+void launch_lw(int lw, const Batch &b, int64_t tiles, int64_t lds, hipStream_t st) {
+    if (lw == 16) launch_one<FMT, 16, R>(b, tiles, lds, st);
+    else if constexpr (FMT != FMT_INT8) {
+        if (lw == 8) launch_one<FMT, 8, R>(b, tiles, lds, st);
+        else launch_one<FMT, 4, R>(b, tiles, lds, st);
+    }
+}
+
+// Launch problems that share the format, M and chunk width; all must pass skinny_ok.
+void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipStream_t st) {
+    const int lw = lw_for(fmt, ps[0].group);
+    const int ck = chunk_k(fmt, lw);
+    const int R = m <= 4 ? 1 : 4;
+    // longest K first: its workgroups run longest, so they start first
+    std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
     Batch b{};
     int64_t tiles = 0, max_lds = 0;
     for (int i = 0; i < count; ++i) {
+        require(lw_for(fmt, ps[i].group) == lw, "batched problems must share the group size class");
         b.p[i] = ps[i];
         b.p[i].tile_begin = static_cast<int32_t>(tiles);
-        b.p[i].kc = kc_for<FMT>(ps[i].k, m);
-        tiles += (ps[i].n + 15) / 16;
+        b.p[i].kc = kc_for(ps[i].k, m, ck);
+        tiles += (ps[i].n + 16 * R - 1) / (16 * R);
         const int64_t lds = m * b.p[i].kc * 2;
         if (lds > max_lds) max_lds = lds;
     }
@@ -354,8 +438,16 @@ void launch_skinny(Problem *ps, int count, int64_t m, int y_bf16, hipStream_t st
     b.m = static_cast<int32_t>(m);
     b.y_bf16 = y_bf16;
     if (tiles == 0) return;
-    skinny_qgemm_kernel<FMT><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
-                               static_cast<size_t>(max_lds), st>>>(b);
+    if (fmt == FMT_INT4) {
+        if (R == 1) launch_lw<FMT_INT4, 1>(lw, b, tiles, max_lds, st);
+        else launch_lw<FMT_INT4, 4>(lw, b, tiles, max_lds, st);
+    } else if (fmt == FMT_NF4) {
+        if (R == 1) launch_lw<FMT_NF4, 1>(lw, b, tiles, max_lds, st);
+        else launch_lw<FMT_NF4, 4>(lw, b, tiles, max_lds, st);
+    } else {
+        if (R == 1) launch_lw<FMT_INT8, 1>(lw, b, tiles, max_lds, st);
+        else launch_lw<FMT_INT8, 4>(lw, b, tiles, max_lds, st);
+    }
     check_launch("skinny_qgemm");
 }
 
@@ -379,19 +471,14 @@ void common_checks(const void *x, int64_t m, int64_t n, int64_t k, const void *c
 
 }  // namespace
 
-// Exposed to the prefill GEMM translation unit: route M <= 16 through the skinny kernel.
-bool gemv_try_skinny(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
-                     const void *codes, const void *scales, const uint32_t *zeros, int per_row,
-                     void *y, int y_bf16, hipStream_t st);
-
+// Routes one problem to the skinny MFMA kernel (M <= 16) when its shape allows it.
 bool gemv_try_skinny(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
                      const void *codes, const void *scales, const uint32_t *zeros, int per_row,
                      void *y, int y_bf16, hipStream_t st) {
     Problem p{x, codes, scales, zeros, y, n, k, static_cast<int32_t>(group), per_row, 0, 0};
-    if (fmt == FMT_INT4 && skinny_ok<FMT_INT4>(p, m)) { launch_skinny<FMT_INT4>(&p, 1, m, y_bf16, st); return true; }
-    if (fmt == FMT_INT8 && skinny_ok<FMT_INT8>(p, m)) { launch_skinny<FMT_INT8>(&p, 1, m, y_bf16, st); return true; }
-    if (fmt == FMT_NF4 && skinny_ok<FMT_NF4>(p, m)) { launch_skinny<FMT_NF4>(&p, 1, m, y_bf16, st); return true; }
-    return false;
+    if (!skinny_ok(fmt, p, m)) return false;
+    launch_skinny(fmt, &p, 1, m, y_bf16, st);
+    return true;
 }
 
 void gemv_generic(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
@@ -473,12 +560,12 @@ int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, in
             require(q.k > 0 && q.scales_f16 && q.zeros, "problem buffers must not be NULL");
             Problem p{q.x, q.codes, q.scales_f16, q.zeros, q.y, q.n, q.k,
                       static_cast<int32_t>(q.group), 1, 0, 0};
-            require(skinny_ok<FMT_INT4>(p, m),
+            require(q.group % 128 == 0 && skinny_ok(FMT_INT4, p, m),
                     "batched GEMV needs k % 128 == 0, group % 128 == 0 and 16-byte aligned x/codes");
             ps[used++] = p;
         }
-        if (used) launch_skinny<FMT_INT4>(ps, used, m, y_dtype == CFH_DTYPE_BF16,
-                                          static_cast<hipStream_t>(stream));
+        if (used) launch_skinny(FMT_INT4, ps, used, m, y_dtype == CFH_DTYPE_BF16,
+                                static_cast<hipStream_t>(stream));
     });
 }
 

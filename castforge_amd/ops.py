@@ -196,6 +196,21 @@ def gemm_nf4(x: torch.Tensor, p: Nf4Packed, out_dtype: torch.dtype = torch.bfloa
     return y
 
 
+def gemm_fp8(qa: torch.Tensor, sa: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """W8A8: qa u8 E4M3 [M, K] with per-token sa [M]; qw u8 E4M3 [N, K] with per-row sw [N];
+    returns bf16 [M, N]."""
+    qa, qw = _dev(qa), _dev(qw)
+    m, k = qa.shape
+    n, k2 = qw.shape
+    if k != k2 or qa.dtype != torch.uint8 or qw.dtype != torch.uint8:
+        raise ValueError("qa [M, K] and qw [N, K] must be uint8 E4M3 codes with the same K")
+    y = out if out is not None else torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    ffi.call("castforge_hip_gemm_fp8", _ptr(qa), _ptr(_dev(sa)), m, _ptr(qw), _ptr(_dev(sw)), n, k,
+             _ptr(y), _stream(qa))
+    return y
+
+
 def gemv_w4a16_batched(xs: list[torch.Tensor], ps: list[Int4Packed], ys: list[torch.Tensor]) -> None:
     """One launch for several W4A16 problems with the same M (1..16); outputs preallocated."""
     if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
