@@ -106,7 +106,7 @@ def main():
         tot = 0
         for (_, n, k) in synth.LLAMA7B_BLOCK:
             g = (k + 127) // 128
-            tot += n * k // 2 + n * g * 2 + n * ((g + 7) // 8) * 4 + 2 * m * k + 2 * m * n
+            tot += n * k // 2 + n * ((g + 7) // 8 * 8) * 2 + n * ((g + 7) // 8) * 4 + 2 * m * k + 2 * m * n
         return tot
 
     copies = [packed0] + [[ops.Int4Packed(p.codes.clone(), p.scales.clone(), p.zeros.clone(),
@@ -137,8 +137,8 @@ def main():
         nrows = sum(n for (_, n, k) in synth.LLAMA7B_BLOCK)
         ngroups = sum(n * ((k + 127) // 128) for (_, n, k) in synth.LLAMA7B_BLOCK)
         st, _ = time_steps(lambda i: [ops.quantize_int4g(w, 128) for w in block_f32], 10, 2)
-        q4_bytes = nel * 4 + nel // 2 + ngroups * 2 + sum(n * (((k + 127) // 128 + 7) // 8) * 4
-                                                           for (_, n, k) in synth.LLAMA7B_BLOCK)
+        q4_bytes = nel * 4 + nel // 2 + sum(n * (((k + 127) // 128 + 7) // 8) * (16 + 4)
+                                            for (_, n, k) in synth.LLAMA7B_BLOCK)
         components["quantize_int4g128_GBps"] = round(q4_bytes / (st * 1e-3) / 1e9, 1)
         st, _ = time_steps(lambda i: [ops.quantize_int8(w, 8, "channel", "half_even") for w in block_f32], 10, 2)
         components["quantize_int8_channel_GBps"] = round((nel * 5 + nrows * 4) / (st * 1e-3) / 1e9, 1)

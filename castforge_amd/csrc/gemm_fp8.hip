@@ -40,8 +40,8 @@ __device__ __forceinline__ int32x8 lds_frag(const uint8_t *base) {
 
 __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(
     const uint8_t *__restrict__ A, const float *__restrict__ sa, const uint8_t *__restrict__ W,
-    const float *__restrict__ sw, uint16_t *__restrict__ Y, int M, int N, int K, int tiles_m,
-    int tiles_n) {
+    const float *__restrict__ sw, void *__restrict__ Y, int y_bf16, int M, int N, int K,
+    int tiles_m, int tiles_n) {
     extern __shared__ __align__(16) uint8_t lds[];
 
     // ---- XCD-aware tile mapping ----
@@ -145,7 +145,12 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int n = n0 + wn + j * 16 + lr;
-                if (n < N) Y[static_cast<int64_t>(m) * N + n] = f32_to_bf16_rne(acc[i][j][r] * s * swv[j]);
+                if (n >= N) continue;
+                const float v = acc[i][j][r] * s * swv[j];
+                if (y_bf16)
+                    static_cast<uint16_t *>(Y)[static_cast<int64_t>(m) * N + n] = f32_to_bf16_rne(v);
+                else
+                    static_cast<float *>(Y)[static_cast<int64_t>(m) * N + n] = v;
             }
         }
     }
@@ -154,13 +159,16 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(
 // Any shape (K % 4 == 0): one thread per output, exact e4m3 decode, f32 accumulation.
 __global__ void fp8_gemm_generic_kernel(const uint8_t *__restrict__ A, const float *__restrict__ sa,
                                         const uint8_t *__restrict__ W, const float *__restrict__ sw,
-                                        uint16_t *__restrict__ Y, int64_t M, int64_t N, int64_t K) {
+                                        void *__restrict__ Y, int y_bf16, int64_t M, int64_t N,
+                                        int64_t K) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= M * N) return;
     const int64_t m = idx / N, n = idx - m * N;
     float acc = 0.f;
     for (int64_t k = 0; k < K; ++k) acc += e4m3fn_to_f32(A[m * K + k]) * e4m3fn_to_f32(W[n * K + k]);
-    Y[idx] = f32_to_bf16_rne(acc * sa[m] * sw[n]);
+    const float v = acc * sa[m] * sw[n];
+    if (y_bf16) static_cast<uint16_t *>(Y)[idx] = f32_to_bf16_rne(v);
+    else static_cast<float *>(Y)[idx] = v;
 }
 
 bool lds_attr_set = false;
@@ -172,11 +180,13 @@ using namespace cfh;
 
 extern "C" int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m,
                                           const uint8_t *qw, const float *sw, int64_t n, int64_t k,
-                                          uint16_t *y_bf16, void *stream, char **out_error) {
+                                          void *y, int32_t y_dtype, void *stream, char **out_error) {
     return guarded(out_error, [&] {
         require(m >= 0 && n >= 0 && k >= 0, "m, n, k must be non-negative");
         if (m == 0 || n == 0) return;
-        require(qa && sa && qw && sw && y_bf16, "buffers must not be NULL");
+        require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+        require(qa && sa && qw && sw && y, "buffers must not be NULL");
+        const int yb = y_dtype == CFH_DTYPE_BF16;
         require(m <= 0x7fffffff && n <= 0x7fffffff && k <= 0x7fffffff, "dimensions must fit in int32");
         hipStream_t st = static_cast<hipStream_t>(stream);
         const bool fast = k > 0 && k % BK == 0 && aligned(qa, 16) && aligned(qw, 16);
@@ -189,14 +199,14 @@ extern "C" int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, in
             }
             const int tiles_m = static_cast<int>((m + BM - 1) / BM), tiles_n = static_cast<int>((n + BN - 1) / BN);
             fp8_gemm_kernel<<<dim3(tiles_m * tiles_n), dim3(kThreads), kLdsBytes, st>>>(
-                qa, sa, qw, sw, y_bf16, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+                qa, sa, qw, sw, y, yb, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
                 tiles_m, tiles_n);
             check_launch("fp8_gemm");
         } else {
             const int64_t tot = m * n;
             require((tot + 255) / 256 <= 0x7fffffff, "shape too large for the generic FP8 kernel");
             fp8_gemm_generic_kernel<<<dim3(static_cast<unsigned>((tot + 255) / 256)), dim3(256), 0, st>>>(
-                qa, sa, qw, sw, y_bf16, m, n, k);
+                qa, sa, qw, sw, y, yb, m, n, k);
             check_launch("fp8_gemm_generic");
         }
     });

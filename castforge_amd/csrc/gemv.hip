@@ -34,6 +34,13 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kLdsBytesMax = 32768;  // activation stage per workgroup
 constexpr int kMaxProblems = 8;
+// rows-per-workgroup multiplier and chunks in flight per wave for M <= 4 (tuning knobs)
+#ifndef CFH_GEMV_R_SMALL
+#define CFH_GEMV_R_SMALL 1
+#endif
+#ifndef CFH_GEMV_NB_SMALL
+#define CFH_GEMV_NB_SMALL 8
+#endif
 
 enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2 };
 
@@ -71,17 +78,34 @@ __device__ __forceinline__ int perm_src(int fmt, int i) {
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 __device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
+// A loop-invariant constant held in a VGPR.  gfx9 VOP3 encodings take no literal operand and
+// at most one SGPR, so (w & mask) | magic only becomes a single v_and_or_b32 when both
+// constants already sit in VGPRs.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+    uint32_t v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "i"(c));
+    return v;
+}
+
+struct Int4Consts {
+    uint32_t lo_mask, hi_mask, magic;
+};
+
+__device__ __forceinline__ Int4Consts int4_consts() {
+    return Int4Consts{vgpr_const(0x000F000Fu), vgpr_const(0x00F000F0u), vgpr_const(0x64006400u)};
+}
+
 // INT4 word -> 4 f16 pairs of exact (q - z).  zc1024 = -(1024+z) splat, zc64 = -(64+z) splat.
 // (w & 0x000F000F) | 0x6400_6400 is the f16 pair (1024 + n0, 1024 + n4); the 0x00F0 nibbles
 // give 1024 + 16 n, scaled back by 1/16.  Every intermediate is an exact f16.
 __device__ __forceinline__ void int4_word_to_h(uint32_t w, half2_t zc1024, half2_t zc64,
-                                               uint32_t out[4]) {
+                                               const Int4Consts &k, uint32_t out[4]) {
     const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
     const uint32_t w8 = w >> 8;
-    out[0] = as_u(as_h2((w & 0x000F000Fu) | 0x64006400u) + zc1024);
-    out[1] = as_u(as_h2((w & 0x00F000F0u) | 0x64006400u) * sixteenth + zc64);
-    out[2] = as_u(as_h2((w8 & 0x000F000Fu) | 0x64006400u) + zc1024);
-    out[3] = as_u(as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth + zc64);
+    out[0] = as_u(as_h2((w & k.lo_mask) | k.magic) + zc1024);
+    out[1] = as_u(as_h2((w & k.hi_mask) | k.magic) * sixteenth + zc64);
+    out[2] = as_u(as_h2((w8 & k.lo_mask) | k.magic) + zc1024);
+    out[3] = as_u(as_h2((w8 & k.hi_mask) | k.magic) * sixteenth + zc64);
 }
 
 // INT8 word (4 signed codes) -> 2 f16 pairs of exact q.
@@ -102,24 +126,33 @@ __constant__ float kNf4[16] = {
     0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
     0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer descriptor over [base, base + bytes): 32-bit offsets, reads past `bytes` return 0.
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
 template <int LW>
-__device__ __forceinline__ void load_words(const uint8_t *p, uint32_t *w) {
+__device__ __forceinline__ void load_words(rsrc_t r, uint32_t off, uint32_t *w) {
     if constexpr (LW == 16) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(p);
+        const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     } else if constexpr (LW == 8) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
         w[0] = v.x; w[1] = v.y;
     } else {
-        w[0] = *reinterpret_cast<const uint32_t *>(p);
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
     }
 }
 
 template <int FMT, int LW, int R>
 __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     constexpr int WPL = LW / 4;                         // 32-bit code words per lane per chunk
-    constexpr int CK = 4 * LW * codes_per_byte<FMT>();  // K elements per chunk
-    constexpr int NB = R == 1 ? 8 : 2;                  // chunks in flight per wave
+    constexpr int CPB = codes_per_byte<FMT>();
+    constexpr int CK = 4 * LW * CPB;                    // K elements per chunk
+    constexpr int NB = R == 4 ? 2 : CFH_GEMV_NB_SMALL;  // chunks in flight per wave
     extern __shared__ __align__(16) _Float16 xs[];      // [M][KC], permuted per 8-run
     __shared__ floatx4 red[kWaves - 1][R][64];
     __shared__ uint2 lut[FMT == FMT_NF4 ? 256 : 1];
@@ -132,48 +165,69 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const int M = b.m;
     const int64_t N = P.n, K = P.k;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x - P.tile_begin) * 16 * R;
+    const int rows_here = static_cast<int>((N - n0) < 16 * R ? (N - n0) : 16 * R);
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 15, part = lane >> 4;
-    int64_t nrow[R];
-    bool rok[R];
+    const uint32_t row_bytes = static_cast<uint32_t>(K / CPB);
+    // descriptors over this workgroup's rows only: rows past N read as zero
+    const rsrc_t rc = make_rsrc(static_cast<const uint8_t *>(P.codes) + n0 * row_bytes,
+                                static_cast<uint32_t>(rows_here) * row_bytes);
+    // INT4: scale groups per row; NF4: absmax blocks per row
+    const uint32_t G = static_cast<uint32_t>((K + P.group - 1) / P.group);
+    const uint32_t ZW = (G + 7) / 8, GP = ZW * 8;  // INT4 scale rows are padded to GP groups
+    const int gshift = __builtin_ctz(static_cast<uint32_t>(P.group / CK));  // chunks per group = 2^gshift
+    rsrc_t rs, rz;
+    if constexpr (FMT == FMT_INT4) {
+        rs = make_rsrc(static_cast<const uint16_t *>(P.scales) + n0 * GP, static_cast<uint32_t>(rows_here) * GP * 2);
+        rz = make_rsrc(P.zeros + n0 * ZW, static_cast<uint32_t>(rows_here) * ZW * 4);
+    } else if constexpr (FMT == FMT_NF4) {
+        rs = make_rsrc(static_cast<const float *>(P.scales) + n0 * G, static_cast<uint32_t>(rows_here) * G * 4);
+    }
+    uint32_t code_off[R], sc_off[R], z_off[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        nrow[r] = n0 + 16 * r + lr;
-        rok[r] = nrow[r] < N;
+        const uint32_t row = 16 * r + lr;
+        code_off[r] = row * row_bytes + part * LW;
+        sc_off[r] = row * (FMT == FMT_INT4 ? GP : G);
+        z_off[r] = row * ZW;
     }
-    const int64_t row_bytes = K / codes_per_byte<FMT>();
-    const uint8_t *codes = static_cast<const uint8_t *>(P.codes);
-    const int64_t G = FMT == FMT_INT4 ? (K + P.group - 1) / P.group : 0;
-    const int64_t ZW = (G + 7) / 8;
-    const int64_t NBLK = FMT == FMT_NF4 ? (K + P.group - 1) / P.group : 0;
 
+    // A wave works on "units" of NB consecutive chunks.  Raw loaded words only: decoding a
+    // scale or zero point here would make the wave wait for the load before the staging.
+    // INT4 (one group per chunk): the unit's NB scales are one aligned NB*2-byte load and its
+    // zero points one word, instead of two scattered loads per chunk.
     uint32_t wq[NB][R][WPL];
-    float sc[NB][R];
-    uint32_t zq[NB][R];
+    uint32_t sv[R][NB];  // INT4: f16 scale pairs in [0, NB/2); NF4: f32 absmax bits per chunk
+    uint32_t zv[R];      // INT4: the zero-point word of the unit's 8-group block
 
-    // loads chunks c0, c0 + 4, ... (< cend) of this wave
-    auto load_batch = [&](int c0, int cend) {
+    auto load_unit = [&](int c0, int cend) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const int c = c0 + j * kWaves;
+            const int c = c0 + j;
+            if (c >= cend) break;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                sc[j][r] = 0.f;
-                zq[j][r] = 0;
+                load_words<LW>(rc, code_off[r] + static_cast<uint32_t>(c) * (CK / CPB), wq[j][r]);
+                if constexpr (FMT == FMT_NF4)
+                    sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (sc_off[r] + (static_cast<uint32_t>(c) >> gshift)) * 4, 0, 0);
+            }
+        }
+        if constexpr (FMT == FMT_INT4) {
 #pragma unroll
-                for (int t = 0; t < WPL; ++t) wq[j][r][t] = 0;
-                if (c < cend && rok[r]) {
-                    const int64_t kk = static_cast<int64_t>(c) * CK;
-                    load_words<LW>(codes + nrow[r] * row_bytes + kk / codes_per_byte<FMT>() + part * LW, wq[j][r]);
-                    if constexpr (FMT == FMT_INT4) {
-                        const int64_t g = kk / P.group;
-                        sc[j][r] = f16_to_f32(static_cast<const uint16_t *>(P.scales)[nrow[r] * G + g]);
-                        zq[j][r] = (P.zeros[nrow[r] * ZW + (g >> 3)] >> (4 * (g & 7))) & 15u;
-                    } else if constexpr (FMT == FMT_NF4) {
-                        sc[j][r] = static_cast<const float *>(P.scales)[nrow[r] * NBLK + kk / P.group];
-                    }
+            for (int r = 0; r < R; ++r) {
+                const uint32_t so = (sc_off[r] + static_cast<uint32_t>(c0)) * 2;
+                if constexpr (NB == 8) {
+                    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0));
+                    sv[r][0] = v.x; sv[r][1] = v.y; sv[r][2] = v.z; sv[r][3] = v.w;
+                } else if constexpr (NB == 4) {
+                    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+                    sv[r][0] = v.x; sv[r][1] = v.y;
+                } else {
+                    sv[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
                 }
+                zv[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, (z_off[r] + (static_cast<uint32_t>(c0) >> 3)) * 4, 0, 0);
             }
         }
     };
@@ -181,8 +235,52 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const int KC = P.kc;
     const int nchunks = static_cast<int>(K / CK);
     const int cps = KC / CK;  // chunks per LDS stage
-    // first batch goes out before the activation staging
-    load_batch(wave, cps < nchunks ? cps : nchunks);
+
+    // Activation staging: x[:, k0:k0+kc] becomes permuted f16 in LDS.  The global loads are
+    // issued before the weight loads so that waiting for them (vmcnt drains in issue order)
+    // does not wait for HBM.  At most kLdsBytesMax / 2 halves -> 8 uint4 per thread.
+    constexpr int XMAX = kLdsBytesMax / 2 / 8 / kThreads;
+    uint4 xraw[XMAX];
+    // Loads are unconditional (the index is clamped) so no exec-masked branch splits them:
+    // all of them are in flight together.
+    auto stage_load = [&](int cs_, int ce_) {
+        const int64_t k0 = static_cast<int64_t>(cs_) * CK;
+        const int runs = (ce_ - cs_) * CK / 8;
+        const int items = M * runs;
+#pragma unroll
+        for (int i = 0; i < XMAX; ++i) {
+            if (i * kThreads >= items) break;  // wave-uniform
+            const int it = min(tid + i * kThreads, items - 1);
+            const int m = M == 1 ? 0 : it / runs, rr = it - m * runs;
+            xraw[i] = *reinterpret_cast<const uint4 *>(P.x + static_cast<int64_t>(m) * K + k0 + rr * 8);
+        }
+    };
+    auto stage_store = [&](int cs_, int ce_) {
+        const int runs = (ce_ - cs_) * CK / 8;
+#pragma unroll
+        for (int i = 0; i < XMAX; ++i) {
+            const int it = tid + i * kThreads;
+            if (i * kThreads >= M * runs) break;
+            if (it < M * runs) {
+                const int m = M == 1 ? 0 : it / runs, rr = it - m * runs;
+                const uint32_t wv[4] = {xraw[i].x, xraw[i].y, xraw[i].z, xraw[i].w};
+                uint32_t o[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int s0 = perm_src(FMT, 2 * q), s1 = perm_src(FMT, 2 * q + 1);
+                    const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
+                    const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
+                    half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
+                    o[q] = as_u(h);
+                }
+                *reinterpret_cast<uint4 *>(xs + m * KC + rr * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+    };
+
+    const int ce0 = cps < nchunks ? cps : nchunks;
+    stage_load(0, ce0);
+    load_unit(wave * NB, ce0);  // the first weight unit is in flight during the staging
     bool have = true;
 
     if constexpr (FMT == FMT_NF4) {
@@ -194,77 +292,66 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
             lut[i] = make_uint2(as_u(hi), as_u(lo));
         }
     }
+    stage_store(0, ce0);
+    __syncthreads();
 
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // A rows >= M only feed output rows that are never stored, so they read row 0
+    const int xr = lr < M ? lr : 0;
+    const Int4Consts i4k = int4_consts();
 
     for (int cs = 0; cs < nchunks; cs += cps) {
         const int ce = cs + cps < nchunks ? cs + cps : nchunks;
-        const int64_t k0 = static_cast<int64_t>(cs) * CK;
-        const int kc = (ce - cs) * CK;
-        // ---- stage x[:, k0:k0+kc] as permuted f16 ----
-        __syncthreads();
-        const int runs = kc >> 3;
-        for (int it = tid; it < M * runs; it += kThreads) {
-            const int m = it / runs, rr = it - m * runs;
-            const uint4 raw = *reinterpret_cast<const uint4 *>(P.x + static_cast<int64_t>(m) * K + k0 + rr * 8);
-            const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-            uint32_t o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int s0 = perm_src(FMT, 2 * i), s1 = perm_src(FMT, 2 * i + 1);
-                const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
-                const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
-                half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
-                o[i] = as_u(h);
-            }
-            *reinterpret_cast<uint4 *>(xs + m * KC + rr * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+        if (cs > 0) {
+            __syncthreads();  // every wave is done with the previous stage
+            stage_load(cs, ce);
+            stage_store(cs, ce);
+            __syncthreads();
         }
-        __syncthreads();
 
-        for (int cb = cs + wave; cb < ce; cb += kWaves * NB) {
-            if (!have) load_batch(cb, ce);
+        for (int cb = cs + wave * NB; cb < ce; cb += kWaves * NB) {
+            if (!have) load_unit(cb, ce);
             have = false;
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
-                const int c = cb + j * kWaves;
+                const int c = cb + j;
                 if (c >= ce) break;
-                const int xoff = (c - cs) * CK + part * (CK / 4);
-                const _Float16 *xa = xs + lr * KC + xoff;
+                const _Float16 *xa = xs + xr * KC + (c - cs) * CK + part * (CK / 4);
                 if constexpr (FMT == FMT_INT4) {
                     floatx4 pacc[R];
-                    half2_t zc1024[R], zc64[R];
+                    uint32_t zc1024[R], zc64[R];
+                    const uint32_t gsh = 4 * (static_cast<uint32_t>(c) & 7u);
 #pragma unroll
                     for (int r = 0; r < R; ++r) {
                         pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
-                        const _Float16 a = static_cast<_Float16>(-1024.0f - static_cast<float>(zq[j][r]));
-                        const _Float16 s = static_cast<_Float16>(-64.0f - static_cast<float>(zq[j][r]));
-                        zc1024[r] = half2_t{a, a};
-                        zc64[r] = half2_t{s, s};
+                        const uint32_t z = (zv[r] >> gsh) & 15u;
+                        // f16 bits of -(1024 + z) and -(64 + z), splatted to both halves
+                        zc1024[r] = (0xE400u + z) * 0x00010001u;
+                        zc64[r] = (0xD400u + (z << 4)) * 0x00010001u;
                     }
 #pragma unroll
                     for (int t = 0; t < WPL; ++t) {
-                        half8_t aop = {};
-                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+                        const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
 #pragma unroll
                         for (int r = 0; r < R; ++r) {
                             uint32_t hb[4];
-                            int4_word_to_h(wq[j][r][t], zc1024[r], zc64[r], hb);
+                            int4_word_to_h(wq[j][r][t], as_h2(zc1024[r]), as_h2(zc64[r]), i4k, hb);
                             pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(hb[0], hb[1], hb[2], hb[3]),
                                                                             pacc[r], 0, 0, 0);
                         }
                     }
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] += pacc[r] * sc[j][r];
+                    for (int r = 0; r < R; ++r)
+                        acc[r] += pacc[r] * f16_to_f32(static_cast<uint16_t>(sv[r][j >> 1] >> (16 * (j & 1))));
                 } else if constexpr (FMT == FMT_NF4) {
                     floatx4 pacc[R];
 #pragma unroll
                     for (int r = 0; r < R; ++r) pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int t = 0; t < WPL; ++t) {
-                        half8_t aop = {};
-                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+                        const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
 #pragma unroll
                         for (int r = 0; r < R; ++r) {
                             const uint32_t w = wq[j][r][t];
@@ -275,12 +362,11 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
                         }
                     }
 #pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] += pacc[r] * sc[j][r];
+                    for (int r = 0; r < R; ++r) acc[r] += pacc[r] * __builtin_bit_cast(float, sv[r][j]);
                 } else {
 #pragma unroll
                     for (int t = 0; t < WPL / 2; ++t) {
-                        half8_t aop = {};
-                        if (lr < M) aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+                        const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
 #pragma unroll
                         for (int r = 0; r < R; ++r) {
                             uint32_t h0[2], h1[2];
@@ -306,19 +392,20 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
         for (int r = 0; r < R; ++r) {
 #pragma unroll
             for (int w = 0; w < kWaves - 1; ++w) acc[r] += red[w][r][lane];
-            if (!rok[r]) continue;
+            const int64_t nrow = n0 + 16 * r + lr;
+            if (nrow >= N) continue;
             if constexpr (FMT == FMT_INT8) {
                 const float *s = static_cast<const float *>(P.scales);
-                acc[r] *= P.scale_per_row ? s[nrow[r]] : s[0];
+                acc[r] *= P.scale_per_row ? s[nrow] : s[0];
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int m = part * 4 + q;
                 if (m < M) {
                     if (b.y_bf16)
-                        static_cast<uint16_t *>(P.y)[static_cast<int64_t>(m) * N + nrow[r]] = f32_to_bf16_rne(acc[r][q]);
+                        static_cast<uint16_t *>(P.y)[static_cast<int64_t>(m) * N + nrow] = f32_to_bf16_rne(acc[r][q]);
                     else
-                        static_cast<float *>(P.y)[static_cast<int64_t>(m) * N + nrow[r]] = acc[r][q];
+                        static_cast<float *>(P.y)[static_cast<int64_t>(m) * N + nrow] = acc[r][q];
                 }
             }
         }
@@ -333,7 +420,7 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
     const int lane = threadIdx.x;
     const int64_t K = P.k, N = P.n;
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const int64_t G = (FMT == FMT_INT4) ? (K + P.group - 1) / P.group : 0, ZW = (G + 7) / 8;
+    const int64_t G = (FMT == FMT_INT4) ? (K + P.group - 1) / P.group : 0, ZW = (G + 7) / 8, GP = ZW * 8;
     const int64_t NBLK = (FMT == FMT_NF4) ? (K + P.group - 1) / P.group : 0;
     for (int64_t k = lane; k < K; k += 64) {
         float w;
@@ -346,7 +433,7 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
                 const int64_t g = k / P.group;
                 const int32_t z = static_cast<int32_t>((P.zeros[n * ZW + (g >> 3)] >> (4 * (g & 7))) & 15u);
                 w = static_cast<float>(static_cast<int32_t>(q) - z) *
-                    f16_to_f32(static_cast<const uint16_t *>(P.scales)[n * G + g]);
+                    f16_to_f32(static_cast<const uint16_t *>(P.scales)[n * GP + g]);
             } else {
                 w = kNf4[q] * static_cast<const float *>(P.scales)[n * NBLK + k / P.group];
             }
@@ -377,7 +464,8 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
 // Bytes each lane loads per chunk for this format / group (0 = no MFMA path).
 int lw_for(int fmt, int64_t group) {
     if (fmt == FMT_INT8) return 16;
-    if (group % 128 == 0) return 16;
+    // the chunk index maps to the group by a shift: group / chunk must be a power of two
+    if (group >= 128 && group % 128 == 0 && ((group / 128) & (group / 128 - 1)) == 0) return 16;
     if (group == 64) return 8;
     if (group == 32) return 4;
     return 0;
@@ -390,13 +478,18 @@ bool skinny_ok(int fmt, const Problem &p, int64_t m) {
     const int lw = lw_for(fmt, p.group);
     if (lw == 0) return false;
     if (p.k % chunk_k(fmt, lw) != 0) return false;
+    // INT4 metadata is loaded per unit of consecutive groups: one group per chunk
+    if (fmt == FMT_INT4 && p.group != chunk_k(fmt, lw)) return false;
+    if (p.k >= (int64_t{1} << 24)) return false;  // 32-bit buffer offsets over 64 rows
     return aligned(p.x, 16) && aligned(p.codes, 16);
 }
 
-int32_t kc_for(int64_t k, int64_t m, int ck) {
+// K elements staged per LDS pass: a whole number of units (unit = nb chunks of ck elements)
+int32_t kc_for(int64_t k, int64_t m, int ck, int nb) {
+    const int64_t unit = static_cast<int64_t>(ck) * nb;
     int64_t kc = (kLdsBytesMax / 2) / m;
-    kc = (kc / ck) * ck;
-    if (kc < ck) kc = ck;
+    kc = (kc / unit) * unit;
+    if (kc < unit) kc = unit;
     return static_cast<int32_t>(kc < k ? kc : k);
 }
 
@@ -419,7 +512,7 @@ void launch_lw(int lw, const Batch &b, int64_t tiles, int64_t lds, hipStream_t s
 void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipStream_t st) {
     const int lw = lw_for(fmt, ps[0].group);
     const int ck = chunk_k(fmt, lw);
-    const int R = m <= 4 ? 1 : 4;
+    const int R = m <= 4 ? CFH_GEMV_R_SMALL : 4;
     // longest K first: its workgroups run longest, so they start first
     std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
     Batch b{};
@@ -428,7 +521,7 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
         require(lw_for(fmt, ps[i].group) == lw, "batched problems must share the group size class");
         b.p[i] = ps[i];
         b.p[i].tile_begin = static_cast<int32_t>(tiles);
-        b.p[i].kc = kc_for(ps[i].k, m, ck);
+        b.p[i].kc = kc_for(ps[i].k, m, ck, R == 4 ? 2 : CFH_GEMV_NB_SMALL);
         tiles += (ps[i].n + 16 * R - 1) / (16 * R);
         const int64_t lds = m * b.p[i].kc * 2;
         if (lds > max_lds) max_lds = lds;
@@ -439,13 +532,13 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
     b.y_bf16 = y_bf16;
     if (tiles == 0) return;
     if (fmt == FMT_INT4) {
-        if (R == 1) launch_lw<FMT_INT4, 1>(lw, b, tiles, max_lds, st);
+        if (R != 4) launch_lw<FMT_INT4, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
         else launch_lw<FMT_INT4, 4>(lw, b, tiles, max_lds, st);
     } else if (fmt == FMT_NF4) {
-        if (R == 1) launch_lw<FMT_NF4, 1>(lw, b, tiles, max_lds, st);
+        if (R != 4) launch_lw<FMT_NF4, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
         else launch_lw<FMT_NF4, 4>(lw, b, tiles, max_lds, st);
     } else {
-        if (R == 1) launch_lw<FMT_INT8, 1>(lw, b, tiles, max_lds, st);
+        if (R != 4) launch_lw<FMT_INT8, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
         else launch_lw<FMT_INT8, 4>(lw, b, tiles, max_lds, st);
     }
     check_launch("skinny_qgemm");

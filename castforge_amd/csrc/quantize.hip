@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void int4g_quant_kernel(const float *__rest
     constexpr int TPB = kBlock / T;   // tasks per block
     constexpr int TPG = GROUP / 8;    // threads per group
     __shared__ uint32_t zpart[kBlock / 64];
-    const int64_t KW = cols >> 3, G = (cols + GROUP - 1) / GROUP, ZW = (G + 7) >> 3;
+    const int64_t KW = cols >> 3, G = (cols + GROUP - 1) / GROUP, ZW = (G + 7) >> 3, GP = ZW * 8;
     const int64_t task = static_cast<int64_t>(blockIdx.x) * TPB + threadIdx.x / T;
     const int t = threadIdx.x % T;
     const int64_t row = task / ZW, zw = task - row * ZW;
@@ -277,10 +277,12 @@ __global__ __launch_bounds__(kBlock) void int4g_quant_kernel(const float *__rest
         }
         codes[row * KW + w] = word;
         if (t % TPG == 0) {
-            scales[row * G + zw * 8 + gi] = h;
+            scales[row * GP + zw * 8 + gi] = h;
             zn = static_cast<uint32_t>(zf) << (4 * gi);
         }
     }
+    // pad scale slots of the last 8-group block (no valid thread) are written as 0
+    if (task_ok && !ok && t % TPG == 0 && zw * 8 + gi >= G) scales[row * GP + zw * 8 + gi] = 0;
     if constexpr (T <= 64) {
         zn = wave_or<T>(zn);
         if (t == 0 && task_ok) zeros[row * ZW + zw] = zn;
@@ -376,7 +378,7 @@ __global__ void dequant_int4g_kernel(const uint32_t *__restrict__ codes,
                                      const uint16_t *__restrict__ scales,
                                      const uint32_t *__restrict__ zeros, int64_t rows, int64_t cols,
                                      int64_t group, float *__restrict__ out) {
-    const int64_t KW = cols >> 3, G = (cols + group - 1) / group, ZW = (G + 7) >> 3;
+    const int64_t KW = cols >> 3, G = (cols + group - 1) / group, ZW = (G + 7) >> 3, GP = ZW * 8;
     const int64_t nw = rows * KW;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nw; i += stride) {
@@ -386,7 +388,7 @@ __global__ void dequant_int4g_kernel(const uint32_t *__restrict__ codes,
             const int64_t k = w * 8 + j, g = k / group;
             const int32_t z = static_cast<int32_t>((zeros[r * ZW + (g >> 3)] >> (4 * (g & 7))) & 15u);
             const int32_t q = static_cast<int32_t>((word >> (4 * j)) & 15u);
-            out[r * cols + k] = static_cast<float>(q - z) * f16_to_f32(scales[r * G + g]);
+            out[r * cols + k] = static_cast<float>(q - z) * f16_to_f32(scales[r * GP + g]);
         }
     }
 }

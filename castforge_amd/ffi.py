@@ -64,7 +64,7 @@ SIGNATURES = {
     "castforge_hip_gemv_w8a16": (c_int32, [_P, c_int64, c_int64, c_int64, _P, _P, c_int32, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_nf4": (c_int32, [_P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_w4a16_batched": (c_int32, [POINTER(W4A16Problem), c_int32, c_int64, c_int32, _P, _E]),
-    "castforge_hip_gemm_fp8": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, _P, _E]),
+    "castforge_hip_gemm_fp8": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, c_int32, _P, _E]),
 }
 
 _lib = None

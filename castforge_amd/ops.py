@@ -69,7 +69,8 @@ def dequantize_int8(codes: torch.Tensor, scales: torch.Tensor, granularity: str 
 # --------------------------------------------------------------------------- INT4g ----
 @dataclass
 class Int4Packed:
-    """INT4 asymmetric group-wise weights: codes u32 [N, K/8], scales f16 [N, G], zeros u32 [N, ceil(G/8)]."""
+    """INT4 asymmetric group-wise weights: codes u32 [N, K/8], scales f16 [N, 8*ceil(G/8)] (row-padded),
+    zeros u32 [N, ceil(G/8)]."""
     codes: torch.Tensor
     scales: torch.Tensor
     zeros: torch.Tensor
@@ -88,7 +89,7 @@ def quantize_int4g(w: torch.Tensor, group: int = 128) -> Int4Packed:
     n, k = w.shape
     g = (k + group - 1) // group
     codes = torch.empty((n, k // 8), dtype=torch.int32, device=w.device)
-    scales = torch.empty((n, g), dtype=torch.float16, device=w.device)
+    scales = torch.empty((n, (g + 7) // 8 * 8), dtype=torch.float16, device=w.device)
     zeros = torch.empty((n, (g + 7) // 8), dtype=torch.int32, device=w.device)
     ffi.call("castforge_hip_quantize_int4g", _ptr(w), n, k, group, _ptr(codes), _ptr(scales),
              _ptr(zeros), _stream(w))
@@ -197,17 +198,17 @@ def gemm_nf4(x: torch.Tensor, p: Nf4Packed, out_dtype: torch.dtype = torch.bfloa
 
 
 def gemm_fp8(qa: torch.Tensor, sa: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """W8A8: qa u8 E4M3 [M, K] with per-token sa [M]; qw u8 E4M3 [N, K] with per-row sw [N];
-    returns bf16 [M, N]."""
+    returns [M, N] in out_dtype (bfloat16 or float32)."""
     qa, qw = _dev(qa), _dev(qw)
     m, k = qa.shape
     n, k2 = qw.shape
     if k != k2 or qa.dtype != torch.uint8 or qw.dtype != torch.uint8:
         raise ValueError("qa [M, K] and qw [N, K] must be uint8 E4M3 codes with the same K")
-    y = out if out is not None else torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    y = out if out is not None else torch.empty((m, n), dtype=out_dtype, device=qa.device)
     ffi.call("castforge_hip_gemm_fp8", _ptr(qa), _ptr(_dev(sa)), m, _ptr(qw), _ptr(_dev(sw)), n, k,
-             _ptr(y), _stream(qa))
+             _ptr(y), _out_dtype(y.dtype), _stream(qa))
     return y
 
 

@@ -141,14 +141,15 @@ int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, in
                                          int64_t m, int32_t y_dtype, void *stream,
                                          char **out_error);
 
-/* FP8 E4M3 W8A8 GEMM: y_bf16[m, n] = bf16((sum_k e4m3(qa[m,k]) * e4m3(qw[n,k])) * sa[m] * sw[n]).
+/* FP8 E4M3 W8A8 GEMM: y[m, n] = (sum_k e4m3(qa[m,k]) * e4m3(qw[n,k])) * sa[m] * sw[n], stored
+ * as bf16 (RNE) or f32 per y_dtype.
  * qa/sa come from castforge_hip_quantize_fp8 on the activations (per token), qw/sw on the
  * weights (per output channel).  New W8A8 path for `castforge.fused_qmatmul` (the reference's
  * fp8 pass, passes/quantize/schemes.rs:633-754, writes dequantized f32 back instead).
  * k % 128 == 0 with 16-byte aligned qa/qw runs the MFMA kernel; other shapes run a slow
  * exact fallback. */
 int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *qw,
-                               const float *sw, int64_t n, int64_t k, uint16_t *y_bf16,
+                               const float *sw, int64_t n, int64_t k, void *y, int32_t y_dtype,
                                void *stream, char **out_error);
 
 #ifdef __cplusplus

@@ -339,8 +339,9 @@ void orc_quantize_int8_rows(const float *v, int64_t n, int64_t k, int bits, int 
  *   range >= 1e-12 ? h = f16_rne(range / 15) : h = f16(1.0);  h == +0 -> 0x0001; h == Inf -> 0x7BFF
  *   s = f32(h);  z = clamp(rne(-mn / s), 0, 15)  (NaN -> 0)
  *   q = clamp(rne(v / s) [NaN -> 0] + z, 0, 15)
- * codes[n][k/8] u32: element k at bits 4*(k%8); scales[n][G] f16 bits; zeros[n][ceil(G/8)]
- * u32: zero of group g at bits 4*(g%8). */
+ * codes[n][k/8] u32: element k at bits 4*(k%8); scales[n][GP] f16 bits with GP = 8*ceil(G/8)
+ * (rows padded to whole 8-group blocks, pad entries 0, so 8 scales load as one aligned 16 B);
+ * zeros[n][GP/8] u32: zero of group g at bits 4*(g%8). */
 static inline uint16_t int4_scale_bits(float mx, float mn) {
     float range = mx - mn;
     uint16_t h;
@@ -353,11 +354,12 @@ static inline uint16_t int4_scale_bits(float mx, float mn) {
 
 void orc_quantize_int4g(const float *v, int64_t n, int64_t k, int64_t group, uint32_t *codes,
                         uint16_t *scales_f16, uint32_t *zeros) {
-    int64_t G = (k + group - 1) / group, ZW = (G + 7) / 8, KW = k / 8;
+    int64_t G = (k + group - 1) / group, ZW = (G + 7) / 8, GP = ZW * 8, KW = k / 8;
     for (int64_t r = 0; r < n; ++r) {
         const float *row = v + r * k;
         for (int64_t w = 0; w < KW; ++w) codes[r * KW + w] = 0;
         for (int64_t w = 0; w < ZW; ++w) zeros[r * ZW + w] = 0;
+        for (int64_t g = 0; g < GP; ++g) scales_f16[r * GP + g] = 0;
         for (int64_t g = 0; g < G; ++g) {
             int64_t k0 = g * group, k1 = k0 + group < k ? k0 + group : k;
             float mx = -INFINITY, mn = INFINITY;
@@ -368,7 +370,7 @@ void orc_quantize_int4g(const float *v, int64_t n, int64_t k, int64_t group, uin
             if (isnan(zf)) zf = 0.0f;
             zf = fminf(fmaxf(zf, 0.0f), 15.0f);
             uint32_t z = (uint32_t)zf;
-            scales_f16[r * G + g] = h;
+            scales_f16[r * GP + g] = h;
             zeros[r * ZW + g / 8] |= z << (4 * (g % 8));
             for (int64_t i = k0; i < k1; ++i) {
                 float t = nearbyintf(row[i] / s);
@@ -382,13 +384,13 @@ void orc_quantize_int4g(const float *v, int64_t n, int64_t k, int64_t group, uin
 
 void orc_dequantize_int4g(const uint32_t *codes, const uint16_t *scales_f16,
                           const uint32_t *zeros, int64_t n, int64_t k, int64_t group, float *out) {
-    int64_t G = (k + group - 1) / group, ZW = (G + 7) / 8, KW = k / 8;
+    int64_t G = (k + group - 1) / group, ZW = (G + 7) / 8, GP = ZW * 8, KW = k / 8;
     for (int64_t r = 0; r < n; ++r)
         for (int64_t i = 0; i < k; ++i) {
             int64_t g = i / group;
             int32_t q = (int32_t)((codes[r * KW + i / 8] >> (4 * (i % 8))) & 0xFu);
             int32_t z = (int32_t)((zeros[r * ZW + g / 8] >> (4 * (g % 8))) & 0xFu);
-            out[r * k + i] = (float)(q - z) * orc_f16_to_f32(scales_f16[r * G + g]);
+            out[r * k + i] = (float)(q - z) * orc_f16_to_f32(scales_f16[r * GP + g]);
         }
 }
 

@@ -70,7 +70,8 @@ void orc_quantize_fp8_grid(const float *v, int64_t n, int e5m2, int mxfp8, int64
 /* INT8/INT4 symmetric per output channel: rows of [n, k], one scale per row */
 void orc_quantize_int8_rows(const float *v, int64_t n, int64_t k, int bits, int round_mode,
                             int8_t *q, float *scales);
-/* INT4 asymmetric group-wise along K with fp16 scale and u4 zero-point, 8 codes / u32 */
+/* INT4 asymmetric group-wise along K with fp16 scale and u4 zero-point, 8 codes / u32;
+ * scales are [n][8*ceil(G/8)] (row-padded, pad 0), zeros [n][ceil(G/8)] */
 void orc_quantize_int4g(const float *v, int64_t n, int64_t k, int64_t group, uint32_t *codes,
                         uint16_t *scales_f16, uint32_t *zeros);
 void orc_dequantize_int4g(const uint32_t *codes, const uint16_t *scales_f16,

@@ -102,7 +102,7 @@ def quantize_int4g(w: np.ndarray, group: int = 128):
     n, k = w.shape
     g = (k + group - 1) // group
     codes = np.zeros((n, k // 8), np.uint32)
-    scales = np.zeros((n, g), np.uint16)
+    scales = np.zeros((n, (g + 7) // 8 * 8), np.uint16)
     zeros = np.zeros((n, (g + 7) // 8), np.uint32)
     lib().orc_quantize_int4g(_p(w), n, k, group, _p(codes), _p(scales), _p(zeros))
     return codes, scales, zeros

@@ -1,6 +1,12 @@
 """GPU parity of the FP8 E4M3 W8A8 GEMM: against the oracle (dequantize, eval_matmul_2d) at
-small shapes and against a torch fp32 GEMM of the same dequantized operands at the BASELINE
-shapes; tolerance |y - ref| <= 1e-3 + 1e-2 |ref|."""
+small shapes and against an fp64 GEMM of the same dequantized operands at the BASELINE shapes.
+
+Tolerance: |y - ref| <= 1e-3 + 1e-2 |ref| + K * 2^-24 * sum_k |a_k w_k|.  The last term is the
+classical worst-case rounding bound of a length-K f32 dot product (gamma_K = K u, u = 2^-24);
+the reference's own sequential f32 loop (eval.rs:1492-1505) carries that error too.  It only
+matters for ill-conditioned outputs (|y| << sum |a w|): with 0.5% x30 outliers the MFMA's
+accumulation order lands a handful of the 45M outputs past the plain 1e-3 / 1e-2 bound while
+staying ~10x inside gamma_K (measured max error / sum|a w| = 1.8e-5 at K = 4096)."""
 import numpy as np
 import pytest
 import torch
@@ -13,12 +19,15 @@ pytestmark = pytest.mark.gpu
 RTOL, ATOL = 1e-2, 1e-3
 
 
-def _close(y, ref):
+def _close(y, ref, mag, k):
     y = y.float().cpu().numpy() if isinstance(y, torch.Tensor) else y
-    ref = ref.cpu().numpy() if isinstance(ref, torch.Tensor) else ref
     err = np.abs(y - ref)
-    bad = err > ATOL + RTOL * np.abs(ref)
+    bad = err > ATOL + RTOL * np.abs(ref) + k * 2.0 ** -24 * mag
     assert not bad.any(), f"{bad.sum()} / {bad.size} outside tol; max err {err.max():.3e}"
+
+
+def _deq(q, s):
+    return torch.from_numpy(q).view(torch.float8_e4m3fn).double().numpy() * s.astype(np.float64)[:, None]
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 128, 256), (300, 200, 384), (256, 128, 128), (17, 33, 1024),
@@ -31,8 +40,10 @@ def test_fp8_gemm_vs_oracle(cuda, m, n, k):
     qa, sa = ops.quantize_fp8(torch.from_numpy(a).to(cuda))
     qw, sw = ops.quantize_fp8(torch.from_numpy(w).to(cuda))
     assert np.array_equal(qa.cpu().numpy(), qa_ref) and np.array_equal(qw.cpu().numpy(), qw_ref)
-    y = ops.gemm_fp8(qa, sa, qw, sw)
-    _close(y, O.gemm_fp8(qa_ref, sa_ref, qw_ref, sw_ref))
+    mag = np.abs(_deq(qa_ref, sa_ref)) @ np.abs(_deq(qw_ref, sw_ref)).T
+    for out in (torch.bfloat16, torch.float32):
+        y = ops.gemm_fp8(qa, sa, qw, sw, out_dtype=out)
+        _close(y, O.gemm_fp8(qa_ref, sa_ref, qw_ref, sw_ref), mag, k)
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 11008, 4096), (4096, 4096, 11008)])
@@ -44,14 +55,16 @@ def test_fp8_gemm_baseline_shapes(cuda, m, n, k):
     w = torch.randn((n, k), generator=g, device=cuda) * 0.02
     qa, sa = ops.quantize_fp8(a.to(torch.bfloat16))
     qw, sw = ops.quantize_fp8(w)
-    y = ops.gemm_fp8(qa, sa, qw, sw)
-    ad = qa.view(torch.float8_e4m3fn).float() * sa[:, None]
-    wd = qw.view(torch.float8_e4m3fn).float() * sw[:, None]
+    ad = qa.view(torch.float8_e4m3fn).double() * sa[:, None].double()
+    wd = qw.view(torch.float8_e4m3fn).double() * sw[:, None].double()
     ref = ad @ wd.t()
-    torch.cuda.synchronize()
-    err = (y.float() - ref).abs()
-    bad = err > ATOL + RTOL * ref.abs()
-    assert int(bad.sum()) == 0, f"{int(bad.sum())} outside tol; max err {float(err.max()):.3e}"
+    mag = ad.abs() @ wd.abs().t()
+    for out in (torch.bfloat16, torch.float32):
+        y = ops.gemm_fp8(qa, sa, qw, sw, out_dtype=out)
+        torch.cuda.synchronize()
+        err = (y.double() - ref).abs()
+        bad = err > ATOL + RTOL * ref.abs() + k * 2.0 ** -24 * mag
+        assert int(bad.sum()) == 0, f"{int(bad.sum())} outside tol; max err {float(err.max()):.3e}"
 
 
 def test_fp8_gemm_zero_and_outliers(cuda):
@@ -65,4 +78,5 @@ def test_fp8_gemm_zero_and_outliers(cuda):
     y = ops.gemm_fp8(qa, sa, qw, sw)
     qa_ref, sa_ref = O.quantize_fp8_rows(a)
     qw_ref, sw_ref = O.quantize_fp8_rows(w)
-    _close(y, O.gemm_fp8(qa_ref, sa_ref, qw_ref, sw_ref))
+    mag = np.abs(_deq(qa_ref, sa_ref)) @ np.abs(_deq(qw_ref, sw_ref)).T
+    _close(y, O.gemm_fp8(qa_ref, sa_ref, qw_ref, sw_ref), mag, k)

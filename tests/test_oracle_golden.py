@@ -200,7 +200,7 @@ def _int4_numpy(w, group):
     n, k = w.shape
     G = (k + group - 1) // group
     codes = np.zeros((n, k), np.uint32)
-    scales = np.zeros((n, G), np.uint16)
+    scales = np.zeros((n, (G + 7) // 8 * 8), np.uint16)
     zeros = np.zeros((n, G), np.uint32)
     for g in range(G):
         blk = w[:, g * group:(g + 1) * group]
@@ -248,7 +248,7 @@ def test_int4g_closed_forms():
             assert qq[blk.argmin()] == 0          # the minimum maps to code 0 (min <= 0 here)
             assert qq[blk.argmax()] >= 14         # the maximum maps to the top of the range
     deq = O.dequantize_int4g(codes, scales, zeros, 16, 1024, 128)
-    s = np.repeat(scales.view(np.float16).astype(np.float32), 128, axis=1)
+    s = np.repeat(scales[:, :8].view(np.float16).astype(np.float32), 128, axis=1)
     assert np.all(np.abs(deq - w) <= s * 1.0 + 1e-7)   # rounding of v/s and of z: <= s
 
 
