@@ -134,6 +134,14 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
                                              static_cast<int>(bytes), 0x00020000);
 }
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory loads are
+// outstanding and ignores the export and LDS/scalar counters.
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Loads one INT4 unit issues per row tile: NB code loads, one scale load, one zero-point load.
+template <int NB, int R>
+constexpr int kVmcntAfterUnitInt4() { return vmcnt_imm(R * (NB + 2)); }
+
 template <int LW>
 __device__ __forceinline__ void load_words(rsrc_t r, uint32_t off, uint32_t *w) {
     if constexpr (LW == 16) {
@@ -206,10 +214,13 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const int c = c0 + j;
-            if (c >= cend) break;
+            // INT4 always issues NB code loads so the staging wait can count them; a chunk
+            // past the end reads out of the descriptor's range and returns zero
+            if (FMT != FMT_INT4 && c >= cend) break;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                load_words<LW>(rc, code_off[r] + static_cast<uint32_t>(c) * (CK / CPB), wq[j][r]);
+                const uint32_t off = c < cend ? code_off[r] + static_cast<uint32_t>(c) * (CK / CPB) : 0x80000000u;
+                load_words<LW>(rc, off, wq[j][r]);
                 if constexpr (FMT == FMT_NF4)
                     sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (sc_off[r] + (static_cast<uint32_t>(c) >> gshift)) * 4, 0, 0);
             }
@@ -236,50 +247,48 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const int nchunks = static_cast<int>(K / CK);
     const int cps = KC / CK;  // chunks per LDS stage
 
-    // Activation staging: x[:, k0:k0+kc] becomes permuted f16 in LDS.  The global loads are
-    // issued before the weight loads so that waiting for them (vmcnt drains in issue order)
-    // does not wait for HBM.  At most kLdsBytesMax / 2 halves -> 8 uint4 per thread.
-    constexpr int XMAX = kLdsBytesMax / 2 / 8 / kThreads;
-    uint4 xraw[XMAX];
-    // Loads are unconditional (the index is clamped) so no exec-masked branch splits them:
-    // all of them are in flight together.
-    auto stage_load = [&](int cs_, int ce_) {
+    // Activation staging.  x[:, k0:k0+kc] is copied as raw bf16 straight into LDS
+    // (global_load_lds: no VGPRs held), laid out [m][kc].  The copy is issued before the weight
+    // loads, so waiting for it (vmcnt drains in issue order) does not wait for HBM.  After a
+    // barrier every thread converts its 16-byte runs in place to f16, permuted into the order
+    // the code extraction produces, and a second barrier publishes them.
+    auto stage_copy = [&](int cs_, int ce_) {
         const int64_t k0 = static_cast<int64_t>(cs_) * CK;
-        const int runs = (ce_ - cs_) * CK / 8;
-        const int items = M * runs;
-#pragma unroll
-        for (int i = 0; i < XMAX; ++i) {
-            if (i * kThreads >= items) break;  // wave-uniform
-            const int it = min(tid + i * kThreads, items - 1);
-            const int m = M == 1 ? 0 : it / runs, rr = it - m * runs;
-            xraw[i] = *reinterpret_cast<const uint4 *>(P.x + static_cast<int64_t>(m) * K + k0 + rr * 8);
+        const int kc = (ce_ - cs_) * CK;
+        const int bytes = M * kc * 2;
+        for (int blk = wave; blk * 1024 < bytes; blk += kWaves) {  // wave-uniform
+            const int e = blk * 1024 + lane * 16;  // byte offset in the stage
+            if (e < bytes) {
+                const int el = e >> 1;
+                const int m = M == 1 ? 0 : el / kc, kk = el - m * kc;
+                __builtin_amdgcn_global_load_lds(
+                    static_cast<const void *>(P.x + static_cast<int64_t>(m) * K + k0 + kk),
+                    reinterpret_cast<__attribute__((address_space(3))) void *>(
+                        reinterpret_cast<uintptr_t>(xs) + blk * 1024),
+                    16, 0, 0);
+            }
         }
     };
-    auto stage_store = [&](int cs_, int ce_) {
-        const int runs = (ce_ - cs_) * CK / 8;
+    auto stage_convert = [&](int cs_, int ce_) {
+        const int runs = M * (ce_ - cs_) * CK / 8;
+        for (int it = tid; it < runs; it += kThreads) {
+            const uint4 raw = *reinterpret_cast<const uint4 *>(xs + it * 8);
+            const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+            uint32_t o[4];
 #pragma unroll
-        for (int i = 0; i < XMAX; ++i) {
-            const int it = tid + i * kThreads;
-            if (i * kThreads >= M * runs) break;
-            if (it < M * runs) {
-                const int m = M == 1 ? 0 : it / runs, rr = it - m * runs;
-                const uint32_t wv[4] = {xraw[i].x, xraw[i].y, xraw[i].z, xraw[i].w};
-                uint32_t o[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int s0 = perm_src(FMT, 2 * q), s1 = perm_src(FMT, 2 * q + 1);
-                    const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
-                    const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
-                    half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
-                    o[q] = as_u(h);
-                }
-                *reinterpret_cast<uint4 *>(xs + m * KC + rr * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+            for (int q = 0; q < 4; ++q) {
+                const int s0 = perm_src(FMT, 2 * q), s1 = perm_src(FMT, 2 * q + 1);
+                const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
+                const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
+                half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
+                o[q] = as_u(h);
             }
+            *reinterpret_cast<uint4 *>(xs + it * 8) = make_uint4(o[0], o[1], o[2], o[3]);
         }
     };
 
     const int ce0 = cps < nchunks ? cps : nchunks;
-    stage_load(0, ce0);
+    stage_copy(0, ce0);
     load_unit(wave * NB, ce0);  // the first weight unit is in flight during the staging
     bool have = true;
 
@@ -292,8 +301,15 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
             lut[i] = make_uint2(as_u(hi), as_u(lo));
         }
     }
-    stage_store(0, ce0);
-    __syncthreads();
+    // Wait for this wave's LDS copies only: they were issued before the weight loads and
+    // vmcnt drains in issue order.  A bare s_barrier is used because __syncthreads() carries a
+    // release fence that would also wait for the weight loads still in flight.
+    if constexpr (FMT == FMT_INT4) __builtin_amdgcn_s_waitcnt(kVmcntAfterUnitInt4<NB, R>());
+    else __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+    stage_convert(0, ce0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));  // this wave's LDS writes are done
+    __builtin_amdgcn_s_barrier();
 
     floatx4 acc[R];
 #pragma unroll
@@ -306,8 +322,10 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
         const int ce = cs + cps < nchunks ? cs + cps : nchunks;
         if (cs > 0) {
             __syncthreads();  // every wave is done with the previous stage
-            stage_load(cs, ce);
-            stage_store(cs, ce);
+            stage_copy(cs, ce);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            stage_convert(cs, ce);
             __syncthreads();
         }
 
@@ -318,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
             for (int j = 0; j < NB; ++j) {
                 const int c = cb + j;
                 if (c >= ce) break;
-                const _Float16 *xa = xs + xr * KC + (c - cs) * CK + part * (CK / 4);
+                const _Float16 *xa = xs + xr * ((ce - cs) * CK) + (c - cs) * CK + part * (CK / 4);
                 if constexpr (FMT == FMT_INT4) {
                     floatx4 pacc[R];
                     uint32_t zc1024[R], zc64[R];
