@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-headline", action="store_true",
                     help="time only the headline kernel (for profiler runs)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain elementwise copy (torch.neg, 1 GiB in, 1 GiB out) so that "
+                         "FETCH_SIZE / WRITE_SIZE counter readings can be scaled to bytes")
     return ap.parse_args()
 
 
@@ -68,25 +71,29 @@ def main():
         return torch.cuda.Event(enable_timing=True)
 
     def time_steps(fn, steps, warmup):
-        """Whole-job time per step (ms) and average per-launch time (ms) from event pairs."""
+        """Milliseconds per step.  `warmup` eager calls of fn(i), then `steps` calls captured
+        into one HIP graph (fn enqueues on torch's current stream, which is the capture stream
+        during capture), replayed once untimed (graph upload) and once between two events on
+        the capture stream.  The graph keeps Python/ctypes launch cost off the clock, so the
+        time is the GPU's: kernel durations plus the gaps between back-to-back launches."""
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, capture_error_mode="thread_local"):
+            for i in range(steps):
+                fn(i)
+        g.replay()
+        torch.cuda.synchronize()
         s, e = ev(), ev()
         s.record()
-        for i in range(steps):
-            fn(i)
+        g.replay()
         e.record()
         e.synchronize()
-        per_step = s.elapsed_time(e) / steps
-        pairs = [(ev(), ev()) for _ in range(steps)]
-        for i in range(steps):
-            pairs[i][0].record()
-            fn(i)
-            pairs[i][1].record()
         torch.cuda.synchronize()
-        per_launch = sum(a.elapsed_time(b) for a, b in pairs) / steps
-        return per_step, per_launch
+        ms = s.elapsed_time(e) / steps
+        del g
+        return ms
 
     # ---------------------------------------------------------------- block weights ----
     t0 = time.time()
@@ -119,28 +126,38 @@ def main():
         return lambda i: ops.gemv_w4a16_batched(xs, copies[i % len(copies)], ys)
 
     components = {}
-    ms_step, ms_launch = time_steps(gemv_case(1), args.steps, args.warmup)
+    ms_step = time_steps(gemv_case(1), args.steps, args.warmup)
     bytes_m1 = w4_bytes(1)
     value = bytes_m1 / (ms_step * 1e-3) / 1e9
-    achieved = bytes_m1 / (ms_launch * 1e-3) / 1e9
-    log(f"[bench] W4A16 GEMV M=1: {ms_step * 1e3:.1f} us/step, {ms_launch * 1e3:.1f} us/launch, "
-        f"{value:.0f} GB/s (launch-only {achieved:.0f} GB/s)")
+    # one step is one launch, so the average launch duration over the timed region (kernel
+    # plus the inter-launch gap) is ms_step and roofline.achieved equals value
+    achieved = value
+    log(f"[bench] W4A16 GEMV M=1: {ms_step * 1e3:.2f} us/step (one launch), {value:.0f} GB/s")
+
+    if args.copy_calibration:
+        # a copy of known size: 2^28 f32 read + 2^28 f32 written per launch
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        log("[bench] copy calibration: 5 launches of neg over 1 GiB")
+        del src, dst
 
     if not args.only_headline:
         for m in (8, 16):
-            st, la = time_steps(gemv_case(m), max(20, args.steps // 4), 5)
+            st = time_steps(gemv_case(m), max(20, args.steps // 4), 5)
             components[f"w4a16_gemv_m{m}_GBps"] = round(w4_bytes(m) / (st * 1e-3) / 1e9, 1)
             log(f"[bench] W4A16 GEMV M={m}: {st * 1e3:.1f} us/step {components[f'w4a16_gemv_m{m}_GBps']} GB/s")
 
         # quantize over the f32 block (809 MB in, > MALL)
         nel = sum(n * k for (_, n, k) in synth.LLAMA7B_BLOCK)
         nrows = sum(n for (_, n, k) in synth.LLAMA7B_BLOCK)
-        ngroups = sum(n * ((k + 127) // 128) for (_, n, k) in synth.LLAMA7B_BLOCK)
-        st, _ = time_steps(lambda i: [ops.quantize_int4g(w, 128) for w in block_f32], 10, 2)
+        st = time_steps(lambda i: [ops.quantize_int4g(w, 128) for w in block_f32], 10, 2)
         q4_bytes = nel * 4 + nel // 2 + sum(n * (((k + 127) // 128 + 7) // 8) * (16 + 4)
                                             for (_, n, k) in synth.LLAMA7B_BLOCK)
         components["quantize_int4g128_GBps"] = round(q4_bytes / (st * 1e-3) / 1e9, 1)
-        st, _ = time_steps(lambda i: [ops.quantize_int8(w, 8, "channel", "half_even") for w in block_f32], 10, 2)
+        st = time_steps(lambda i: [ops.quantize_int8(w, 8, "channel", "half_even") for w in block_f32], 10, 2)
         components["quantize_int8_channel_GBps"] = round((nel * 5 + nrows * 4) / (st * 1e-3) / 1e9, 1)
         log(f"[bench] quantize int4g {components['quantize_int4g128_GBps']} GB/s, "
             f"int8 {components['quantize_int8_channel_GBps']} GB/s")
@@ -156,7 +173,7 @@ def main():
                 ffi.call("castforge_hip_gemv_w8a16", x.data_ptr(), 1, q.shape[0], q.shape[1], q.data_ptr(),
                          s.data_ptr(), ffi.GRAN_CHANNEL, y.data_ptr(), ffi.DTYPE_BF16,
                          torch.cuda.current_stream().cuda_stream)
-        st, _ = time_steps(w8_step, 50, 5)
+        st = time_steps(w8_step, 50, 5)
         w8_bytes = nel + nrows * 4 + sum(2 * k + 2 * n for (_, n, k) in synth.LLAMA7B_BLOCK)
         components["w8a16_gemv_m1_GBps"] = round(w8_bytes / (st * 1e-3) / 1e9, 1)
         del q8, q8c
@@ -173,7 +190,7 @@ def main():
                 ffi.call("castforge_hip_gemv_nf4", x.data_ptr(), 1, p.n, p.k, p.block, p.codes.data_ptr(),
                          p.absmax.data_ptr(), y.data_ptr(), ffi.DTYPE_BF16,
                          torch.cuda.current_stream().cuda_stream)
-        st, _ = time_steps(nf_step, 50, 5)
+        st = time_steps(nf_step, 50, 5)
         nf_bytes = sum(p.nbytes() + 2 * p.k + 2 * p.n for p in nf)
         components["nf4_gemv_m1_GBps"] = round(nf_bytes / (st * 1e-3) / 1e9, 1)
         log(f"[bench] W8A16 M=1 {components['w8a16_gemv_m1_GBps']} GB/s, NF4 M=1 {components['nf4_gemv_m1_GBps']} GB/s")
@@ -190,11 +207,11 @@ def main():
             qw, sw = ops.quantize_fp8(w)
             qa, sa = ops.quantize_fp8(a16)
             y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-            _, la = time_steps(lambda i: ops.gemm_fp8(qa, sa, qw, sw, y), 30, 3)
+            la = time_steps(lambda i: ops.gemm_fp8(qa, sa, qw, sw, y), 30, 3)
             tag = f"m{m}_n{n}_k{k}"
             components[f"fp8_gemm_{tag}_TFLOPs"] = round(2.0 * m * n * k / (la * 1e-3) / 1e12, 1)
             components[f"fp8_gemm_{tag}_pct_fp8_peak"] = round(100 * 2.0 * m * n * k / (la * 1e-3) / 5.0e15, 1)
-            _, lq = time_steps(lambda i: ops.quantize_fp8(a16), 20, 3)
+            lq = time_steps(lambda i: ops.quantize_fp8(a16), 20, 3)
             components[f"fp8_act_quant_{tag}_GBps"] = round((m * k * 3 + m * 4) / (lq * 1e-3) / 1e9, 1)
             log(f"[bench] FP8 GEMM {tag}: {la * 1e3:.1f} us, {components[f'fp8_gemm_{tag}_TFLOPs']} TFLOP/s; "
                 f"act quant {components[f'fp8_act_quant_{tag}_GBps']} GB/s")
@@ -250,7 +267,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": "skinny_qgemm_kernel<FMT_INT4>", "bytes_per_launch": bytes_m1,
-                     "us_per_launch": round(ms_launch * 1e3, 2)},
+                     "us_per_launch": round(ms_step * 1e3, 2)},
         "cpu_baseline": cpu,
         "components": components,
     }

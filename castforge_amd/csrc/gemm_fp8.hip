@@ -11,6 +11,8 @@
 //   * global -> registers -> LDS double buffer (one barrier per K step), rows padded to 144 B;
 //   * XCD-aware tile order: consecutive tiles run on the same XCD (shared L2), grouped by 8
 //     M-tiles so an XCD reuses the same W columns.
+#include <atomic>
+
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
 
@@ -171,7 +173,8 @@ __global__ void fp8_gemm_generic_kernel(const uint8_t *__restrict__ A, const flo
     else static_cast<float *>(Y)[idx] = v;
 }
 
-bool lds_attr_set = false;
+// devices (bit = device ordinal < 64) on which the kernel's dynamic-LDS limit has been raised
+std::atomic<uint64_t> lds_attr_devices{0};
 
 }  // namespace
 }  // namespace cfh
@@ -191,11 +194,14 @@ extern "C" int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, in
         hipStream_t st = static_cast<hipStream_t>(stream);
         const bool fast = k > 0 && k % BK == 0 && aligned(qa, 16) && aligned(qw, 16);
         if (fast) {
-            if (!lds_attr_set) {
+            int dev = 0;
+            check_hip(hipGetDevice(&dev), "hipGetDevice");
+            const uint64_t bit = dev < 64 ? (uint64_t{1} << dev) : 0;
+            if (bit == 0 || !(lds_attr_devices.load(std::memory_order_acquire) & bit)) {
                 check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(fp8_gemm_kernel),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
                           "hipFuncSetAttribute(fp8_gemm_kernel)");
-                lds_attr_set = true;
+                lds_attr_devices.fetch_or(bit, std::memory_order_acq_rel);
             }
             const int tiles_m = static_cast<int>((m + BM - 1) / BM), tiles_n = static_cast<int>((n + BN - 1) / BN);
             fp8_gemm_kernel<<<dim3(tiles_m * tiles_n), dim3(kThreads), kLdsBytes, st>>>(

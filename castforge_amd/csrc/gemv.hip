@@ -47,7 +47,7 @@ enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2 };
 struct Problem {
     const uint16_t *x;      // bf16 [M, K]
     const void *codes;      // INT4/NF4: u32 [N, K/8]; INT8: i8 [N, K]
-    const void *scales;     // INT4: f16 [N, G]; INT8: f32 [N] or [1]; NF4: f32 [N, K/block]
+    const void *scales;     // INT4: f16 [N, GP] (GP = 8*ceil(G/8)); INT8: f32 [N] or [1]; NF4: f32 [N, K/block]
     const uint32_t *zeros;  // INT4: u32 [N, ceil(G/8)]
     void *y;                // [M, N] f32 or bf16
     int64_t n, k;

@@ -16,7 +16,8 @@
  *
  * Packed formats (new in this library; the reference stores one i8 per element):
  *   INT8  : codes i8 [N, K]; scales f32 [N] (per channel) or [1] (per tensor).
- *   INT4g : codes u32 [N, K/8], element k in bits 4*(k%8); scales f16 bits [N, G];
+ *   INT4g : codes u32 [N, K/8], element k in bits 4*(k%8); scales f16 bits [N, GP] with
+ *           GP = 8*ceil(G/8) (each row padded to a 16-byte multiple, pad slots written 0);
  *           zeros u32 [N, ceil(G/8)], group g in bits 4*(g%8); G = ceil(K/group).
  *           dequant = (q - z) * f32(scale).
  *   NF4   : codes u32 [N, K/8] (same packing); absmax f32 [N, ceil(K/block)].
@@ -131,7 +132,7 @@ int32_t castforge_hip_gemv_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t 
 typedef struct cfh_w4a16_problem_t {
     const uint16_t *x;          /* bf16 [M, k] */
     const uint32_t *codes;      /* u32 [n, k/8] */
-    const uint16_t *scales_f16; /* f16 [n, G] */
+    const uint16_t *scales_f16; /* f16 [n, GP] */
     const uint32_t *zeros;      /* u32 [n, ceil(G/8)] */
     void *y;                    /* [M, n] */
     int64_t n, k, group;
