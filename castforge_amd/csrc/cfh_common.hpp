@@ -10,6 +10,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 #include <cstring>
@@ -73,6 +75,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float v) {
     if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
     u += 0x7fffu + ((u >> 16) & 1u);
     return static_cast<uint16_t>(u >> 16);
+}
+
+// Two f32 -> packed bf16 (low half = a) with round-to-nearest-even: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2_rne(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
@@ -162,6 +171,20 @@ __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
 #pragma unroll
     for (int o = WIDTH / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
     return v;
+}
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory loads are
+// outstanding and ignores the export and LDS/scalar counters.
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Calls f(std::integral_constant<int, I>{}) for I = 0 .. N-1 with I a compile-time constant,
+// so register arrays indexed by I never fall back to scratch memory.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, I + 1>(f);
+    }
 }
 
 }  // namespace cfh

@@ -134,10 +134,6 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
                                              static_cast<int>(bytes), 0x00020000);
 }
 
-// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory loads are
-// outstanding and ignores the export and LDS/scalar counters.
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
 // Loads one INT4 unit issues per row tile: NB code loads, one scale load, one zero-point load.
 template <int NB, int R>
 constexpr int kVmcntAfterUnitInt4() { return vmcnt_imm(R * (NB + 2)); }
