@@ -7,7 +7,8 @@ activations.  Steps rotate over `--copies` distinct copies of the packed block s
 set (16 x 105 MB) exceeds the 256 MB MALL and every step streams from HBM.
 
 Also reported (`components`): quantize GB/s (INT4 g128 and INT8 per-channel over the f32
-block), W4A16 GEMV at M=8/16, W8A16 GEMV at M=1 (config 1) and NF4 GEMV at M=1 (config 3).
+block), W4A16 GEMV at M=8/16, W8A16 GEMV at M=1 (config 1), NF4 GEMV at M=1 and NF4 GEMM at
+M=64/512 (config 3), W4A16 prefill GEMM at M=4096 (config 5) and FP8 W8A8 GEMM (config 4).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -195,6 +196,30 @@ def main():
         components["nf4_gemv_m1_GBps"] = round(nf_bytes / (st * 1e-3) / 1e9, 1)
         log(f"[bench] W8A16 M=1 {components['w8a16_gemv_m1_GBps']} GB/s, NF4 M=1 {components['nf4_gemv_m1_GBps']} GB/s")
         del nf, nfc
+
+        # prefill GEMMs on MFMA: W4A16 INT4 g128 at M=4096 (config 5 follow-on) and NF4 b64 at
+        # M=64 / 512 over W_gate / W_up / W_down (config 3)
+        for (name, n, k) in (synth.LLAMA7B_BLOCK[4], synth.LLAMA7B_BLOCK[6]):
+            m = 4096
+            xp = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+            pp = packed0[4 if name == "w_gate" else 6]
+            yp = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            st = time_steps(lambda i: ops.gemm_w4a16(xp, pp, torch.bfloat16), 10, 2)
+            components[f"w4a16_prefill_m{m}_n{n}_k{k}_TFLOPs"] = round(2.0 * m * n * k / (st * 1e-3) / 1e12, 1)
+            log(f"[bench] W4A16 prefill M={m} {name}: {st * 1e3:.1f} us, "
+                f"{components[f'w4a16_prefill_m{m}_n{n}_k{k}_TFLOPs']} TFLOP/s")
+            del xp, yp
+        nf3 = [ops.quantize_nf4(w, 64) for w in block_f32[4:]]
+        for m in (64, 512):
+            xs3 = [torch.randn((m, p.k), generator=gen, device=dev).to(torch.bfloat16) for p in nf3]
+            st = time_steps(lambda i: [ops.gemm_nf4(x, p, torch.bfloat16) for x, p in zip(xs3, nf3)], 10, 2)
+            fl = sum(2.0 * m * p.n * p.k for p in nf3)
+            by = sum(p.nbytes() + 2 * m * p.k + 2 * m * p.n for p in nf3)
+            components[f"nf4_gemm_m{m}_TFLOPs"] = round(fl / (st * 1e-3) / 1e12, 1)
+            components[f"nf4_gemm_m{m}_GBps"] = round(by / (st * 1e-3) / 1e9, 1)
+            log(f"[bench] NF4 GEMM M={m} (Wg, Wu, Wd): {st * 1e3:.1f} us, "
+                f"{components[f'nf4_gemm_m{m}_TFLOPs']} TFLOP/s, {components[f'nf4_gemm_m{m}_GBps']} GB/s")
+        del nf3
 
         # FP8 E4M3 W8A8 GEMM at M=4096 (config 4): N(0,1) inputs with 0.5% outliers x30
         for (m, n, k) in ((4096, 11008, 4096), (4096, 4096, 11008)):

@@ -1,0 +1,470 @@
+// Prefill (M > 16) dequant-fused GEMM for packed INT4 / INT8 / NF4 weights on gfx950 MFMA.
+//
+// Y[m, n] = sum_k x[m, k] * dequant(W)[n, k]: x bf16 [M, K]; W packed [N, K] (the packed_rhs
+// layout, passes/weights/fold.rs:549-554).  This is the evaluation of `castforge.fused_qmatmul`
+// (codegen/eval.rs:1145-1179 -> eval_matmul_2d, eval.rs:1465-1507) at prefill sizes, where the
+// reference interpreter runs an M*N*K scalar f32 loop on one core.
+//
+// Exactness.  The product must stay within 1e-2 relative / 1e-3 absolute of the f32 evaluator
+// for any row, including near-zero outputs, so the dequantized weight is never rounded to
+// 16 bits.  Every weight w (an f32 value in the evaluator) is carried as an exact f16 pair
+// hi + lo and the tile runs two MFMAs, x * hi and x * lo:
+//   INT4  w = (q - z) * s with s an f16 scale: (q - z) is an exact f16, hi = f16(w) and
+//         lo = w - hi are exact (a 15-bit product split over two 11-bit halves);
+//   NF4   w = f32(T[q] * absmax) as the evaluator rounds it, hi = f16(w), lo = f16(w - hi)
+//         (relative error <= 2^-22);
+//   INT8  w = q * s with one scale per row (or tensor): q is an exact f16 and s multiplies
+//         the f32 accumulator in the epilogue, so one MFMA suffices.
+// Activations are converted bf16 -> f16 (exact for 2^-14 <= |x| < 65504).
+//
+// Design:
+//   * workgroup tile BN (n) x BM (m) with 4 waves; W is the MFMA row operand, so each lane
+//     ends with 4 consecutive n of one m;
+//   * per K slice of 32 the workgroup loads codes / metadata and x into registers, dequantizes
+//     once per workgroup (shared by all BM rows of x) and writes f16 planes to LDS: W hi
+//     [BN][32], W lo [BN][32] (INT4 / NF4) and x [BM][32]; 64-byte rows, 16-byte chunks
+//     XOR-swizzled by row so fragment reads hit distinct banks;
+//   * v_mfma_f32_32x32x16_f16; two LDS stages: while slice t's MFMAs run, slice t+1 is
+//     converted from registers into the other stage and slice t+2's global loads are issued;
+//   * the nibble / byte extraction places codes in a fixed order inside each 16-byte chunk;
+//     x is written to LDS in the same order, so the MFMA's k index matches on both operands;
+//   * XCD-aware tile order (each XCD owns a contiguous range of tiles grouped by m).
+#include "../../include/castforge_hip.h"
+#include "cfh_common.hpp"
+
+namespace cfh {
+namespace {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2 };
+
+constexpr int kThreads = 256;
+constexpr int BK = 32;     // K elements per slice: one 64-byte f16 row per tile row
+constexpr int kXcds = 8;
+constexpr int kGroupM = 4;
+
+__constant__ float kNf4Pf[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+struct PfArgs {
+    const uint16_t *x;      // bf16 [M, K]
+    const void *codes;      // INT4 / NF4: u32 [N, K/8]; INT8: i8 [N, K]
+    const void *scales;     // INT4: f16 [N, GP]; INT8: f32 [N] or [1]; NF4: f32 [N, NB]
+    const uint32_t *zeros;  // INT4: u32 [N, ZW]
+    void *y;                // [M, N] f32 or bf16
+    int M, N, K;
+    int group;              // INT4 group / NF4 block (multiple of 32)
+    int per_row;            // INT8: 1 per-channel scales, 0 per-tensor
+    int y_bf16;
+    int y_vec;              // N % 4 == 0 and y 16-byte aligned: 4 outputs per store
+    int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Physical 16-byte chunk of logical chunk c in a 64-byte tile row r.
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+// Index, within an 8-element k-run, of the element the code extraction puts in f16 slot i.
+template <int FMT>
+__device__ __forceinline__ int perm_src(int i) {
+    if constexpr (FMT == FMT_INT4) return (i >> 1) + ((i & 1) << 2);
+    else if constexpr (FMT == FMT_INT8) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
+    else return i;
+}
+
+// INT4 word (8 codes) -> 4 f16 pairs of exact (q - z), slot order (n0,n4),(n1,n5),(n2,n6),(n3,n7).
+__device__ __forceinline__ void int4_word_qz(uint32_t w, uint32_t z, uint32_t out[4]) {
+    const uint32_t zc1024 = (0xE400u + z) * 0x00010001u;       // -(1024 + z) splatted
+    const uint32_t zc64 = (0xD400u + (z << 4)) * 0x00010001u;  // -(64 + z) splatted
+    const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+    const uint32_t w8 = w >> 8;
+    out[0] = as_u(as_h2((w & 0x000F000Fu) | 0x64006400u) + as_h2(zc1024));
+    out[1] = as_u(as_h2((w & 0x00F000F0u) | 0x64006400u) * sixteenth + as_h2(zc64));
+    out[2] = as_u(as_h2((w8 & 0x000F000Fu) | 0x64006400u) + as_h2(zc1024));
+    out[3] = as_u(as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth + as_h2(zc64));
+}
+
+// INT8 word (4 signed codes) -> 2 f16 pairs of exact q, slot order (b0,b2),(b1,b3).
+__device__ __forceinline__ void int8_word_q(uint32_t w, uint32_t out[2]) {
+    const half2_t c1152 = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+    const uint32_t u = w ^ 0x80808080u;
+    out[0] = as_u(as_h2((u & 0x00FF00FFu) | 0x64006400u) + c1152);
+    out[1] = as_u(as_h2(((u >> 8) & 0x00FF00FFu) | 0x64006400u) + c1152);
+}
+
+// f32 pair -> exact-as-possible f16 hi pair and f16 residual pair (hi + lo == w to 2^-22).
+__device__ __forceinline__ void split_pair(float w0, float w1, uint32_t &hi, uint32_t &lo) {
+    const _Float16 h0 = static_cast<_Float16>(w0), h1 = static_cast<_Float16>(w1);
+    const _Float16 l0 = static_cast<_Float16>(w0 - static_cast<float>(h0));
+    const _Float16 l1 = static_cast<_Float16>(w1 - static_cast<float>(h1));
+    hi = as_u(half2_t{h0, h1});
+    lo = as_u(half2_t{l0, l1});
+}
+
+template <int BM, int BN, int WN>
+struct Cfg {
+    static constexpr int WM = 4 / WN;            // waves along m
+    static constexpr int TN = BN / WN;           // wave tile (n)
+    static constexpr int TM = BM / WM;           // wave tile (m)
+    static constexpr int I = TN / 32, J = TM / 32;
+    static constexpr int kRowBytes = BK * 2;     // 64
+};
+
+// W rows handled per thread per slice: BN / 256 (BN = 256 -> 1 row, BN = 128 -> lanes pair up)
+template <int FMT, int BM, int BN, int WN>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_qgemm_kernel(PfArgs a) {
+    using C = Cfg<BM, BN, WN>;
+    constexpr int P = FMT == FMT_INT8 ? 1 : 2;   // f16 planes of W (hi, lo)
+    constexpr int kWPlane = BN * C::kRowBytes;
+    constexpr int kXPlane = BM * C::kRowBytes;
+    constexpr int kStage = P * kWPlane + kXPlane;
+    // x slice: BM rows x 4 chunks of 16 bytes; W slice: BN rows x (16 B INT4/NF4 | 32 B INT8)
+    constexpr int kXPieces = BM * 4 / kThreads;  // 16-byte x pieces per thread
+    constexpr int kWRowsPerThread = BN >= kThreads ? BN / kThreads : 1;
+    constexpr int kWThreadsPerRow = BN >= kThreads ? 1 : kThreads / BN;  // split a row's bytes
+    constexpr int kWBytesRow = FMT == FMT_INT8 ? 32 : 16;
+    constexpr int kWBytesThread = kWBytesRow / kWThreadsPerRow;  // 16, 8 or 4 (per row)
+    static_assert(kXPieces >= 1 && kWRowsPerThread == 1, "tile / thread mapping");
+    static_assert(kWBytesThread >= 4, "W bytes per thread");
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ uint2 lut[FMT == FMT_NF4 ? 256 : 1];  // NF4: byte -> (T[lo], T[hi]) as f32 bits
+
+    const int M = a.M, N = a.N, K = a.K;
+    // ---- XCD-aware tile order ----
+    const int ntiles = a.tiles_m * a.tiles_n;
+    int pid = blockIdx.x;
+    {
+        const int per_xcd = ntiles / kXcds, full = per_xcd * kXcds;
+        if (pid < full) pid = (pid % kXcds) * per_xcd + pid / kXcds;
+    }
+    const int group_span = kGroupM * a.tiles_n;
+    const int grp = pid / group_span;
+    const int first_m = grp * kGroupM;
+    const int gsize = (a.tiles_m - first_m) < kGroupM ? (a.tiles_m - first_m) : kGroupM;
+    const int tm = first_m + (pid % group_span) % gsize;
+    const int tn = (pid % group_span) / gsize;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    if constexpr (FMT == FMT_NF4) {
+        for (int i = tid; i < 256; i += kThreads)
+            lut[i] = make_uint2(__float_as_uint(kNf4Pf[i & 15]), __float_as_uint(kNf4Pf[i >> 4]));
+    }
+
+    // ---- global sources (descriptors over the tile's rows: rows past M / N read zero) ----
+    const int m_valid = min(BM, M - m0), n_valid = min(BN, N - n0);
+    const rsrc_t rx = make_rsrc(a.x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(m_valid) * K * 2);
+    const int64_t w_row_bytes = FMT == FMT_INT8 ? K : K / 2;
+    const rsrc_t rw = make_rsrc(static_cast<const uint8_t *>(a.codes) + n0 * w_row_bytes,
+                                static_cast<uint32_t>(n_valid * w_row_bytes));
+    const int G = (K + a.group - 1) / a.group;     // INT4 groups / NF4 blocks per row
+    const int ZW = (G + 7) / 8, GP = ZW * 8;
+    rsrc_t rs = make_rsrc(a.codes, 0), rz = rs;  // empty ranges unless the format has metadata
+    if constexpr (FMT == FMT_INT4) {
+        rs = make_rsrc(static_cast<const uint16_t *>(a.scales) + static_cast<int64_t>(n0) * GP,
+                       static_cast<uint32_t>(n_valid) * GP * 2);
+        rz = make_rsrc(a.zeros + static_cast<int64_t>(n0) * ZW, static_cast<uint32_t>(n_valid) * ZW * 4);
+    } else if constexpr (FMT == FMT_NF4) {
+        rs = make_rsrc(static_cast<const float *>(a.scales) + static_cast<int64_t>(n0) * G,
+                       static_cast<uint32_t>(n_valid) * G * 4);
+    }
+
+    // this thread's x pieces: piece p covers row (tid + p * 256) / 4, chunk (tid % 4)
+    // this thread's W part: row wr, bytes [wb, wb + kWBytesThread) of the row's slice
+    const int wr = tid / kWThreadsPerRow;
+    const int wb = (tid % kWThreadsPerRow) * kWBytesThread;
+
+    struct Regs {
+        uint4 x[kXPieces];
+        uint32_t w[kWBytesThread / 4];
+        uint32_t s, z;  // INT4: f16 scale bits, zero word; NF4: absmax bits
+    };
+    auto gload = [&](Regs &r, int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int p = 0; p < kXPieces; ++p) {
+            const int piece = tid + p * kThreads;
+            const int row = piece >> 2, ch = piece & 3;
+            r.x[p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rx, static_cast<uint32_t>(row * K + k0 + ch * 8) * 2, 0, 0));
+        }
+        const uint32_t wo = static_cast<uint32_t>(wr * w_row_bytes + (FMT == FMT_INT8 ? k0 : k0 / 2) + wb);
+        if constexpr (kWBytesThread >= 16) {
+#pragma unroll
+            for (int h = 0; h < kWBytesThread / 16; ++h) {
+                const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 16 * h, 0, 0));
+                r.w[4 * h] = v.x; r.w[4 * h + 1] = v.y; r.w[4 * h + 2] = v.z; r.w[4 * h + 3] = v.w;
+            }
+        } else if constexpr (kWBytesThread == 8) {
+            const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, wo, 0, 0));
+            r.w[0] = v.x; r.w[1] = v.y;
+        } else {
+            r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rw, wo, 0, 0);
+        }
+        // raw metadata words only: decoding them here would wait for the loads
+        const int g = k0 / a.group;
+        if constexpr (FMT == FMT_INT4) {
+            r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<uint32_t>(wr * GP + (g & ~1)) * 2, 0, 0);
+            r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, static_cast<uint32_t>(wr * ZW + (g >> 3)) * 4, 0, 0);
+        } else if constexpr (FMT == FMT_NF4) {
+            r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<uint32_t>(wr * G + g) * 4, 0, 0);
+        }
+    };
+
+    // registers of slice kt -> f16 planes of LDS stage `st`
+    auto lwrite = [&](const Regs &r, int kt, int st) {
+        uint8_t *base = lds + st * kStage;
+        uint8_t *wplane = base;
+        uint8_t *xplane = base + P * kWPlane;
+#pragma unroll
+        for (int p = 0; p < kXPieces; ++p) {
+            const int piece = tid + p * kThreads;
+            const int row = piece >> 2, ch = piece & 3;
+            const uint32_t v[4] = {r.x[p].x, r.x[p].y, r.x[p].z, r.x[p].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int s0 = perm_src<FMT>(2 * q), s1 = perm_src<FMT>(2 * q + 1);
+                const uint16_t b0 = static_cast<uint16_t>(v[s0 >> 1] >> (16 * (s0 & 1)));
+                const uint16_t b1 = static_cast<uint16_t>(v[s1 >> 1] >> (16 * (s1 & 1)));
+                o[q] = as_u(half2_t{static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))});
+            }
+            *reinterpret_cast<uint4 *>(xplane + row * C::kRowBytes + swz(row, ch) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        // W: this thread's bytes cover chunks [c0, c0 + nch) of row wr
+        if constexpr (FMT == FMT_INT4) {
+            // one code word = 8 k = one 16-byte chunk of each plane
+            const int g = kt * BK / a.group;
+            const uint32_t s2 = ((g & 1) ? (r.s >> 16) : (r.s & 0xFFFFu)) * 0x00010001u;
+            const uint32_t z = (r.z >> (4 * (g & 7))) & 15u;
+#pragma unroll
+            for (int t = 0; t < kWBytesThread / 4; ++t) {
+                const int ch = wb / 4 + t;
+                uint32_t qz[4], hi[4], lo[4];
+                int4_word_qz(r.w[t], z, qz);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const half2_t h = as_h2(qz[q]) * as_h2(s2);
+                    hi[q] = as_u(h);
+                    lo[q] = as_u(__builtin_elementwise_fma(as_h2(qz[q]), as_h2(s2), -h));
+                }
+                const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
+                *reinterpret_cast<uint4 *>(wplane + off) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *reinterpret_cast<uint4 *>(wplane + kWPlane + off) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            }
+        } else if constexpr (FMT == FMT_NF4) {
+            const float am = __uint_as_float(r.s);
+#pragma unroll
+            for (int t = 0; t < kWBytesThread / 4; ++t) {
+                const int ch = wb / 4 + t;
+                uint32_t hi[4], lo[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint2 e = lut[(r.w[t] >> (8 * q)) & 255u];
+                    split_pair(__uint_as_float(e.x) * am, __uint_as_float(e.y) * am, hi[q], lo[q]);
+                }
+                const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
+                *reinterpret_cast<uint4 *>(wplane + off) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *reinterpret_cast<uint4 *>(wplane + kWPlane + off) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            }
+        } else {
+            // INT8: two code words = 8 k = one chunk
+#pragma unroll
+            for (int t = 0; t < kWBytesThread / 8; ++t) {
+                const int ch = wb / 8 + t;
+                uint32_t h0[2], h1[2];
+                int8_word_q(r.w[2 * t], h0);
+                int8_word_q(r.w[2 * t + 1], h1);
+                *reinterpret_cast<uint4 *>(wplane + wr * C::kRowBytes + swz(wr, ch) * 16) =
+                    make_uint4(h0[0], h0[1], h1[0], h1[1]);
+            }
+        }
+    };
+
+    // ---- fragments: row lane % 32 of each 32-row sub-tile, chunk 2 kk + lane / 32 ----
+    const int wn = (wave % WN) * C::TN, wm = (wave / WN) * C::TM;
+    const int fr = lane & 31, fh = lane >> 5;
+    floatx16 acc[C::I][C::J];
+#pragma unroll
+    for (int i = 0; i < C::I; ++i)
+#pragma unroll
+        for (int j = 0; j < C::J; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    auto mma_stage = [&](int st) {
+        const uint8_t *base = lds + st * kStage;
+        const uint8_t *wplane = base;
+        const uint8_t *xplane = base + P * kWPlane;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int ch = 2 * kk + fh;
+            half8_t wf[P][C::I], xf[C::J];
+#pragma unroll
+            for (int i = 0; i < C::I; ++i) {
+                const int r = wn + i * 32 + fr;
+#pragma unroll
+                for (int p = 0; p < P; ++p)
+                    wf[p][i] = *reinterpret_cast<const half8_t *>(wplane + p * kWPlane + r * C::kRowBytes + swz(r, ch) * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < C::J; ++j) {
+                const int r = wm + j * 32 + fr;
+                xf[j] = *reinterpret_cast<const half8_t *>(xplane + r * C::kRowBytes + swz(r, ch) * 16);
+            }
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+#pragma unroll
+                for (int i = 0; i < C::I; ++i)
+#pragma unroll
+                    for (int j = 0; j < C::J; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[p][i], xf[j], acc[i][j], 0, 0, 0);
+#ifdef CFH_PF_SB
+            __builtin_amdgcn_sched_barrier(0);
+#endif
+        }
+    };
+
+    const int KT = K / BK;
+    Regs ra, rb;
+    if constexpr (FMT == FMT_NF4) __syncthreads();  // LUT ready
+    gload(ra, 0);
+    if (KT > 1) gload(rb, 1);
+    lwrite(ra, 0, 0);
+    __syncthreads();
+    // Step t: stage t & 1 holds slice t and `nx` holds slice t + 1 (loads issued a step ago);
+    // `fr2` is free.  Issue slice t + 2 into fr2, run slice t's MFMAs, convert slice t + 1 into
+    // the other stage (last read in step t - 1), then barrier.  The barrier is a bare
+    // s_barrier after the LDS writes retire: __syncthreads() would also wait for the global
+    // loads of slice t + 2.  Steady steps are branch-free, so the compiler's vmcnt waits cover
+    // only the loads being consumed.
+    auto step = [&](auto steady, int t, Regs &nx, Regs &fr2) {
+        constexpr bool kSteady = decltype(steady)::value;
+        if (kSteady || t + 2 < KT) gload(fr2, t + 2);
+        mma_stage(t & 1);
+        if (kSteady || t + 1 < KT) lwrite(nx, t + 1, (t + 1) & 1);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));
+        __builtin_amdgcn_s_barrier();
+    };
+    int kt = 0;
+    for (; kt + 3 < KT; kt += 2) {
+        step(std::true_type{}, kt, rb, ra);
+        step(std::true_type{}, kt + 1, ra, rb);
+    }
+    for (; kt < KT; kt += 2) {
+        step(std::false_type{}, kt, rb, ra);
+        if (kt + 1 < KT) step(std::false_type{}, kt + 1, ra, rb);
+    }
+
+    // ---- epilogue: acc[i][j] holds n = wn + 32 i + 8 g + 4 (lane / 32) + q (reg 4 g + q),
+    // m = wm + 32 j + lane % 32 ----
+    float sc[C::I][4][4];  // INT8: scale of each output column (0 past N)
+    if constexpr (FMT == FMT_INT8) {
+        const float *sp = static_cast<const float *>(a.scales);
+#pragma unroll
+        for (int i = 0; i < C::I; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int n = n0 + wn + i * 32 + g * 8 + fh * 4 + q;
+                    sc[i][g][q] = n < N ? sp[a.per_row ? n : 0] : 0.f;
+                }
+    }
+    // a workgroup whose tile lies inside [M, N] with 4-aligned rows stores without checks
+    const bool full = a.y_vec && m0 + BM <= M && n0 + BN <= N;
+    static_for<C::J>([&](auto JJ) {
+        constexpr int j = decltype(JJ)::value;
+        const int m = m0 + wm + j * 32 + fr;
+        static_for<C::I>([&](auto II) {
+            constexpr int i = decltype(II)::value;
+            static_for<4>([&](auto GG) {
+                constexpr int g = decltype(GG)::value;
+                const int n = n0 + wn + i * 32 + g * 8 + fh * 4;
+                float v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[q] = acc[i][j][g * 4 + q];
+                    if constexpr (FMT == FMT_INT8) v[q] *= sc[i][g][q];
+                }
+                const int64_t o = static_cast<int64_t>(m) * N + n;
+                if (full) {
+                    if (a.y_bf16)
+                        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) =
+                            make_uint2(f32x2_to_bf16x2_rne(v[0], v[1]), f32x2_to_bf16x2_rne(v[2], v[3]));
+                    else
+                        *reinterpret_cast<float4 *>(static_cast<float *>(a.y) + o) = make_float4(v[0], v[1], v[2], v[3]);
+                } else if (m < M) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (n + q < N) {
+                            if (a.y_bf16) static_cast<uint16_t *>(a.y)[o + q] = f32_to_bf16_rne(v[q]);
+                            else static_cast<float *>(a.y)[o + q] = v[q];
+                        }
+                    }
+                }
+            });
+        });
+    });
+}
+
+template <int FMT, int BM, int BN, int WN>
+void launch_cfg(PfArgs a, hipStream_t st) {
+    constexpr int P = FMT == FMT_INT8 ? 1 : 2;
+    constexpr int lds = 2 * (P * BN * 64 + BM * 64);
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
+    const int64_t tiles = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
+    require(tiles <= 0x7fffffff, "too many tiles");
+    prefill_qgemm_kernel<FMT, BM, BN, WN><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), lds, st>>>(a);
+    check_launch("prefill_qgemm");
+}
+
+template <int FMT>
+void launch_fmt(const PfArgs &a, hipStream_t st) {
+    // prefer the 256 x 256 tile; smaller m tiles when M is small so workgroups cover the CUs
+    const int64_t t256 = ((a.M + 255) / 256) * static_cast<int64_t>((a.N + 255) / 256);
+    if (a.M > 128 && t256 >= 256) launch_cfg<FMT, 256, 256, 2>(a, st);
+    else if (a.M > 64) launch_cfg<FMT, 128, 256, 2>(a, st);
+    else launch_cfg<FMT, 64, 256, 4>(a, st);
+}
+
+}  // namespace
+
+// Routes one problem to the prefill MFMA kernel when its shape allows it.
+bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
+                 const void *codes, const void *scales, const uint32_t *zeros, int per_row, void *y,
+                 int y_bf16, hipStream_t st) {
+    if (m < 17 || n < 1 || k < BK || k % BK != 0) return false;
+    if (fmt != FMT_INT8 && (group < BK || group % BK != 0)) return false;
+    if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return false;
+    // 32-bit buffer offsets over one tile's rows
+    if (256 * k * 2 >= (int64_t{1} << 31) || 256 * k >= (int64_t{1} << 31)) return false;
+    if (!aligned(x, 16) || !aligned(codes, 16)) return false;
+    PfArgs a{x, codes, scales, zeros, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
+             static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
+    if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
+    else if (fmt == FMT_NF4) launch_fmt<FMT_NF4>(a, st);
+    else launch_fmt<FMT_INT8>(a, st);
+    return true;
+}
+
+}  // namespace cfh

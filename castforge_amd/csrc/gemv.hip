@@ -16,8 +16,10 @@
 //   * v_mfma_f32_16x16x32_f16 with dequantized W rows as B and the activation rows as A; x is
 //     converted once per workgroup from bf16 to f16 in LDS, in the permuted order the nibble
 //     extraction produces, so M = 1..16 costs the same MFMA count;
-//   * 8 chunks (8 KB per wave) are in flight before the x staging starts; problems with the
-//     longest K are dispatched first so no long workgroup forms a tail.
+//   * weight loads are double-buffered per wave in units of NB chunks (the next unit is in
+//     flight while the current one is consumed); the first unit is issued before the x
+//     staging starts; problems with the longest K are dispatched first so no long workgroup
+//     forms a tail.
 #include <algorithm>
 
 #include "../../include/castforge_hip.h"
@@ -39,7 +41,11 @@ constexpr int kMaxProblems = 8;
 #define CFH_GEMV_R_SMALL 1
 #endif
 #ifndef CFH_GEMV_NB_SMALL
-#define CFH_GEMV_NB_SMALL 8
+#define CFH_GEMV_NB_SMALL 4
+#endif
+// cache policy of the streamed weight-code loads (2 = nt: the codes are read once)
+#ifndef CFH_GEMV_CPOL
+#define CFH_GEMV_CPOL 0
 #endif
 
 enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2 };
@@ -134,24 +140,27 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
                                              static_cast<int>(bytes), 0x00020000);
 }
 
-// Loads one INT4 unit issues per row tile: NB code loads, one scale load, one zero-point load.
-template <int NB, int R>
-constexpr int kVmcntAfterUnitInt4() { return vmcnt_imm(R * (NB + 2)); }
+// Loads one unit issues: per row tile NB code loads, plus one scale and one zero-point load
+// (INT4) or one absmax load per chunk (NF4).
+template <int FMT, int NB, int R>
+constexpr int kVmcntAfterUnit() { return vmcnt_imm(R * (NB + (FMT == 0 ? 2 : FMT == 2 ? NB : 0))); }
 
 template <int LW>
 __device__ __forceinline__ void load_words(rsrc_t r, uint32_t off, uint32_t *w) {
     if constexpr (LW == 16) {
-        const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+        const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CFH_GEMV_CPOL));
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     } else if constexpr (LW == 8) {
-        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CFH_GEMV_CPOL));
         w[0] = v.x; w[1] = v.y;
     } else {
-        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+        w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CFH_GEMV_CPOL);
     }
 }
 
-template <int FMT, int LW, int R>
+// ONE: M == 1, so only accumulator slot 0 of the lanes with part == 0 is ever stored and the
+// per-chunk scale is applied to that slot alone.
+template <int FMT, int LW, int R, bool ONE>
 __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     constexpr int WPL = LW / 4;                         // 32-bit code words per lane per chunk
     constexpr int CPB = codes_per_byte<FMT>();
@@ -198,43 +207,54 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
         z_off[r] = row * ZW;
     }
 
-    // A wave works on "units" of NB consecutive chunks.  Raw loaded words only: decoding a
-    // scale or zero point here would make the wave wait for the load before the staging.
+    // A wave works on "units" of NB consecutive chunks, double-buffered in registers: the
+    // next unit's loads are issued before the current unit is consumed.  Raw loaded words
+    // only: decoding a scale or zero point at load time would make the wave wait for it.
     // INT4 (one group per chunk): the unit's NB scales are one aligned NB*2-byte load and its
     // zero points one word, instead of two scattered loads per chunk.
-    uint32_t wq[NB][R][WPL];
-    uint32_t sv[R][NB];  // INT4: f16 scale pairs in [0, NB/2); NF4: f32 absmax bits per chunk
-    uint32_t zv[R];      // INT4: the zero-point word of the unit's 8-group block
+    struct Unit {
+        uint32_t wq[NB][R][WPL];
+        uint32_t sv[R][NB];  // INT4: f16 scale pairs in [0, NB/2); NF4: f32 absmax bits per chunk
+        uint32_t zv[R];      // INT4: the zero-point word of the unit's 8-group block
+    };
+    Unit ua, ub;
 
-    auto load_unit = [&](int c0, int cend) {
+    // Every call issues the same loads (NB code loads per row tile, plus the unit's scale and
+    // zero-point loads for INT4 or one absmax load per chunk for NF4), so the loop below is
+    // straight-line and the compiler's vmcnt waits only cover the unit being consumed.
+    // Chunks at or past `cend` use an offset beyond the descriptor's range: the buffer unit
+    // returns zero for them without touching memory.
+    constexpr uint32_t kOob = 0x80000000u;
+    auto load_unit = [&](Unit &u, int c0, int cend) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const int c = c0 + j;
-            // INT4 always issues NB code loads so the staging wait can count them; a chunk
-            // past the end reads out of the descriptor's range and returns zero
-            if (FMT != FMT_INT4 && c >= cend) break;
+            const bool in = c < cend;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const uint32_t off = c < cend ? code_off[r] + static_cast<uint32_t>(c) * (CK / CPB) : 0x80000000u;
-                load_words<LW>(rc, off, wq[j][r]);
+                load_words<LW>(rc, in ? code_off[r] + static_cast<uint32_t>(c) * (CK / CPB) : kOob, u.wq[j][r]);
                 if constexpr (FMT == FMT_NF4)
-                    sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (sc_off[r] + (static_cast<uint32_t>(c) >> gshift)) * 4, 0, 0);
+                    u.sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(
+                        rs, in ? (sc_off[r] + (static_cast<uint32_t>(c) >> gshift)) * 4 : kOob, 0, 0);
             }
         }
         if constexpr (FMT == FMT_INT4) {
+            // a unit past the end reads metadata it never uses (within or past this tile's rows,
+            // where the descriptor returns zero): 20 bytes per lane, no branch
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const uint32_t so = (sc_off[r] + static_cast<uint32_t>(c0)) * 2;
                 if constexpr (NB == 8) {
                     const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0));
-                    sv[r][0] = v.x; sv[r][1] = v.y; sv[r][2] = v.z; sv[r][3] = v.w;
+                    u.sv[r][0] = v.x; u.sv[r][1] = v.y; u.sv[r][2] = v.z; u.sv[r][3] = v.w;
                 } else if constexpr (NB == 4) {
                     const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
-                    sv[r][0] = v.x; sv[r][1] = v.y;
+                    u.sv[r][0] = v.x; u.sv[r][1] = v.y;
                 } else {
-                    sv[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
+                    static_assert(NB == 2, "INT4 units hold 2, 4 or 8 chunks");
+                    u.sv[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
                 }
-                zv[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, (z_off[r] + (static_cast<uint32_t>(c0) >> 3)) * 4, 0, 0);
+                u.zv[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, (z_off[r] + (static_cast<uint32_t>(c0) >> 3)) * 4, 0, 0);
             }
         }
     };
@@ -285,8 +305,7 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
 
     const int ce0 = cps < nchunks ? cps : nchunks;
     stage_copy(0, ce0);
-    load_unit(wave * NB, ce0);  // the first weight unit is in flight during the staging
-    bool have = true;
+    load_unit(ua, wave * NB, ce0);  // the first weight unit is in flight during the staging
 
     if constexpr (FMT == FMT_NF4) {
         for (int i = tid; i < 256; i += kThreads) {
@@ -300,8 +319,7 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     // Wait for this wave's LDS copies only: they were issued before the weight loads and
     // vmcnt drains in issue order.  A bare s_barrier is used because __syncthreads() carries a
     // release fence that would also wait for the weight loads still in flight.
-    if constexpr (FMT == FMT_INT4) __builtin_amdgcn_s_waitcnt(kVmcntAfterUnitInt4<NB, R>());
-    else __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_waitcnt(kVmcntAfterUnit<FMT, NB, R>());
     __builtin_amdgcn_s_barrier();
     stage_convert(0, ce0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));  // this wave's LDS writes are done
@@ -314,6 +332,81 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const int xr = lr < M ? lr : 0;
     const Int4Consts i4k = int4_consts();
 
+    auto process = [&](const Unit &u, int cb, int cs, int ce) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int c = cb + j;
+            if (c >= ce) break;
+            const _Float16 *xa = xs + xr * ((ce - cs) * CK) + (c - cs) * CK + part * (CK / 4);
+            if constexpr (FMT == FMT_INT4) {
+                floatx4 pacc[R];
+                uint32_t zc1024[R], zc64[R];
+                const uint32_t gsh = 4 * (static_cast<uint32_t>(c) & 7u);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+                    const uint32_t z = (u.zv[r] >> gsh) & 15u;
+                    // f16 bits of -(1024 + z) and -(64 + z), splatted to both halves
+                    zc1024[r] = (0xE400u + z) * 0x00010001u;
+                    zc64[r] = (0xD400u + (z << 4)) * 0x00010001u;
+                }
+#pragma unroll
+                for (int t = 0; t < WPL; ++t) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        uint32_t hb[4];
+                        int4_word_to_h(u.wq[j][r][t], as_h2(zc1024[r]), as_h2(zc64[r]), i4k, hb);
+                        pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(hb[0], hb[1], hb[2], hb[3]),
+                                                                        pacc[r], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                {
+                    const float sc = f16_to_f32(static_cast<uint16_t>(u.sv[r][j >> 1] >> (16 * (j & 1))));
+                    if constexpr (ONE) acc[r][0] += pacc[r][0] * sc;
+                    else acc[r] += pacc[r] * sc;
+                }
+            } else if constexpr (FMT == FMT_NF4) {
+                floatx4 pacc[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < WPL; ++t) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const uint32_t w = u.wq[j][r][t];
+                        const uint2 e0 = lut[w & 255u], e1 = lut[(w >> 8) & 255u];
+                        const uint2 e2 = lut[(w >> 16) & 255u], e3 = lut[w >> 24];
+                        pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.x, e1.x, e2.x, e3.x), pacc[r], 0, 0, 0);
+                        pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.y, e1.y, e2.y, e3.y), pacc[r], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if constexpr (ONE) acc[r][0] += pacc[r][0] * __builtin_bit_cast(float, u.sv[r][j]);
+                    else acc[r] += pacc[r] * __builtin_bit_cast(float, u.sv[r][j]);
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < WPL / 2; ++t) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        uint32_t h0[2], h1[2];
+                        int8_word_to_h(u.wq[j][r][2 * t], h0);
+                        int8_word_to_h(u.wq[j][r][2 * t + 1], h1);
+                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]),
+                                                                       acc[r], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    };
+
+    constexpr int S = kWaves * NB;  // chunks between a wave's consecutive units
     for (int cs = 0; cs < nchunks; cs += cps) {
         const int ce = cs + cps < nchunks ? cs + cps : nchunks;
         if (cs > 0) {
@@ -323,75 +416,15 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
             __syncthreads();
             stage_convert(cs, ce);
             __syncthreads();
+            load_unit(ua, cs + wave * NB, ce);
         }
-
-        for (int cb = cs + wave * NB; cb < ce; cb += kWaves * NB) {
-            if (!have) load_unit(cb, ce);
-            have = false;
-#pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const int c = cb + j;
-                if (c >= ce) break;
-                const _Float16 *xa = xs + xr * ((ce - cs) * CK) + (c - cs) * CK + part * (CK / 4);
-                if constexpr (FMT == FMT_INT4) {
-                    floatx4 pacc[R];
-                    uint32_t zc1024[R], zc64[R];
-                    const uint32_t gsh = 4 * (static_cast<uint32_t>(c) & 7u);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
-                        const uint32_t z = (zv[r] >> gsh) & 15u;
-                        // f16 bits of -(1024 + z) and -(64 + z), splatted to both halves
-                        zc1024[r] = (0xE400u + z) * 0x00010001u;
-                        zc64[r] = (0xD400u + (z << 4)) * 0x00010001u;
-                    }
-#pragma unroll
-                    for (int t = 0; t < WPL; ++t) {
-                        const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
-#pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            uint32_t hb[4];
-                            int4_word_to_h(wq[j][r][t], as_h2(zc1024[r]), as_h2(zc64[r]), i4k, hb);
-                            pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(hb[0], hb[1], hb[2], hb[3]),
-                                                                            pacc[r], 0, 0, 0);
-                        }
-                    }
-#pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        acc[r] += pacc[r] * f16_to_f32(static_cast<uint16_t>(sv[r][j >> 1] >> (16 * (j & 1))));
-                } else if constexpr (FMT == FMT_NF4) {
-                    floatx4 pacc[R];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int t = 0; t < WPL; ++t) {
-                        const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
-#pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            const uint32_t w = wq[j][r][t];
-                            const uint2 e0 = lut[w & 255u], e1 = lut[(w >> 8) & 255u];
-                            const uint2 e2 = lut[(w >> 16) & 255u], e3 = lut[w >> 24];
-                            pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.x, e1.x, e2.x, e3.x), pacc[r], 0, 0, 0);
-                            pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.y, e1.y, e2.y, e3.y), pacc[r], 0, 0, 0);
-                        }
-                    }
-#pragma unroll
-                    for (int r = 0; r < R; ++r) acc[r] += pacc[r] * __builtin_bit_cast(float, sv[r][j]);
-                } else {
-#pragma unroll
-                    for (int t = 0; t < WPL / 2; ++t) {
-                        const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
-#pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            uint32_t h0[2], h1[2];
-                            int8_word_to_h(wq[j][r][2 * t], h0);
-                            int8_word_to_h(wq[j][r][2 * t + 1], h1);
-                            acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]),
-                                                                           acc[r], 0, 0, 0);
-                        }
-                    }
-                }
-            }
+        // ua holds the unit at cb; the unit at cb + S goes into ub before ua is consumed
+        for (int cb = cs + wave * NB; cb < ce; cb += 2 * S) {
+            load_unit(ub, cb + S, ce);
+            process(ua, cb, cs, ce);
+            if (cb + S >= ce) break;
+            load_unit(ua, cb + 2 * S, ce);
+            process(ub, cb + S, cs, ce);
         }
     }
 
@@ -509,8 +542,12 @@ int32_t kc_for(int64_t k, int64_t m, int ck, int nb) {
 
 template <int FMT, int LW, int R>
 void launch_one(const Batch &b, int64_t tiles, int64_t lds, hipStream_t st) {
-    skinny_qgemm_kernel<FMT, LW, R><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
-                                      static_cast<size_t>(lds), st>>>(b);
+    if (R != 4 && b.m == 1)
+        skinny_qgemm_kernel<FMT, LW, R, true><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
+                                                static_cast<size_t>(lds), st>>>(b);
+    else
+        skinny_qgemm_kernel<FMT, LW, R, false><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
+                                                 static_cast<size_t>(lds), st>>>(b);
 }
 
 template <int FMT, int R>
@@ -578,6 +615,11 @@ void common_checks(const void *x, int64_t m, int64_t n, int64_t k, const void *c
 
 }  // namespace
 
+// Prefill MFMA kernel for M > 16 (gemm_prefill.hip); false when the shape does not fit it.
+bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
+                 const void *codes, const void *scales, const uint32_t *zeros, int per_row, void *y,
+                 int y_bf16, hipStream_t st);
+
 // Routes one problem to the skinny MFMA kernel (M <= 16) when its shape allows it.
 bool gemv_try_skinny(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
                      const void *codes, const void *scales, const uint32_t *zeros, int per_row,
@@ -614,7 +656,8 @@ int32_t castforge_hip_gemv_w4a16(const uint16_t *x, int64_t m, int64_t n, int64_
         require(k == 0 || (scales_f16 && zeros), "scales and zeros must not be NULL");
         hipStream_t st = static_cast<hipStream_t>(stream);
         const int yb = y_dtype == CFH_DTYPE_BF16;
-        if (!gemv_try_skinny(FMT_INT4, x, m, n, k, group, codes, scales_f16, zeros, 1, y, yb, st))
+        if (!gemv_try_skinny(FMT_INT4, x, m, n, k, group, codes, scales_f16, zeros, 1, y, yb, st) &&
+            !prefill_try(FMT_INT4, x, m, n, k, group, codes, scales_f16, zeros, 1, y, yb, st))
             gemv_generic(FMT_INT4, x, m, n, k, group, codes, scales_f16, zeros, 1, y, yb, st);
     });
 }
@@ -630,7 +673,8 @@ int32_t castforge_hip_gemv_w8a16(const uint16_t *x, int64_t m, int64_t n, int64_
         require(scales != nullptr, "scales must not be NULL");
         hipStream_t st = static_cast<hipStream_t>(stream);
         const int yb = y_dtype == CFH_DTYPE_BF16, pr = granularity == CFH_GRAN_CHANNEL;
-        if (!gemv_try_skinny(FMT_INT8, x, m, n, k, 0, codes, scales, nullptr, pr, y, yb, st))
+        if (!gemv_try_skinny(FMT_INT8, x, m, n, k, 0, codes, scales, nullptr, pr, y, yb, st) &&
+            !prefill_try(FMT_INT8, x, m, n, k, 0, codes, scales, nullptr, pr, y, yb, st))
             gemv_generic(FMT_INT8, x, m, n, k, 0, codes, scales, nullptr, pr, y, yb, st);
     });
 }
@@ -645,7 +689,8 @@ int32_t castforge_hip_gemv_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t 
         require(k == 0 || absmax, "absmax must not be NULL");
         hipStream_t st = static_cast<hipStream_t>(stream);
         const int yb = y_dtype == CFH_DTYPE_BF16;
-        if (!gemv_try_skinny(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st))
+        if (!gemv_try_skinny(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st) &&
+            !prefill_try(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st))
             gemv_generic(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st);
     });
 }
