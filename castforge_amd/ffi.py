@@ -21,6 +21,8 @@ ROUND_HALF_AWAY, ROUND_HALF_EVEN = 0, 1
 GRAN_TENSOR, GRAN_CHANNEL = 0, 1
 DTYPE_F32, DTYPE_BF16 = 0, 1
 MAX_BATCH = 8
+GROUPWISE_WORKSPACE_BYTES = 2048
+EPI_BIAS, EPI_RELU, EPI_TANH, EPI_SILU, EPI_GELU, EPI_SCALE = range(6)
 
 
 class CastForgeHipError(RuntimeError):
@@ -65,6 +67,14 @@ SIGNATURES = {
     "castforge_hip_gemv_nf4": (c_int32, [_P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_w4a16_batched": (c_int32, [POINTER(W4A16Problem), c_int32, c_int64, c_int32, _P, _E]),
     "castforge_hip_gemm_fp8": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, c_int32, _P, _E]),
+    "castforge_hip_quantize_groupwise": (c_int32, [_P, c_int64, c_int32, c_int64, c_int32, ctypes.c_float, c_int32,
+                                                   _P, _P, _P, POINTER(c_int64), _P, _E]),
+    "castforge_hip_quantize_fp8_grid": (c_int32, [_P, c_int64, c_int32, c_int32, c_int64, _P, _P, _E]),
+    "castforge_hip_qmatmul_epilogue": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, c_int32, _P, _E]),
+    "castforge_hip_convert_f32_to_bf16": (c_int32, [_P, c_int64, _P, _P, _E]),
+    "castforge_hip_convert_bf16_to_f32": (c_int32, [_P, c_int64, _P, _P, _E]),
+    "castforge_hip_transpose": (c_int32, [_P, c_int64, c_int64, c_int32, _P, _P, _E]),
+    "castforge_hip_matmul_f32": (c_int32, [_P, c_int64, c_int64, _P, c_int64, c_int32, _P, _P, _E]),
 }
 
 _lib = None

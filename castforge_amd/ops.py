@@ -4,6 +4,7 @@ streams; every computation happens in libcastforge_hip.so.
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -226,3 +227,102 @@ def gemv_w4a16_batched(xs: list[torch.Tensor], ps: list[Int4Packed], ys: list[to
                                   p.n, p.k, p.group)
     yd = _out_dtype(ys[0].dtype)
     ffi.call("castforge_hip_gemv_w4a16_batched", arr, len(ps), m, yd, _stream(xs[0]))
+
+
+# ------------------------------------------------------- reference write-back quantizers ----
+def quantize_groupwise(w: torch.Tensor, bits: int = 4, group_size: int = 32, awq_salient: bool = True,
+                       salient_ratio: float = 0.01, round: str = "half_away"
+                       ) -> tuple[torch.Tensor, torch.Tensor, int]:
+    """QuantizeGroupwisePass on one tensor (flattened): returns (dequantized f32 of w's shape,
+    group scales f32, salient count)."""
+    w = _dev(w)
+    if w.dtype != torch.float32:
+        raise ValueError("quantize_groupwise takes float32 values")
+    n = w.numel()
+    gs = max(int(group_size), 2)
+    deq = torch.empty_like(w)
+    scales = torch.empty(max(1, (n + gs - 1) // gs), dtype=torch.float32, device=w.device)
+    ws = torch.empty(ffi.GROUPWISE_WORKSPACE_BYTES // 4, dtype=torch.int32, device=w.device)
+    cnt = ctypes.c_int64(0)
+    ffi.call("castforge_hip_quantize_groupwise", _ptr(w), n, bits, gs, 1 if awq_salient else 0,
+             float(salient_ratio), _ROUND[round], _ptr(deq), _ptr(scales), _ptr(ws), ctypes.byref(cnt),
+             _stream(w))
+    return deq, scales[: (n + gs - 1) // gs], int(cnt.value)
+
+
+def quantize_fp8_grid(w: torch.Tensor, fmt: str = "e4m3", mxfp8: bool = True, block_size: int = 32) -> torch.Tensor:
+    """QuantizeFp8Pass on one tensor (flattened): dequantized f32 of w's shape."""
+    w = _dev(w)
+    if w.dtype != torch.float32:
+        raise ValueError("quantize_fp8_grid takes float32 values")
+    deq = torch.empty_like(w)
+    ffi.call("castforge_hip_quantize_fp8_grid", _ptr(w), w.numel(), 1 if fmt.lower() == "e5m2" else 0,
+             1 if mxfp8 else 0, int(block_size), _ptr(deq), _stream(w))
+    return deq
+
+
+# ----------------------------------------------------------- around the fused matmul ----
+_EPI = {"bias": ffi.EPI_BIAS, "relu": ffi.EPI_RELU, "bias_relu": ffi.EPI_RELU, "tanh": ffi.EPI_TANH,
+        "bias_tanh": ffi.EPI_TANH, "silu": ffi.EPI_SILU, "bias_silu": ffi.EPI_SILU, "gelu": ffi.EPI_GELU,
+        "bias_gelu": ffi.EPI_GELU, "bias_scale": ffi.EPI_SCALE}
+
+
+def qmatmul_epilogue(y: torch.Tensor, bias: torch.Tensor, z: torch.Tensor | None = None,
+                     epilogue: str = "bias") -> torch.Tensor:
+    """In place on f32 y: eval.rs:1151-1176 (unknown epilogue names keep val = mm + bias)."""
+    y, bias = _dev(y), _dev(bias)
+    if y.dtype != torch.float32 or bias.dtype != torch.float32:
+        raise ValueError("epilogue runs on float32 y and bias")
+    kind = _EPI.get(epilogue, ffi.EPI_BIAS)
+    zl = 0 if z is None else z.numel()
+    ffi.call("castforge_hip_qmatmul_epilogue", _ptr(y), y.numel(), _ptr(bias), bias.numel(),
+             None if z is None else _ptr(_dev(z)), zl, kind, _stream(y))
+    return y
+
+
+def to_bf16(x: torch.Tensor) -> torch.Tensor:
+    """f32 -> bf16 with round-to-nearest-even, on the GPU."""
+    x = _dev(x)
+    if x.dtype == torch.bfloat16:
+        return x
+    if x.dtype != torch.float32:
+        raise ValueError("to_bf16 takes float32")
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    ffi.call("castforge_hip_convert_f32_to_bf16", _ptr(x), x.numel(), _ptr(out), _stream(x))
+    return out
+
+
+def to_f32(x: torch.Tensor) -> torch.Tensor:
+    x = _dev(x)
+    if x.dtype == torch.float32:
+        return x
+    if x.dtype != torch.bfloat16:
+        raise ValueError("to_f32 takes bfloat16")
+    out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+    ffi.call("castforge_hip_convert_bf16_to_f32", _ptr(x), x.numel(), _ptr(out), _stream(x))
+    return out
+
+
+def transpose2d(x: torch.Tensor) -> torch.Tensor:
+    """[R, C] -> [C, R] for 1-, 2- or 4-byte elements, on the GPU."""
+    x = _dev(x)
+    if x.dim() != 2:
+        raise ValueError("transpose2d takes a 2-D tensor")
+    r, c = x.shape
+    out = torch.empty((c, r), dtype=x.dtype, device=x.device)
+    ffi.call("castforge_hip_transpose", _ptr(x), r, c, x.element_size(), _ptr(out), _stream(x))
+    return out
+
+
+def matmul_f32(a: torch.Tensor, b: torch.Tensor, packed_rhs: bool = False) -> torch.Tensor:
+    """eval_matmul_2d on the GPU (bit-identical order): a [M, K] f32, b [K, N] or packed [N, K]."""
+    a, b = _dev(a), _dev(b)
+    if a.dtype != torch.float32 or b.dtype != torch.float32 or a.dim() != 2 or b.dim() != 2:
+        raise ValueError("matmul_f32 takes 2-D float32 operands")
+    m, k = a.shape
+    n = b.shape[0] if packed_rhs else b.shape[1]
+    if (b.shape[1] if packed_rhs else b.shape[0]) != k:
+        raise ValueError("contracting dimensions differ")
+    out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    ffi.call("castforge_hip_matmul_f32", _ptr(a), m, k, _ptr(b), n, 1 if packed_rhs else 0, _ptr(out), _stream(a))
+    return out

@@ -108,6 +108,30 @@ int32_t castforge_hip_quantize_fp8(const void *src, int32_t src_dtype, int64_t r
 int32_t castforge_hip_dequantize_fp8(const uint8_t *codes, const float *scales, int64_t rows,
                                      int64_t cols, float *out, void *stream, char **out_error);
 
+/* Group-wise symmetric write-back quantizer with AWQ salient protection.  Replaces
+ * QuantizeGroupwisePass::run (passes/quantize/schemes.rs:456-630) on one tensor flattened to n
+ * elements: chunks of max(group_size, 2) consecutive elements; scale = gmax < 1e-12 ? 1 :
+ * gmax / qmax; salient elements (|v| >= the salient_count-th largest |v| in total order, with
+ * salient_count = min(max(ceil(f32(n) * clamp(salient_ratio, 0.001, 0.5)), 1), n)) use half
+ * the scale when awq_salient is set; deq = clamp(round(v / eff), qmin, qmax) * eff.
+ * Writes deq (f32 [n]), the group scales (f32 [ceil(n / group)], may be NULL) and, when
+ * salient_count_out is not NULL, the salient count (a host pointer).  The threshold search
+ * needs a device workspace of CFH_GROUPWISE_WORKSPACE_BYTES (unused when awq_salient = 0). */
+#define CFH_GROUPWISE_WORKSPACE_BYTES 2048
+int32_t castforge_hip_quantize_groupwise(const float *src, int64_t n, int32_t bits, int64_t group_size,
+                                         int32_t awq_salient, float salient_ratio, int32_t round_mode,
+                                         float *deq, float *scales, void *workspace,
+                                         int64_t *salient_count_out, void *stream, char **out_error);
+
+/* FP8 / MXFP8 uniform-grid write-back quantizer.  Replaces QuantizeFp8Pass::run
+ * (passes/quantize/schemes.rs:633-754): blocks of max(block_size, 4) consecutive elements;
+ * raw = amax < 1e-12 ? 1 : amax / fp8_max (448 E4M3, 57344 E5M2); scale = mxfp8 ?
+ * powf(2, ceilf(log2f(raw))) (glibc's rounding of log2f reproduced exactly) : raw;
+ * deq = round(clamp(v / scale, -max, max) / step) * step * scale with step = max / 31 (E4M3)
+ * or max / 15 (E5M2), round half away from zero. */
+int32_t castforge_hip_quantize_fp8_grid(const float *src, int64_t n, int32_t e5m2, int32_t mxfp8,
+                                        int64_t block_size, float *deq, void *stream, char **out_error);
+
 /* ---- dequant-fused matmul ----------------------------------------------------------------- */
 /* y[m, n] = sum_k x[m, k] * dequant(W)[n, k]; x bf16 [M, K]; y f32 or bf16 [M, N].
  * Replaces the evaluation of `castforge.fused_qmatmul` (passes/fuse/epilogue.rs:10-94,
@@ -152,6 +176,39 @@ int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, in
 int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *qw,
                                const float *sw, int64_t n, int64_t k, void *y, int32_t y_dtype,
                                void *stream, char **out_error);
+
+/* ---- steps either side of the fused matmul ------------------------------------------------- */
+
+/* Epilogue of `castforge.fused_qmatmul` (codegen/eval.rs:1151-1176), in place on f32 y[count]:
+ * val = y[i] + bias[i % bias_len]; RELU: max(val, z[i % z_len]); TANH: tanh(val); SILU:
+ * val / (1 + exp(-val)); GELU: the tanh form of eval.rs:1733-1735; SCALE: val * z[i % z_len];
+ * BIAS: val.  z_len == 0 means z = 0 (the evaluator's default). */
+enum { CFH_EPI_BIAS = 0, CFH_EPI_RELU = 1, CFH_EPI_TANH = 2, CFH_EPI_SILU = 3, CFH_EPI_GELU = 4,
+       CFH_EPI_SCALE = 5 };
+int32_t castforge_hip_qmatmul_epilogue(float *y, int64_t count, const float *bias, int64_t bias_len,
+                                       const float *z, int64_t z_len, int32_t kind, void *stream,
+                                       char **out_error);
+
+/* f32 -> bf16 with round-to-nearest-even (NaN stays NaN): the bf16 activations the fused
+ * matmul consumes after `lower-mixed-precision` (passes/quantize/formats.rs:563-591).  The
+ * reference's evaluator treats that convert as a copy (codegen/eval.rs:674-676); here the
+ * operand really is bf16. */
+int32_t castforge_hip_convert_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, void *stream,
+                                          char **out_error);
+int32_t castforge_hip_convert_bf16_to_f32(const uint16_t *src, int64_t n, float *dst, void *stream,
+                                          char **out_error);
+
+/* dst[c, r] = src[r, c] for [rows, cols] elements of elem_bytes (1, 2 or 4): the [K, N] ->
+ * [N, K] transpose of PackWeightsPass (passes/weights/fold.rs:549-554). */
+int32_t castforge_hip_transpose(const void *src, int64_t rows, int64_t cols, int32_t elem_bytes, void *dst,
+                                void *stream, char **out_error);
+
+/* out[m, n] = sum_k a[m, k] * b[k, n] (or b[n, k] when packed_rhs), f32 operands, k ascending
+ * with separate multiply and add per output: bit-identical to eval_matmul_2d
+ * (codegen/eval.rs:1465-1507).  The evaluator's unfused dot_general; the quantized hot path
+ * is castforge_hip_gemv_* / castforge_hip_gemm_fp8. */
+int32_t castforge_hip_matmul_f32(const float *a, int64_t m, int64_t k, const float *b, int64_t n,
+                                 int32_t packed_rhs, float *out, void *stream, char **out_error);
 
 #ifdef __cplusplus
 }

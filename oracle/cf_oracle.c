@@ -325,6 +325,43 @@ void orc_quantize_fp8_grid(const float *v, int64_t n, int e5m2, int mxfp8, int64
     }
 }
 
+/* Closed form of ceilf(log2f(raw)) for a positive normal f32, the MX exponent of
+ * schemes.rs:706: e for raw = 2^e, else e + 1 unless log2f's f32 rounding lands exactly on e,
+ * which happens for raw = 2^e (1 + m 2^-23) with m below (2^h - 1) 2^23, h the half-spacing
+ * of f32 values next to e (below |e| when e < 0).  The GPU kernel computes the exponent this
+ * way; orc_mx_scale_crosscheck compares it with glibc's log2f. */
+int orc_mx_scale_exp_model(float raw) {
+    uint32_t b = f2u(raw);
+    int e = (int)((b >> 23) & 0xffu) - 127;
+    uint32_t m = b & 0x7fffffu;
+    if (m == 0) return e;
+    if (e == 0) return 1;
+    int a = e > 0 ? e : -e;
+    int fl = 31 - __builtin_clz((unsigned)a);
+    double h = (e < 0 && (a & (a - 1)) == 0) ? ldexp(1.0, fl - 25) : ldexp(1.0, fl - 24);
+    double thr = (exp2(h) - 1.0) * 8388608.0;
+    return (double)m < thr ? e : e + 1;
+}
+
+/* Counts f32 bit patterns x in [lo, hi) (positive normals) where ceilf(log2f(x)) differs from
+ * the closed form. */
+int64_t orc_mx_scale_crosscheck(uint32_t lo, uint32_t hi, uint32_t *first_bad) {
+    int64_t bad = 0;
+    uint64_t first = UINT64_MAX;
+    int64_t count = (int64_t)hi - (int64_t)lo;
+#pragma omp parallel for reduction(+ : bad) reduction(min : first) schedule(static)
+    for (int64_t i = 0; i < count; ++i) {
+        uint32_t x = lo + (uint32_t)i;
+        float f = u2f(x);
+        if ((int)ceilf(log2f(f)) != orc_mx_scale_exp_model(f)) {
+            bad++;
+            if (x < first) first = x;
+        }
+    }
+    if (first_bad) *first_bad = bad ? (uint32_t)first : 0;
+    return bad;
+}
+
 /* ======================= BASELINE schemes (written spec) ================================ */
 
 /* Per-output-channel symmetric: formats.rs:670-677 applied to every row of [n, k]. */

@@ -111,6 +111,10 @@ void orc_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *
 /* timing helper for the CPU baseline: quantize_int4g + gemv over a row slice */
 double orc_now_seconds(void);
 
+/* closed form of the MX scale exponent ceilf(log2f(raw)) (schemes.rs:706) and its check */
+int orc_mx_scale_exp_model(float raw);
+int64_t orc_mx_scale_crosscheck(uint32_t lo, uint32_t hi, uint32_t *first_bad);
+
 #ifdef __cplusplus
 }
 #endif

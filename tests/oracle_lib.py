@@ -56,6 +56,8 @@ def lib() -> ctypes.CDLL:
             "orc_gemm_nf4": (None, [P, I64, I64, I64, I64, P, P, P]),
             "orc_gemm_fp8": (None, [P, P, I64, P, P, I64, I64, P]),
             "orc_now_seconds": (ctypes.c_double, []),
+            "orc_mx_scale_exp_model": (c_int, [c_float]),
+            "orc_mx_scale_crosscheck": (I64, [c_uint32, c_uint32, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(l, name)

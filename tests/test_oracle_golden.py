@@ -358,3 +358,21 @@ def test_epilogues():
         o = out.copy()
         O.lib().orc_epilogue(O._p(o), 3, O._p(bias), 1, None, 0, mode)
         np.testing.assert_allclose(o, fn(out + 0.5), rtol=1e-6)
+
+
+def test_mx_scale_exponent_closed_form_matches_glibc_log2f():
+    """The MX scale exponent ceilf(log2f(amax / max)) (schemes.rs:706), computed by the GPU
+    kernel in closed form, equals glibc's ceilf(log2f(x)) for every positive normal f32 x
+    (2^31 inputs); 3676 of them sit just above a power of two where log2f rounds to the
+    integer and the reference keeps the smaller scale."""
+    import ctypes
+
+    first = ctypes.c_uint32(0)
+    bad = O.lib().orc_mx_scale_crosscheck(0x00800000, 0x7F800000, ctypes.byref(first))
+    assert bad == 0, f"first mismatch at bits {first.value:#010x}"
+    quirks = 0
+    for e in range(-126, 128):
+        for m in range(1, 64):
+            x = np.array([(e + 127) << 23 | m], np.uint32).view(np.float32)[0]
+            quirks += O.lib().orc_mx_scale_exp_model(float(x)) == e
+    assert quirks == 3676
