@@ -8,7 +8,9 @@ set (16 x 105 MB) exceeds the 256 MB MALL and every step streams from HBM.
 
 Also reported (`components`): quantize GB/s (INT4 g128 and INT8 per-channel over the f32
 block), W4A16 GEMV at M=8/16, W8A16 GEMV at M=1 (config 1), NF4 GEMV at M=1 and NF4 GEMM at
-M=64/512 (config 3), W4A16 prefill GEMM at M=4096 (config 5) and FP8 W8A8 GEMM (config 4).
+M=64/512 (config 3), W4A16 prefill GEMM at M=4096 (config 5), FP8 W8A8 GEMM (config 4), and
+the 32-layer AWQ-style INT4 model (config 5): quantize, decode GEMV and prefill GEMM over all
+layers.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -39,12 +41,104 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-model", action="store_true",
+                    help="skip the 32-layer (25.9 GB f32) AWQ quantize / decode / prefill components")
     ap.add_argument("--only-headline", action="store_true",
                     help="time only the headline kernel (for profiler runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain elementwise copy (torch.neg, 1 GiB in, 1 GiB out) so that "
                          "FETCH_SIZE / WRITE_SIZE counter readings can be scaled to bytes")
     return ap.parse_args()
+
+
+def model_32_layers(args, dev, gen, torch, synth, ops, log, time_steps, ev):
+    """BASELINE config 5 over all 32 layers; returns the component figures."""
+    out = {}
+    layers = 32
+    t0 = time.time()
+    f32_layers, scales = [], []
+    for li in range(layers):
+        ws = []
+        for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK):
+            ws.append(torch.randn((n, k), generator=gen, device=dev, dtype=torch.float32) * 0.02)
+        f32_layers.append(ws)
+        scales.append([torch.from_numpy(synth.awq_channel_scales(0, 1000 + li * 7 + tid, k)).to(dev)
+                       for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)])
+    torch.cuda.synchronize()
+    log(f"[bench] 32-layer f32 weight set generated in {time.time() - t0:.1f}s")
+
+    packed = [[None] * 7 for _ in range(layers)]
+
+    def quantize_all():
+        for li in range(layers):
+            for j in range(7):
+                packed[li][j] = ops.quantize_int4g(f32_layers[li][j], 128, scales[li][j])
+
+    quantize_all()  # warm-up (and the packed set the GEMMs below use)
+    torch.cuda.synchronize()
+    s, e = ev(), ev()
+    s.record()
+    quantize_all()
+    e.record()
+    e.synchronize()
+    ms_q = s.elapsed_time(e)
+    q_bytes = 0
+    for (_, n, k) in synth.LLAMA7B_BLOCK:
+        g = (k + 127) // 128
+        q_bytes += n * k * 4 + k * 4 + n * k // 2 + n * ((g + 7) // 8 * 8) * 2 + n * ((g + 7) // 8) * 4
+    q_bytes *= layers
+    out["model32_awq_int4g128_quantize_GBps"] = round(q_bytes / (ms_q * 1e-3) / 1e9, 1)
+    out["model32_awq_int4g128_quantize_ms"] = round(ms_q, 3)
+    log(f"[bench] 32-layer AWQ INT4 quantize: {ms_q:.2f} ms, {out['model32_awq_int4g128_quantize_GBps']} GB/s")
+    del f32_layers
+    torch.cuda.empty_cache()
+
+    # decode: one batched 7-projection launch per layer, 32 launches in one graph
+    xs1 = {k: torch.randn((1, k), generator=gen, device=dev).to(torch.bfloat16) for k in (4096, 11008)}
+    ys1 = [torch.empty((1, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
+
+    def decode(i):
+        for li in range(layers):
+            ops.gemv_w4a16_batched([xs1[k] for (_, n, k) in synth.LLAMA7B_BLOCK], packed[li], ys1)
+
+    ms_d = time_steps(decode, 5, 2)
+    d_bytes = 0
+    for (_, n, k) in synth.LLAMA7B_BLOCK:
+        g = (k + 127) // 128
+        d_bytes += n * k // 2 + n * ((g + 7) // 8 * 8) * 2 + n * ((g + 7) // 8) * 4 + 2 * k + 2 * n
+    d_bytes *= layers
+    out["model32_decode_m1_GBps"] = round(d_bytes / (ms_d * 1e-3) / 1e9, 1)
+    out["model32_decode_m1_ms"] = round(ms_d, 4)
+    log(f"[bench] 32-layer decode M=1: {ms_d * 1e3:.1f} us, {out['model32_decode_m1_GBps']} GB/s")
+
+    # prefill M=4096 over every projection of every layer
+    m = 4096
+    xs = {k: torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16) for k in (4096, 11008)}
+    ys = {n: torch.empty((m, n), dtype=torch.bfloat16, device=dev) for n in (4096, 11008)}
+
+    def prefill():
+        for li in range(layers):
+            for j, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK):
+                p = packed[li][j]
+                ops.ffi.call("castforge_hip_gemv_w4a16", xs[k].data_ptr(), m, n, k, 128, p.codes.data_ptr(),
+                             p.scales.data_ptr(), p.zeros.data_ptr(), ys[n].data_ptr(), ops.ffi.DTYPE_BF16,
+                             torch.cuda.current_stream().cuda_stream)
+
+    prefill()
+    torch.cuda.synchronize()
+    s, e = ev(), ev()
+    s.record()
+    prefill()
+    e.record()
+    e.synchronize()
+    ms_p = s.elapsed_time(e)
+    flops = 2.0 * m * sum(n * k for (_, n, k) in synth.LLAMA7B_BLOCK) * layers
+    out["model32_prefill_m4096_TFLOPs"] = round(flops / (ms_p * 1e-3) / 1e12, 1)
+    out["model32_prefill_m4096_ms"] = round(ms_p, 2)
+    log(f"[bench] 32-layer prefill M=4096: {ms_p:.1f} ms, {out['model32_prefill_m4096_TFLOPs']} TFLOP/s")
+    del packed, xs, ys
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -220,6 +314,13 @@ def main():
             log(f"[bench] NF4 GEMM M={m} (Wg, Wu, Wd): {st * 1e3:.1f} us, "
                 f"{components[f'nf4_gemm_m{m}_TFLOPs']} TFLOP/s, {components[f'nf4_gemm_m{m}_GBps']} GB/s")
         del nf3
+
+        # Config 5: a 32-layer LLaMA-7B-shaped f32 weight set (6.476 B linear params, 25.9 GB),
+        # quantized end to end INT4 g128 with the AWQ-style per-input-channel pre-scale
+        # s = a^0.5 fused into the quantize pass; then a W4A16 decode GEMV (M = 1) and a prefill
+        # GEMM (M = 4096) over every layer.  3.4 GB of packed weights: no cache holds them.
+        if not args.skip_model:
+            components.update(model_32_layers(args, dev, gen, torch, synth, ops, log, time_steps, ev))
 
         # FP8 E4M3 W8A8 GEMM at M=4096 (config 4): N(0,1) inputs with 0.5% outliers x30
         for (m, n, k) in ((4096, 11008, 4096), (4096, 4096, 11008)):

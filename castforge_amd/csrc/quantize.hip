@@ -230,8 +230,11 @@ __device__ __forceinline__ uint16_t int4_scale_bits(float mx, float mn) {
     return h;
 }
 
+// in_scale (optional, f32 [cols]): AWQ-style per-input-channel pre-scale, w' = f32(w * s[k])
+// is what gets quantized (one rounding, as the oracle computes it).
 template <int GROUP>
 __global__ __launch_bounds__(kBlock) void int4g_quant_kernel(const float *__restrict__ src,
+                                                             const float *__restrict__ in_scale,
                                                              int64_t rows, int64_t cols,
                                                              uint32_t *__restrict__ codes,
                                                              uint16_t *__restrict__ scales,
@@ -254,6 +257,12 @@ __global__ __launch_bounds__(kBlock) void int4g_quant_kernel(const float *__rest
         float4 a = p[0], b = p[1];
         x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
         x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+        if (in_scale) {
+            const float4 *q = reinterpret_cast<const float4 *>(in_scale + w * 8);
+            const float4 c = q[0], d = q[1];
+            x[0] *= c.x; x[1] *= c.y; x[2] *= c.z; x[3] *= c.w;
+            x[4] *= d.x; x[5] *= d.y; x[6] *= d.z; x[7] *= d.w;
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, x[i]); mn = fminf(mn, x[i]); }
     }
@@ -487,33 +496,56 @@ int32_t castforge_hip_dequantize_int8(const int8_t *codes, const float *scales, 
     });
 }
 
+}  // extern "C"
+
+namespace cfh {
+namespace {
+void quantize_int4g_impl(const float *src, const float *in_scale, int64_t rows, int64_t cols, int64_t group,
+                         uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros, void *stream) {
+    check_shape(rows, cols);
+    require(pow2_in(group, 8, 256), "group must be a power of two in [8, 256]");
+    require(cols % 8 == 0, "cols must be a multiple of 8 (8 codes per 32-bit word)");
+    if (rows == 0 || cols == 0) return;
+    require(src && codes && scales_f16 && zeros, "buffers must not be NULL");
+    require(aligned(src, 16), "src must be 16-byte aligned");
+    require(!in_scale || aligned(in_scale, 16), "in_scale must be 16-byte aligned");
+    require(aligned(codes, 4) && aligned(scales_f16, 2) && aligned(zeros, 4),
+            "codes/zeros must be 4-byte and scales 2-byte aligned");
+    const int64_t G = (cols + group - 1) / group, ZW = (G + 7) / 8;
+    const int64_t tasks = rows * ZW, tpb = kBlock / group;
+    const int64_t blocks = (tasks + tpb - 1) / tpb;
+    require(blocks <= 0x7fffffff, "tensor too large for one launch");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    dim3 g(static_cast<unsigned>(blocks)), b(kBlock);
+    switch (group) {
+    case 8: int4g_quant_kernel<8><<<g, b, 0, st>>>(src, in_scale, rows, cols, codes, scales_f16, zeros); break;
+    case 16: int4g_quant_kernel<16><<<g, b, 0, st>>>(src, in_scale, rows, cols, codes, scales_f16, zeros); break;
+    case 32: int4g_quant_kernel<32><<<g, b, 0, st>>>(src, in_scale, rows, cols, codes, scales_f16, zeros); break;
+    case 64: int4g_quant_kernel<64><<<g, b, 0, st>>>(src, in_scale, rows, cols, codes, scales_f16, zeros); break;
+    case 128: int4g_quant_kernel<128><<<g, b, 0, st>>>(src, in_scale, rows, cols, codes, scales_f16, zeros); break;
+    default: int4g_quant_kernel<256><<<g, b, 0, st>>>(src, in_scale, rows, cols, codes, scales_f16, zeros); break;
+    }
+    check_launch("int4g_quant");
+}
+}  // namespace
+}  // namespace cfh
+
+extern "C" {
+
 int32_t castforge_hip_quantize_int4g(const float *src, int64_t rows, int64_t cols, int64_t group,
                                      uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros,
                                      void *stream, char **out_error) {
     return guarded(out_error, [&] {
-        check_shape(rows, cols);
-        require(pow2_in(group, 8, 256), "group must be a power of two in [8, 256]");
-        require(cols % 8 == 0, "cols must be a multiple of 8 (8 codes per 32-bit word)");
-        if (rows == 0 || cols == 0) return;
-        require(src && codes && scales_f16 && zeros, "buffers must not be NULL");
-        require(aligned(src, 16), "src must be 16-byte aligned");
-        require(aligned(codes, 4) && aligned(scales_f16, 2) && aligned(zeros, 4),
-                "codes/zeros must be 4-byte and scales 2-byte aligned");
-        const int64_t G = (cols + group - 1) / group, ZW = (G + 7) / 8;
-        const int64_t tasks = rows * ZW, tpb = kBlock / group;
-        const int64_t blocks = (tasks + tpb - 1) / tpb;
-        require(blocks <= 0x7fffffff, "tensor too large for one launch");
-        hipStream_t st = static_cast<hipStream_t>(stream);
-        dim3 g(static_cast<unsigned>(blocks)), b(kBlock);
-        switch (group) {
-        case 8: int4g_quant_kernel<8><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
-        case 16: int4g_quant_kernel<16><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
-        case 32: int4g_quant_kernel<32><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
-        case 64: int4g_quant_kernel<64><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
-        case 128: int4g_quant_kernel<128><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
-        default: int4g_quant_kernel<256><<<g, b, 0, st>>>(src, rows, cols, codes, scales_f16, zeros); break;
-        }
-        check_launch("int4g_quant");
+        quantize_int4g_impl(src, nullptr, rows, cols, group, codes, scales_f16, zeros, stream);
+    });
+}
+
+int32_t castforge_hip_quantize_int4g_awq(const float *src, const float *in_scale, int64_t rows, int64_t cols,
+                                         int64_t group, uint32_t *codes, uint16_t *scales_f16,
+                                         uint32_t *zeros, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(rows == 0 || cols == 0 || in_scale != nullptr, "in_scale must not be NULL");
+        quantize_int4g_impl(src, in_scale, rows, cols, group, codes, scales_f16, zeros, stream);
     });
 }
 

@@ -57,6 +57,7 @@ SIGNATURES = {
     "castforge_hip_quantize_int8": (c_int32, [_P, c_int64, c_int64, c_int32, c_int32, c_int32, _P, _P, _P, _E]),
     "castforge_hip_dequantize_int8": (c_int32, [_P, _P, c_int64, c_int64, c_int32, _P, _P, _E]),
     "castforge_hip_quantize_int4g": (c_int32, [_P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _E]),
+    "castforge_hip_quantize_int4g_awq": (c_int32, [_P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _E]),
     "castforge_hip_dequantize_int4g": (c_int32, [_P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _E]),
     "castforge_hip_quantize_nf4": (c_int32, [_P, c_int64, c_int64, c_int64, _P, _P, _P, _E]),
     "castforge_hip_dequantize_nf4": (c_int32, [_P, _P, c_int64, c_int64, c_int64, _P, _P, _E]),

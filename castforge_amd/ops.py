@@ -83,7 +83,9 @@ class Int4Packed:
         return sum(t.numel() * t.element_size() for t in (self.codes, self.scales, self.zeros))
 
 
-def quantize_int4g(w: torch.Tensor, group: int = 128) -> Int4Packed:
+def quantize_int4g(w: torch.Tensor, group: int = 128, in_scale: torch.Tensor | None = None) -> Int4Packed:
+    """INT4 asymmetric group-wise; with `in_scale` (f32 [K]) the AWQ-style pre-scaled
+    W * in_scale[k] is quantized (fused, one pass)."""
     w = _dev(w)
     if w.dtype != torch.float32 or w.dim() != 2:
         raise ValueError("quantize_int4g takes a 2-D float32 [N, K] weight")
@@ -92,8 +94,15 @@ def quantize_int4g(w: torch.Tensor, group: int = 128) -> Int4Packed:
     codes = torch.empty((n, k // 8), dtype=torch.int32, device=w.device)
     scales = torch.empty((n, (g + 7) // 8 * 8), dtype=torch.float16, device=w.device)
     zeros = torch.empty((n, (g + 7) // 8), dtype=torch.int32, device=w.device)
-    ffi.call("castforge_hip_quantize_int4g", _ptr(w), n, k, group, _ptr(codes), _ptr(scales),
-             _ptr(zeros), _stream(w))
+    if in_scale is None:
+        ffi.call("castforge_hip_quantize_int4g", _ptr(w), n, k, group, _ptr(codes), _ptr(scales),
+                 _ptr(zeros), _stream(w))
+    else:
+        in_scale = _dev(in_scale)
+        if in_scale.dtype != torch.float32 or in_scale.numel() != k:
+            raise ValueError("in_scale must be float32 [K]")
+        ffi.call("castforge_hip_quantize_int4g_awq", _ptr(w), _ptr(in_scale), n, k, group, _ptr(codes),
+                 _ptr(scales), _ptr(zeros), _stream(w))
     return Int4Packed(codes, scales, zeros, n, k, group)
 
 

@@ -58,3 +58,10 @@ def fp8_inputs(seed: int, tensor_id: int, rows: int, cols: int, outlier_frac: fl
         idx = g.choice(x.size, size=n_out, replace=False)
         x.reshape(-1)[idx] *= np.float32(outlier_scale)
     return x
+
+
+def awq_channel_scales(seed: int, tensor_id: int, k: int) -> np.ndarray:
+    """s = a^0.5 per input channel with a ~ LogNormal(0, 1), computed on the
+    host in f64 and rounded once to f32 (the device never recomputes the transcendental)."""
+    a = rng(seed, tensor_id).lognormal(0.0, 1.0, size=k)
+    return np.sqrt(a).astype(np.float32)

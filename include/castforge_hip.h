@@ -83,6 +83,14 @@ int32_t castforge_hip_quantize_int4g(const float *src, int64_t rows, int64_t col
                                      uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros,
                                      void *stream, char **out_error);
 
+/* castforge_hip_quantize_int4g of the AWQ-style pre-scaled weight W'[n, k] = f32(W[n, k] *
+ * in_scale[k]) (s = a^0.5 per input channel), fused into the same pass so
+ * W' is never written.  in_scale: device f32 [cols], 16-byte aligned.  New; no reference
+ * counterpart (the reference's "AWQ" is the salient halving of quantize-groupwise). */
+int32_t castforge_hip_quantize_int4g_awq(const float *src, const float *in_scale, int64_t rows, int64_t cols,
+                                         int64_t group, uint32_t *codes, uint16_t *scales_f16,
+                                         uint32_t *zeros, void *stream, char **out_error);
+
 int32_t castforge_hip_dequantize_int4g(const uint32_t *codes, const uint16_t *scales_f16,
                                        const uint32_t *zeros, int64_t rows, int64_t cols,
                                        int64_t group, float *out, void *stream, char **out_error);

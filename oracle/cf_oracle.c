@@ -419,6 +419,16 @@ void orc_quantize_int4g(const float *v, int64_t n, int64_t k, int64_t group, uin
     }
 }
 
+/* AWQ-style pre-scale: quantize W'[r][c] = f32(W[r][c] * s[c]). */
+void orc_quantize_int4g_awq(const float *v, const float *s, int64_t n, int64_t k, int64_t group,
+                            uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros) {
+    float *t = (float *)malloc(sizeof(float) * (size_t)(n * k > 0 ? n * k : 1));
+    for (int64_t r = 0; r < n; ++r)
+        for (int64_t c = 0; c < k; ++c) t[r * k + c] = v[r * k + c] * s[c];
+    orc_quantize_int4g(t, n, k, group, codes, scales_f16, zeros);
+    free(t);
+}
+
 void orc_dequantize_int4g(const uint32_t *codes, const uint16_t *scales_f16,
                           const uint32_t *zeros, int64_t n, int64_t k, int64_t group, float *out) {
     int64_t G = (k + group - 1) / group, ZW = (G + 7) / 8, GP = ZW * 8, KW = k / 8;

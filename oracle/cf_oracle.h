@@ -111,6 +111,8 @@ void orc_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *
 /* timing helper for the CPU baseline: quantize_int4g + gemv over a row slice */
 double orc_now_seconds(void);
 
+void orc_quantize_int4g_awq(const float *v, const float *s, int64_t n, int64_t k, int64_t group,
+                            uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros);
 /* closed form of the MX scale exponent ceilf(log2f(raw)) (schemes.rs:706) and its check */
 int orc_mx_scale_exp_model(float raw);
 int64_t orc_mx_scale_crosscheck(uint32_t lo, uint32_t hi, uint32_t *first_bad);

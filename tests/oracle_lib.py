@@ -57,6 +57,7 @@ def lib() -> ctypes.CDLL:
             "orc_gemm_fp8": (None, [P, P, I64, P, P, I64, I64, P]),
             "orc_now_seconds": (ctypes.c_double, []),
             "orc_mx_scale_exp_model": (c_int, [c_float]),
+            "orc_quantize_int4g_awq": (None, [P, P, I64, I64, I64, P, P, P]),
             "orc_mx_scale_crosscheck": (I64, [c_uint32, c_uint32, P]),
         }
         for name, (res, args) in sig.items():
@@ -107,6 +108,19 @@ def quantize_int4g(w: np.ndarray, group: int = 128):
     scales = np.zeros((n, (g + 7) // 8 * 8), np.uint16)
     zeros = np.zeros((n, (g + 7) // 8), np.uint32)
     lib().orc_quantize_int4g(_p(w), n, k, group, _p(codes), _p(scales), _p(zeros))
+    return codes, scales, zeros
+
+
+def quantize_int4g_awq(w: np.ndarray, s: np.ndarray, group: int = 128):
+    w = np.ascontiguousarray(w, np.float32)
+    s = np.ascontiguousarray(s, np.float32)
+    n, k = w.shape
+    g = (k + group - 1) // group
+    zw = (g + 7) // 8
+    codes = np.zeros((n, k // 8), np.uint32)
+    scales = np.zeros((n, zw * 8), np.uint16)
+    zeros = np.zeros((n, zw), np.uint32)
+    lib().orc_quantize_int4g_awq(_p(w), _p(s), n, k, group, _p(codes), _p(scales), _p(zeros))
     return codes, scales, zeros
 
 

@@ -106,6 +106,33 @@ def test_int4g_edge_groups(cuda):
     assert np.array_equal(_u32(p.zeros), z_ref)
 
 
+@pytest.mark.parametrize("group", [32, 128])
+@pytest.mark.parametrize("n,k", [(16, 1024), (3, 11008), (4096, 4096)])
+def test_int4g_awq_prescale_bit_exact(cuda, group, n, k):
+    """BASELINE config 5: W' = W * a^0.5 per input channel, quantized INT4 g128 in one pass;
+    codes / scales / zeros equal the oracle's quantization of f32(W * s)."""
+    w = _w(23, n, k, specials=(n * k >= 1024))
+    s = synth.awq_channel_scales(23, 9, k)
+    c_ref, s_ref, z_ref = O.quantize_int4g_awq(w, s, group)
+    p = ops.quantize_int4g(torch.from_numpy(w).to(cuda), group, torch.from_numpy(s).to(cuda))
+    assert np.array_equal(_u32(p.codes), c_ref)
+    assert np.array_equal(p.scales.cpu().numpy().view(np.uint16), s_ref)
+    assert np.array_equal(_u32(p.zeros), z_ref)
+
+
+def test_int4g_awq_rejects_bad_scale(cuda):
+    from castforge_amd.ffi import CastForgeHipError
+
+    w = torch.zeros((4, 64), device=cuda)
+    with pytest.raises(ValueError):
+        ops.quantize_int4g(w, 32, torch.zeros(63, device=cuda))
+    from castforge_amd import ffi
+    p = ops.quantize_int4g(w, 32)
+    with pytest.raises(CastForgeHipError, match="in_scale must not be NULL"):
+        ffi.call("castforge_hip_quantize_int4g_awq", w.data_ptr(), None, 4, 64, 32, p.codes.data_ptr(),
+                 p.scales.data_ptr(), p.zeros.data_ptr(), torch.cuda.current_stream().cuda_stream)
+
+
 # ---------------------------------------------------------------------------- NF4 ----
 @pytest.mark.parametrize("block", [8, 32, 64, 128, 512])
 @pytest.mark.parametrize("n,k", [(16, 1024), (7, 200), (2, 11008)])
