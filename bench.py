@@ -392,7 +392,7 @@ def main():
                    "value_is": "W4A16 GEMV GB/s at M=1 (algorithmic bytes / whole-job time per step)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "skinny_qgemm_kernel<FMT_INT4>", "bytes_per_launch": bytes_m1,
+                     "kernel": "skinny_m1_split_kernel<FMT_INT4, 16>", "bytes_per_launch": bytes_m1,
                      "us_per_launch": round(ms_step * 1e3, 2)},
         "cpu_baseline": cpu,
         "components": components,

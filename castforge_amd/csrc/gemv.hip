@@ -6,20 +6,19 @@
 // row-major (packed_rhs layout, fold.rs:549-554).
 //
 // Decode is HBM-bound on the packed weight stream.  Design:
-//   * a workgroup (4 waves) owns 16*R weight rows; the 4 waves interleave over K "chunks";
+//   * a workgroup (4 waves) owns a tile of 16*R weight rows (R = 1 for M = 1);
 //   * a chunk is what one wave-wide load brings for 16 rows: lane%16 = row, lane/16 = part,
 //     each lane loads LW bytes (16, 8 or 4), so one chunk spans exactly one quantization
 //     group / NF4 block per row and its scale multiplies the fp32 MFMA result (no rounding of
 //     the scale into the f16 operand);
-//   * codes become exact f16 operands: INT4 (q - z) and INT8 q by the magic-exponent trick,
-//     NF4 table values as an exact f16 hi + lo pair (two MFMAs) from an LDS table;
 //   * v_mfma_f32_16x16x32_f16 with dequantized W rows as B and the activation rows as A; x is
-//     converted once per workgroup from bf16 to f16 in LDS, in the permuted order the nibble
-//     extraction produces, so M = 1..16 costs the same MFMA count;
-//   * weight loads are double-buffered per wave in units of NB chunks (the next unit is in
-//     flight while the current one is consumed); the first unit is issued before the x
-//     staging starts; problems with the longest K are dispatched first so no long workgroup
-//     forms a tail.
+//     converted from bf16 to f16 in LDS, in the permuted order the nibble extraction produces;
+//   * M = 1 (skinny_m1_split_kernel): each wave owns a contiguous quarter of K, copies its
+//     groups' scales / zero points and its x slice into its own LDS region up front, and then
+//     streams codes only, with the INT4 zero point folded out of the per-code decode;
+//   * M = 2..16 (skinny_qgemm_kernel): the waves interleave over K in units of NB chunks,
+//     double-buffered per wave, with exact (q - z) / q / NF4 hi+lo operands;
+//   * problems with the longest K are dispatched first so no long workgroup forms a tail.
 #include <algorithm>
 
 #include "../../include/castforge_hip.h"
@@ -34,7 +33,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kLdsBytesMax = 32768;  // activation stage per workgroup
+constexpr int kLdsBytesMax = 32768;    // activation stage per workgroup
+constexpr int kLdsBytesSplit = 65536;  // the M = 1 split-K kernel's x slices per workgroup
 constexpr int kMaxProblems = 8;
 // rows-per-workgroup multiplier and chunks in flight per wave for M <= 4 (tuning knobs)
 #ifndef CFH_GEMV_R_SMALL
@@ -42,6 +42,10 @@ constexpr int kMaxProblems = 8;
 #endif
 #ifndef CFH_GEMV_NB_SMALL
 #define CFH_GEMV_NB_SMALL 4
+#endif
+// M = 1 decode uses the split-K kernel (0: the per-tile kernel, for comparison)
+#ifndef CFH_GEMV_SPLIT
+#define CFH_GEMV_SPLIT 1
 #endif
 // cache policy of the streamed weight-code loads (2 = nt: the codes are read once)
 #ifndef CFH_GEMV_CPOL
@@ -60,7 +64,9 @@ struct Problem {
     int32_t group;          // INT4 group / NF4 block
     int32_t scale_per_row;  // INT8: 1 per-channel, 0 per-tensor
     int32_t tile_begin;     // first workgroup index of this problem
-    int32_t kc;             // K elements staged per LDS pass
+    int32_t kc;             // K elements staged per LDS pass (M = 1 split-K: LDS bytes per wave)
+    int32_t soff, zoff;     // M = 1 split-K: scale and zero-point pieces within a wave's LDS bytes
+    int32_t xsoff;          // M = 1 split-K, INT4: per-chunk x sums within a wave's LDS bytes
 };
 
 struct Batch {
@@ -140,6 +146,17 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
                                              static_cast<int>(bytes), 0x00020000);
 }
 
+// The same over values the caller knows to be wave-uniform, moved to scalar registers (a
+// descriptor built from values the compiler cannot prove uniform is re-read per lane).
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ rsrc_t make_rsrc_u(const void *base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = static_cast<uint32_t>(uni(static_cast<int>(static_cast<uint32_t>(a))));
+    const uint32_t hi = static_cast<uint32_t>(uni(static_cast<int>(static_cast<uint32_t>(a >> 32))));
+    return make_rsrc(reinterpret_cast<const void *>((static_cast<uint64_t>(hi) << 32) | lo),
+                     static_cast<uint32_t>(uni(static_cast<int>(bytes))));
+}
+
 // Loads one unit issues: per row tile NB code loads, plus one scale and one zero-point load
 // (INT4) or one absmax load per chunk (NF4).
 template <int FMT, int NB, int R>
@@ -188,9 +205,10 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const rsrc_t rc = make_rsrc(static_cast<const uint8_t *>(P.codes) + n0 * row_bytes,
                                 static_cast<uint32_t>(rows_here) * row_bytes);
     // INT4: scale groups per row; NF4: absmax blocks per row
-    const uint32_t G = static_cast<uint32_t>((K + P.group - 1) / P.group);
+    const int64_t grp = FMT == FMT_INT8 ? CK : P.group;  // INT8 has no groups (group 0)
+    const uint32_t G = static_cast<uint32_t>((K + grp - 1) / grp);
     const uint32_t ZW = (G + 7) / 8, GP = ZW * 8;  // INT4 scale rows are padded to GP groups
-    const int gshift = __builtin_ctz(static_cast<uint32_t>(P.group / CK));  // chunks per group = 2^gshift
+    const int gshift = __builtin_ctz(static_cast<uint32_t>(grp / CK));  // chunks per group = 2^gshift
     rsrc_t rs, rz;
     if constexpr (FMT == FMT_INT4) {
         rs = make_rsrc(static_cast<const uint16_t *>(P.scales) + n0 * GP, static_cast<uint32_t>(rows_here) * GP * 2);
@@ -459,6 +477,332 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     }
 }
 
+// ---- M = 1 split-K kernel ------------------------------------------------------------------
+// Decode (M = 1): one workgroup per 16-row tile, each of its 4 waves owning a contiguous
+// quarter of K (whole units of NB chunks) and its own LDS region, so no wave waits for
+// another before the final cross-wave sum.  A wave first copies, straight into its region
+// (buffer loads to LDS, 16 bytes per lane), the scales and zero points of its groups for the
+// 16 rows and its slice of x; then it issues the code loads of its first kSplitDepth units,
+// waits for the copies alone (vmcnt drains in issue order), converts the x slice in place to
+// permuted f16, and from then on keeps kSplitDepth - 1 units in flight while it consumes one.
+// The main loop loads codes only: metadata read per unit would be a 4-byte access to each of
+// 16 rows, as many memory requests as the codes themselves.  The loop has one exit, no branch
+// inside and no load under a branch, so the compiler's vmcnt waits cover only the unit being
+// consumed (an early exit, even a uniform one, turns the loop into exec-mask flow whose
+// merges wait for loads in flight).
+#ifndef CFH_GEMV_NB_SPLIT
+#define CFH_GEMV_NB_SPLIT 2
+#endif
+#ifndef CFH_GEMV_DEPTH_SPLIT
+#define CFH_GEMV_DEPTH_SPLIT 2
+#endif
+constexpr int kSplitDepth = CFH_GEMV_DEPTH_SPLIT;
+
+// Metadata copies: bytes [lo, lo + 16 * pieces) of each of the 16 rows' metadata arrays, in
+// 16-byte pieces; copy i moves pieces 4i .. 4i + 3 of every row into 1 KB of LDS, lane
+// (row r, part p) writing piece 4i + p of row r at i * 1024 + (16 p + r) * 16.
+__device__ __forceinline__ uint32_t meta_lds_off(uint32_t b, int r) {
+    const uint32_t p = b >> 4;
+    return (p >> 2) * 1024u + ((p & 3u) * 16u + static_cast<uint32_t>(r)) * 16u + (b & 15u);
+}
+
+// waves per SIMD the split kernel's register budget is sized for (0: the compiler's choice)
+#ifndef CFH_GEMV_SPLIT_WPE
+#define CFH_GEMV_SPLIT_WPE 5
+#endif
+template <int FMT, int LW>
+__global__ __launch_bounds__(kThreads)
+#if CFH_GEMV_SPLIT_WPE
+__attribute__((amdgpu_waves_per_eu(CFH_GEMV_SPLIT_WPE)))
+#endif
+void skinny_m1_split_kernel(Batch b) {
+    constexpr int WPL = LW / 4;
+    constexpr int CPB = codes_per_byte<FMT>();
+    constexpr int CK = 4 * LW * CPB;
+    constexpr int NB = CFH_GEMV_NB_SPLIT;
+    constexpr int D = kSplitDepth;
+    constexpr uint32_t kOob = 0x80000000u;  // past every descriptor's range: reads zero, no traffic
+    // INT4 with at least two code words per lane and chunk: the zero point is folded out of
+    // the per-code decode (below); with one word (group 32) the exact per-code decode is used
+    constexpr bool kFold = FMT == FMT_INT4 && WPL >= 2;
+    extern __shared__ __align__(16) uint8_t lds[];  // [kWaves][region]: x slice, scales, zero points
+    __shared__ float red[kWaves][64];
+    __shared__ uint2 lut[FMT == FMT_NF4 ? kWaves * 256 : 1];  // NF4: one table per wave
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = uni(tid >> 6);
+    const int lr = lane & 15, part = lane >> 4;
+
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxProblems; ++i)
+        if (i < b.count && static_cast<int>(blockIdx.x) >= b.p[i].tile_begin) pi = i;
+    const Problem &P = b.p[pi];
+    const int64_t N = P.n, K = P.k;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x - P.tile_begin) * 16;
+    const uint32_t rows = static_cast<uint32_t>((N - n0) < 16 ? (N - n0) : 16);
+    const uint32_t row_bytes = static_cast<uint32_t>(uni(static_cast<int>(K / CPB)));
+    const rsrc_t rc = make_rsrc_u(static_cast<const uint8_t *>(P.codes) + n0 * row_bytes, rows * row_bytes);
+    const int64_t grp = FMT == FMT_INT8 ? CK : P.group;  // INT8 has no groups (group 0)
+    const uint32_t Gr = static_cast<uint32_t>(uni(static_cast<int>((K + grp - 1) / grp)));
+    const uint32_t ZW = (Gr + 7) / 8, GP = ZW * 8;
+    const int gshift = uni(__builtin_ctz(static_cast<uint32_t>(grp / CK)));
+    const uint32_t code_off = static_cast<uint32_t>(lr) * row_bytes + part * LW;
+
+    // this wave's units [u0, u1) and chunks [c_lo, c_hi)
+    const int nchunks = uni(static_cast<int>(K / CK));
+    const int nunits = (nchunks + NB - 1) / NB;
+    const int u0 = uni(wave * nunits / kWaves), u1 = uni((wave + 1) * nunits / kWaves);
+    const int U = u1 - u0;
+    const int c_lo = u0 * NB;
+    const int c_hi = u1 * NB < nchunks ? u1 * NB : nchunks;
+    uint8_t *const reg = lds + wave * P.kc;  // kc: region bytes per wave
+    _Float16 *const xw = reinterpret_cast<_Float16 *>(reg);
+    const uint8_t *const ms = reg + P.soff;  // scale (INT4) / absmax (NF4) pieces
+    const uint8_t *const mz = reg + P.zoff;  // zero-point pieces (INT4)
+    float2 *const xsum = reinterpret_cast<float2 *>(reg + P.xsoff);  // INT4: per chunk (T, X), see below
+    uint2 *const wl = lut + (FMT == FMT_NF4 ? wave * 256 : 0);
+
+    // NF4 decode table (hi, lo f16 pairs of two codes), written before any copy into LDS is
+    // issued: an LDS write after an LDS-bound copy is made to wait for every load in flight
+    if constexpr (FMT == FMT_NF4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = lane + 64 * q;
+            const _Float16 h0 = static_cast<_Float16>(kNf4[i & 15]), h1 = static_cast<_Float16>(kNf4[i >> 4]);
+            const _Float16 l0 = static_cast<_Float16>(kNf4[i & 15] - static_cast<float>(h0));
+            const _Float16 l1 = static_cast<_Float16>(kNf4[i >> 4] - static_cast<float>(h1));
+            half2_t hi = {h0, h1}, lo = {l0, l1};
+            wl[i] = make_uint2(as_u(hi), as_u(lo));
+        }
+    }
+
+    // metadata of the wave's groups: first byte (16-byte aligned) of the span in each row
+    uint32_t s_lo = 0, z_lo = 0;
+    if (c_hi > c_lo) {
+        auto copy_span = [&](const void *base, uint32_t row_stride, uint32_t lo, uint32_t hi, const uint8_t *dst) {
+            const rsrc_t r = make_rsrc_u(static_cast<const uint8_t *>(base) + n0 * row_stride, rows * row_stride);
+            const int pieces = static_cast<int>((hi - lo + 15) / 16);
+            for (int i = 0; i * 4 < pieces; ++i) {  // wave-uniform
+                const int p = 4 * i + part;
+                const uint32_t off = (static_cast<uint32_t>(lr) * row_stride + lo + 16u * p) | (p < pieces ? 0u : kOob);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    r, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(dst) + i * 1024),
+                    16, off, 0, 0, 0);
+            }
+        };
+        if constexpr (FMT == FMT_INT4) {
+            s_lo = (static_cast<uint32_t>(c_lo) * 2u) & ~15u;
+            copy_span(P.scales, GP * 2, s_lo, static_cast<uint32_t>(c_hi) * 2u, ms);
+            z_lo = (static_cast<uint32_t>(c_lo >> 3) * 4u) & ~15u;
+            copy_span(P.zeros, ZW * 4, z_lo, static_cast<uint32_t>(((c_hi - 1) >> 3) + 1) * 4u, mz);
+        } else if constexpr (FMT == FMT_NF4) {
+            s_lo = (static_cast<uint32_t>(c_lo >> gshift) * 4u) & ~15u;
+            copy_span(P.scales, Gr * 4, s_lo, static_cast<uint32_t>(((c_hi - 1) >> gshift) + 1) * 4u, ms);
+        }
+    }
+    // x slice: bf16 x[c_lo * CK, c_hi * CK) copied straight into the region
+    {
+        const int bytes = (c_hi > c_lo ? c_hi - c_lo : 0) * CK * 2;
+        const uint16_t *src = P.x + static_cast<int64_t>(c_lo) * CK;
+        for (int blk = 0; blk * 1024 < bytes; ++blk) {  // wave-uniform
+            const int e = blk * 1024 + lane * 16;
+            if (e < bytes)
+                __builtin_amdgcn_global_load_lds(
+                    static_cast<const void *>(src + (e >> 1)),
+                    reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(xw) + blk * 1024),
+                    16, 0, 0);
+        }
+    }
+
+    struct Unit {
+        uint32_t wq[NB][WPL];
+    };
+    // Unit k of this wave (k >= U: past the wave's range, reads nothing).  Offsets are computed
+    // unconditionally and pushed out of range by OR-ing in kOob (every real offset is below
+    // 2^31): a select between an offset and kOob would be compiled as a branch.
+    auto load_unit = [&](Unit &u, int k) {
+        const uint32_t c0 = static_cast<uint32_t>((u0 + k) * NB);
+        const uint32_t okm = k < U ? 0u : kOob;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint32_t m = (static_cast<int>(c0) + j < nchunks) ? okm : kOob;
+            load_words<LW>(rc, (code_off + (c0 + j) * (CK / CPB)) | m, u.wq[j]);
+        }
+    };
+    Unit ub[D];
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+        load_unit(ub[i], i);
+        __builtin_amdgcn_sched_barrier(0);  // unit by unit, in the order they are consumed
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(D * NB));  // the copies into LDS have landed
+    if constexpr (kFold) {
+        // Groups of 16 x values (the codes of two words) become f16 in the order the INT4
+        // decode below produces: the low nibbles of each byte (codes 0, 4, 2, 6 of each word)
+        // of both words, then the high nibbles (1, 5, 3, 7).  Per chunk, X = sum of its x and
+        // T = 1024 * (sum over low-nibble positions) + 64 * (sum over high-nibble positions),
+        // in f32 of the f16 values; the lanes of a chunk (one per group) reduce them.
+        constexpr int kSrc[16] = {0, 4, 2, 6, 8, 12, 10, 14, 1, 5, 3, 7, 9, 13, 11, 15};
+        constexpr int GPC = CK / 16;  // groups per chunk
+        const int groups = (c_hi > c_lo ? c_hi - c_lo : 0) * CK / 16;
+        for (int it = lane; it < groups; it += 64) {
+            const uint4 r0 = *reinterpret_cast<const uint4 *>(xw + it * 16);
+            const uint4 r1 = *reinterpret_cast<const uint4 *>(xw + it * 16 + 8);
+            const uint32_t wv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+            uint32_t o[8];
+            float slo = 0.0f, shi = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int s0 = kSrc[2 * q], s1 = kSrc[2 * q + 1];
+                const _Float16 h0 = static_cast<_Float16>(bf16_to_f32(static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)))));
+                const _Float16 h1 = static_cast<_Float16>(bf16_to_f32(static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)))));
+                const float f = static_cast<float>(h0) + static_cast<float>(h1);
+                if (q < 4) slo += f;
+                else shi += f;
+                half2_t h = {h0, h1};
+                o[q] = as_u(h);
+            }
+            *reinterpret_cast<uint4 *>(xw + it * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4 *>(xw + it * 16 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+#pragma unroll
+            for (int m = 1; m < GPC; m <<= 1) {
+                slo += __shfl_xor(slo, m);
+                shi += __shfl_xor(shi, m);
+            }
+            if (it % GPC == 0) xsum[it / GPC] = make_float2(1024.0f * slo + 64.0f * shi, slo + shi);
+        }
+    } else {
+        const int runs = (c_hi > c_lo ? c_hi - c_lo : 0) * CK / 8;
+        for (int it = lane; it < runs; it += 64) {
+            const uint4 raw = *reinterpret_cast<const uint4 *>(xw + it * 8);
+            const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int s0 = perm_src(FMT, 2 * q), s1 = perm_src(FMT, 2 * q + 1);
+                const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
+                const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
+                half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
+                o[q] = as_u(h);
+            }
+            *reinterpret_cast<uint4 *>(xw + it * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));  // this wave's LDS writes are done
+
+    const Int4Consts i4k = int4_consts();
+    float acc = 0.0f;  // slot 0 of the 16x16 MFMA tile: row lr of this tile (lanes with part 0)
+    // A chunk past K (the last unit may be partial) or of a unit past the wave's range reads
+    // zero codes, takes its x and metadata from the wave's first chunk (finite) and is scaled
+    // by 0: no branch, so no path leaves a unit's registers unread.
+    auto process = [&](const Unit &u, int k) {
+        const int cb = (u0 + k) * NB;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const bool live = k < U && cb + j < nchunks;
+            const int c = live ? cb + j : c_lo;
+            const _Float16 *xa = xw + (c - c_lo) * CK + part * (CK / 4);
+            floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (kFold) {
+                // Codes decode to 1024 + q (low nibbles) and 1024 + 16 q (high nibbles) by one
+                // AND-OR each; the two MFMA chains give sum x (1024 + q) and sum x (1024 + 16 q),
+                // and sum x (q - z) = lo + hi / 16 - T - z X with the chunk's x sums.
+                const uint32_t zw = *reinterpret_cast<const uint32_t *>(
+                    mz + meta_lds_off(static_cast<uint32_t>(c >> 3) * 4u - z_lo, lr));
+                const float z = static_cast<float>((zw >> (4 * (static_cast<uint32_t>(c) & 7u))) & 15u);
+                floatx4 plo = floatx4{0.f, 0.f, 0.f, 0.f}, phi = plo;
+#pragma unroll
+                for (int q = 0; q < WPL / 2; ++q) {
+                    const uint32_t wa = u.wq[j][2 * q], wb = u.wq[j][2 * q + 1];
+                    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+                    // masks and magic in VGPRs: each AND-OR is then one v_and_or_b32
+                    const uint32_t LO = i4k.lo_mask, HI = i4k.hi_mask, MG = i4k.magic;
+                    const half8_t alo = *reinterpret_cast<const half8_t *>(xa + q * 16);
+                    const half8_t ahi = *reinterpret_cast<const half8_t *>(xa + q * 16 + 8);
+                    plo = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        alo, pack8((wa & LO) | MG, (wa8 & LO) | MG, (wb & LO) | MG, (wb8 & LO) | MG), plo, 0, 0, 0);
+                    phi = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        ahi, pack8((wa & HI) | MG, (wa8 & HI) | MG, (wb & HI) | MG, (wb8 & HI) | MG), phi, 0, 0, 0);
+                }
+                const float2 tx = xsum[c - c_lo];
+                const float r = fmaf(phi[0], 0.0625f, plo[0]) - fmaf(z, tx.y, tx.x);
+                const float sc = f16_to_f32(*reinterpret_cast<const uint16_t *>(
+                    ms + meta_lds_off(static_cast<uint32_t>(c) * 2u - s_lo, lr)));
+                acc += r * (live ? sc : 0.0f);
+            } else if constexpr (FMT == FMT_INT4) {  // one word per lane: exact (q - z) codes
+                const uint32_t zw = *reinterpret_cast<const uint32_t *>(
+                    mz + meta_lds_off(static_cast<uint32_t>(c >> 3) * 4u - z_lo, lr));
+                const uint32_t z = (zw >> (4 * (static_cast<uint32_t>(c) & 7u))) & 15u;
+                const uint32_t zc1024 = (0xE400u + z) * 0x00010001u, zc64 = (0xD400u + (z << 4)) * 0x00010001u;
+#pragma unroll
+                for (int q = 0; q < WPL; ++q) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xa + q * 8);
+                    uint32_t hb[4];
+                    int4_word_to_h(u.wq[j][q], as_h2(zc1024), as_h2(zc64), i4k, hb);
+                    pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(hb[0], hb[1], hb[2], hb[3]), pacc, 0, 0, 0);
+                }
+                const float sc = f16_to_f32(*reinterpret_cast<const uint16_t *>(
+                    ms + meta_lds_off(static_cast<uint32_t>(c) * 2u - s_lo, lr)));
+                acc += pacc[0] * (live ? sc : 0.0f);
+            } else if constexpr (FMT == FMT_NF4) {
+#pragma unroll
+                for (int q = 0; q < WPL; ++q) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xa + q * 8);
+                    const uint32_t w = u.wq[j][q];
+                    const uint2 e0 = wl[w & 255u], e1 = wl[(w >> 8) & 255u];
+                    const uint2 e2 = wl[(w >> 16) & 255u], e3 = wl[w >> 24];
+                    pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.x, e1.x, e2.x, e3.x), pacc, 0, 0, 0);
+                    pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(e0.y, e1.y, e2.y, e3.y), pacc, 0, 0, 0);
+                }
+                const float am = *reinterpret_cast<const float *>(
+                    ms + meta_lds_off(static_cast<uint32_t>(c >> gshift) * 4u - s_lo, lr));
+                acc += pacc[0] * (live ? am : 0.0f);
+            } else {
+#pragma unroll
+                for (int q = 0; q < WPL / 2; ++q) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xa + q * 8);
+                    uint32_t h0[2], h1[2];
+                    int8_word_to_h(u.wq[j][2 * q], h0);
+                    int8_word_to_h(u.wq[j][2 * q + 1], h1);
+                    pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]), pacc, 0, 0, 0);
+                }
+                acc += live ? pacc[0] : 0.0f;
+            }
+        }
+    };
+
+    // unit k sits in ub[k % D]: consumed, then refilled with unit k + D (past the wave's range
+    // the refill reads nothing and the unit adds zero)
+    for (int k = 0; k < U; k += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            process(ub[i], k + i);
+            load_unit(ub[i], k + i + D);
+            __builtin_amdgcn_sched_barrier(0);  // the refill stays ahead of the next unit's waits
+        }
+    }
+
+    // cross-wave sum; lanes 0..15 of wave 0 store rows n0 .. n0 + 15 (a store past N, or from
+    // a lane without a row, goes to an offset the descriptor drops)
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        float v = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+        if constexpr (FMT == FMT_INT8) {
+            const rsrc_t rs = P.scale_per_row ? make_rsrc_u(static_cast<const float *>(P.scales) + n0, rows * 4)
+                                              : make_rsrc_u(P.scales, 4);
+            v *= __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                               rs, lane < 16 ? (P.scale_per_row ? lane * 4u : 0u) : kOob, 0, 0));
+        }
+        const int esz = b.y_bf16 ? 2 : 4;
+        const rsrc_t ry = make_rsrc_u(static_cast<const uint8_t *>(P.y) + n0 * esz, rows * esz);
+        const uint32_t off = lane < 16 ? static_cast<uint32_t>(lane * esz) : kOob;
+        if (b.y_bf16) __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(v), ry, off, 0, 0);
+        else __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ry, off, 0, 0);
+    }
+}
+
 // ---- generic fallback: any M, any group/block, K % 8 == 0 (f32 VALU, one wave per row) ----
 template <int FMT>
 __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int y_bf16) {
@@ -559,10 +903,67 @@ void launch_lw(int lw, const Batch &b, int64_t tiles, int64_t lds, hipStream_t s
     }
 }
 
+template <int FMT, int LW>
+void launch_split(const Batch &b, int64_t tiles, int64_t lds, hipStream_t st) {
+    skinny_m1_split_kernel<FMT, LW><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), static_cast<size_t>(lds), st>>>(b);
+}
+
 // Launch problems that share the format, M and chunk width; all must pass skinny_ok.
 void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipStream_t st) {
     const int lw = lw_for(fmt, ps[0].group);
     const int ck = chunk_k(fmt, lw);
+    if (m == 1 && CFH_GEMV_SPLIT) {
+        // LDS bytes of one wave: its x slice, then its groups' scale and zero-point pieces
+        // (1 KB per copy of 4 pieces of 16 bytes per row); bounds over the waves' ranges
+        std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
+        Batch b{};
+        int64_t region_max = 0, tiles = 0;
+        auto copies = [](int64_t span) { return ((span + 15) / 16 + 3) / 4; };
+        for (int i = 0; i < count; ++i) {
+            require(lw_for(fmt, ps[i].group) == lw, "batched problems must share the group size class");
+            const int64_t nunits = (ps[i].k / ck + CFH_GEMV_NB_SPLIT - 1) / CFH_GEMV_NB_SPLIT;
+            const int64_t cw = (nunits + kWaves - 1) / kWaves * CFH_GEMV_NB_SPLIT;  // chunks per wave, at most
+            const int64_t xbytes = (cw * ck * 2 + 255) / 256 * 256;
+            const int64_t tbytes = fmt == FMT_INT4 && lw >= 8 ? (cw * 8 + 255) / 256 * 256 : 0;  // x sums
+            int64_t sbytes = 0, zbytes = 0;
+            if (fmt == FMT_INT4) {
+                sbytes = 1024 * copies(2 * cw + 14);
+                zbytes = 1024 * copies(4 * ((cw + 7) / 8 + 1) + 12);
+            } else if (fmt == FMT_NF4) {
+                const int64_t cpb = ps[i].group / ck;  // chunks per absmax block
+                sbytes = 1024 * copies(4 * ((cw + cpb - 1) / cpb + 1) + 12);
+            }
+            b.p[i] = ps[i];
+            b.p[i].tile_begin = static_cast<int32_t>(tiles);
+            b.p[i].kc = static_cast<int32_t>(xbytes + tbytes + sbytes + zbytes);
+            b.p[i].xsoff = static_cast<int32_t>(xbytes);
+            b.p[i].soff = static_cast<int32_t>(xbytes + tbytes);
+            b.p[i].zoff = static_cast<int32_t>(xbytes + tbytes + sbytes);
+            region_max = std::max(region_max, xbytes + tbytes + sbytes + zbytes);
+            tiles += (ps[i].n + 15) / 16;
+        }
+        if (region_max * kWaves <= kLdsBytesSplit) {
+            require(tiles <= 0x7fffffff, "too many rows for one launch");
+            if (tiles == 0) return;
+            b.count = count;
+            b.m = 1;
+            b.y_bf16 = y_bf16;
+            const int64_t lds = region_max * kWaves;
+            if (fmt == FMT_INT4) {
+                if (lw == 16) launch_split<FMT_INT4, 16>(b, tiles, lds, st);
+                else if (lw == 8) launch_split<FMT_INT4, 8>(b, tiles, lds, st);
+                else launch_split<FMT_INT4, 4>(b, tiles, lds, st);
+            } else if (fmt == FMT_NF4) {
+                if (lw == 16) launch_split<FMT_NF4, 16>(b, tiles, lds, st);
+                else if (lw == 8) launch_split<FMT_NF4, 8>(b, tiles, lds, st);
+                else launch_split<FMT_NF4, 4>(b, tiles, lds, st);
+            } else {
+                launch_split<FMT_INT8, 16>(b, tiles, lds, st);
+            }
+            check_launch("skinny_m1_split");
+            return;
+        }
+    }
     const int R = m <= 4 ? CFH_GEMV_R_SMALL : 4;
     // longest K first: its workgroups run longest, so they start first
     std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
