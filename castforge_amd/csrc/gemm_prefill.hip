@@ -29,6 +29,10 @@
 //   * the nibble / byte extraction places codes in a fixed order inside each 16-byte chunk;
 //     x is written to LDS in the same order, so the MFMA's k index matches on both operands;
 //   * XCD-aware tile order (each XCD owns a contiguous range of tiles grouped by m).
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
 
@@ -125,8 +129,10 @@ struct Cfg {
 };
 
 // W rows handled per thread per slice: BN / 256 (BN = 256 -> 1 row, BN = 128 -> lanes pair up)
+// Large tiles keep one wave per SIMD (their accumulators fill the register file); tiles of
+// 128 x 128 and below leave room for a second workgroup per CU.
 template <int FMT, int BM, int BN, int WN>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM * BN > 128 * 128 ? 1 : 2, BM * BN > 128 * 128 ? 1 : 2)))
 void prefill_qgemm_kernel(PfArgs a) {
     using C = Cfg<BM, BN, WN>;
     constexpr int P = FMT == FMT_INT8 ? 1 : 2;   // f16 planes of W (hi, lo)
@@ -438,13 +444,44 @@ void launch_cfg(PfArgs a, hipStream_t st) {
     check_launch("prefill_qgemm");
 }
 
+// Tile shapes, largest first.  The largest one that still gives every CU a workgroup is used;
+// small M or N falls through to smaller tiles rather than leaving CUs idle (NF4 at M = 64 over
+// an 11008 x 4096 matrix: 227 us with 256 x 256 tiles, 45 us with 64 x 64).
+// CASTFORGE_PREFILL_TILE (e.g. "64x128") forces a shape.
+enum PfTile { PF_256x256, PF_128x256, PF_128x128, PF_64x128, PF_64x64, PF_NTILES };
+constexpr int kPfTileM[PF_NTILES] = {256, 128, 128, 64, 64};
+constexpr int kPfTileN[PF_NTILES] = {256, 256, 128, 128, 64};
+
+int pick_tile(int64_t M, int64_t N) {
+    if (const char *e = std::getenv("CASTFORGE_PREFILL_TILE")) {
+        for (int t = 0; t < PF_NTILES; ++t) {
+            char name[16];
+            std::snprintf(name, sizeof(name), "%dx%d", kPfTileM[t], kPfTileN[t]);
+            if (std::strcmp(e, name) == 0) return t;
+        }
+    }
+    int cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    }
+    for (int t = 0; t < PF_NTILES; ++t) {
+        const int64_t tiles = ((M + kPfTileM[t] - 1) / kPfTileM[t]) * ((N + kPfTileN[t] - 1) / kPfTileN[t]);
+        if (M > kPfTileM[t] / 2 && tiles >= static_cast<int64_t>(cus)) return t;
+    }
+    return PF_64x64;
+}
+
 template <int FMT>
 void launch_fmt(const PfArgs &a, hipStream_t st) {
-    // prefer the 256 x 256 tile; smaller m tiles when M is small so workgroups cover the CUs
-    const int64_t t256 = ((a.M + 255) / 256) * static_cast<int64_t>((a.N + 255) / 256);
-    if (a.M > 128 && t256 >= 256) launch_cfg<FMT, 256, 256, 2>(a, st);
-    else if (a.M > 64) launch_cfg<FMT, 128, 256, 2>(a, st);
-    else launch_cfg<FMT, 64, 256, 4>(a, st);
+    switch (pick_tile(a.M, a.N)) {
+        case PF_256x256: launch_cfg<FMT, 256, 256, 2>(a, st); break;
+        case PF_128x256: launch_cfg<FMT, 128, 256, 2>(a, st); break;
+        case PF_128x128: launch_cfg<FMT, 128, 128, 2>(a, st); break;
+        case PF_64x128: launch_cfg<FMT, 64, 128, 2>(a, st); break;
+        default: launch_cfg<FMT, 64, 64, 2>(a, st); break;
+    }
 }
 
 }  // namespace

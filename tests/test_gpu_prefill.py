@@ -76,6 +76,32 @@ def test_nf4_prefill(cuda, m, block):
     _close(y, ref, "nf4")
 
 
+@pytest.mark.parametrize("tile", ["256x256", "128x256", "128x128", "64x128", "64x64"])
+@pytest.mark.parametrize("fmt", ["int4", "nf4", "int8"])
+def test_prefill_every_tile_shape(cuda, monkeypatch, tile, fmt):
+    """Each tile shape forced through CASTFORGE_PREFILL_TILE, with partial tiles in m and n
+    (300 x 328 is not a multiple of any tile) and K over several slices."""
+    m, n, k = 300, 328, 768
+    print(f"[prefill tile] {fmt} {tile}", flush=True)
+    monkeypatch.setenv("CASTFORGE_PREFILL_TILE", tile)
+    w = synth.weight(91, 1, n, k)
+    xb, x = _x(92, m, k, cuda)
+    if fmt == "int4":
+        p, (c, s, z) = _int4(w, 128, cuda)
+        y = ops.gemm_w4a16(x, p, torch.float32)
+        ref = O.gemm_w4a16(xb, c, s, z, n, k, 128)
+    elif fmt == "nf4":
+        p = ops.quantize_nf4(torch.from_numpy(w).to(cuda), 64)
+        y = ops.gemm_nf4(x, p, torch.bfloat16)
+        ref = O.gemm_nf4(xb, p.codes.cpu().numpy().view(np.uint32), p.absmax.cpu().numpy(), n, k, 64)
+    else:
+        q, sc = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, "channel")
+        y = ops.gemm_w8a16(x, q, sc, "channel", torch.float32)
+        ref = O.gemm_w8a16(xb, q.cpu().numpy(), sc.cpu().numpy())
+    torch.cuda.synchronize()
+    _close(y, ref, f"{fmt} {tile}")
+
+
 @pytest.mark.parametrize("m", [17, 200])
 @pytest.mark.parametrize("gran", ["channel", "tensor"])
 def test_w8a16_prefill(cuda, m, gran):
