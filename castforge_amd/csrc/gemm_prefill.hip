@@ -131,7 +131,7 @@ struct Cfg {
 // W rows handled per thread per slice: BN / 256 (BN = 256 -> 1 row, BN = 128 -> lanes pair up)
 // Large tiles keep one wave per SIMD (their accumulators fill the register file); tiles of
 // 128 x 128 and below leave room for a second workgroup per CU.
-template <int FMT, int BM, int BN, int WN>
+template <int FMT, int BM, int BN, int WN, int R>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM * BN > 128 * 128 ? 1 : 2, BM * BN > 128 * 128 ? 1 : 2)))
 void prefill_qgemm_kernel(PfArgs a) {
     using C = Cfg<BM, BN, WN>;
@@ -349,35 +349,38 @@ void prefill_qgemm_kernel(PfArgs a) {
     };
 
     const int KT = K / BK;
-    Regs ra, rb;
+    // R register sets: set t % R carries slice t from its global loads to its LDS write.
+    Regs ring[R];
     if constexpr (FMT == FMT_NF4) __syncthreads();  // LUT ready
-    gload(ra, 0);
-    if (KT > 1) gload(rb, 1);
-    lwrite(ra, 0, 0);
+    static_for<R>([&](auto II) {
+        constexpr int i = decltype(II)::value;
+        if (i < KT) gload(ring[i], i);
+    });
+    lwrite(ring[0], 0, 0);
     __syncthreads();
-    // Step t: stage t & 1 holds slice t and `nx` holds slice t + 1 (loads issued a step ago);
-    // `fr2` is free.  Issue slice t + 2 into fr2, run slice t's MFMAs, convert slice t + 1 into
-    // the other stage (last read in step t - 1), then barrier.  The barrier is a bare
-    // s_barrier after the LDS writes retire: __syncthreads() would also wait for the global
-    // loads of slice t + 2.  Steady steps are branch-free, so the compiler's vmcnt waits cover
-    // only the loads being consumed.
-    auto step = [&](auto steady, int t, Regs &nx, Regs &fr2) {
+    // Step t: stage t & 1 holds slice t, sets (t + 1) % R .. hold slices t + 1 .. t + R - 1
+    // (loads in flight) and set t % R is free (slice t went to LDS in step t - 1).  Issue
+    // slice t + R into set t % R, run slice t's MFMAs, convert slice t + 1 into the other stage
+    // (last read in step t - 1), then barrier.  The barrier is a bare s_barrier after the LDS
+    // writes retire: __syncthreads() would also wait for the global loads in flight.  Steady
+    // steps are branch-free, so the compiler's vmcnt waits cover only the loads being consumed.
+    // Small tiles finish a slice quickly, so they keep more slices in flight (larger R).
+    auto step = [&](auto steady, auto SI, int t) {
         constexpr bool kSteady = decltype(steady)::value;
-        if (kSteady || t + 2 < KT) gload(fr2, t + 2);
+        constexpr int si = decltype(SI)::value;
+        if (kSteady || t + R < KT) gload(ring[si], t + R);
         mma_stage(t & 1);
-        if (kSteady || t + 1 < KT) lwrite(nx, t + 1, (t + 1) & 1);
+        if (kSteady || t + 1 < KT) lwrite(ring[(si + 1) % R], t + 1, (t + 1) & 1);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));
         __builtin_amdgcn_s_barrier();
     };
     int kt = 0;
-    for (; kt + 3 < KT; kt += 2) {
-        step(std::true_type{}, kt, rb, ra);
-        step(std::true_type{}, kt + 1, ra, rb);
-    }
-    for (; kt < KT; kt += 2) {
-        step(std::false_type{}, kt, rb, ra);
-        if (kt + 1 < KT) step(std::false_type{}, kt + 1, ra, rb);
-    }
+    for (; kt + 2 * R - 1 < KT; kt += R)
+        static_for<R>([&](auto II) { step(std::true_type{}, II, kt + decltype(II)::value); });
+    for (; kt < KT; kt += R)
+        static_for<R>([&](auto II) {
+            if (kt + decltype(II)::value < KT) step(std::false_type{}, II, kt + decltype(II)::value);
+        });
 
     // ---- epilogue: acc[i][j] holds n = wn + 32 i + 8 g + 4 (lane / 32) + q (reg 4 g + q),
     // m = wm + 32 j + lane % 32 ----
@@ -431,7 +434,7 @@ void prefill_qgemm_kernel(PfArgs a) {
     });
 }
 
-template <int FMT, int BM, int BN, int WN>
+template <int FMT, int BM, int BN, int WN, int R>
 void launch_cfg(PfArgs a, hipStream_t st) {
     constexpr int P = FMT == FMT_INT8 ? 1 : 2;
     constexpr int lds = 2 * (P * BN * 64 + BM * 64);
@@ -440,7 +443,7 @@ void launch_cfg(PfArgs a, hipStream_t st) {
     a.tiles_n = (a.N + BN - 1) / BN;
     const int64_t tiles = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
     require(tiles <= 0x7fffffff, "too many tiles");
-    prefill_qgemm_kernel<FMT, BM, BN, WN><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), lds, st>>>(a);
+    prefill_qgemm_kernel<FMT, BM, BN, WN, R><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), lds, st>>>(a);
     check_launch("prefill_qgemm");
 }
 
@@ -448,6 +451,22 @@ void launch_cfg(PfArgs a, hipStream_t st) {
 // small M or N falls through to smaller tiles rather than leaving CUs idle (NF4 at M = 64 over
 // an 11008 x 4096 matrix: 227 us with 256 x 256 tiles, 45 us with 64 x 64).
 // CASTFORGE_PREFILL_TILE (e.g. "64x128") forces a shape.
+// register sets in flight per tile shape (slices loaded ahead of their LDS write)
+#ifndef CFH_PF_R_256
+#define CFH_PF_R_256 2
+#endif
+#ifndef CFH_PF_R_128x256
+#define CFH_PF_R_128x256 2
+#endif
+#ifndef CFH_PF_R_128
+#define CFH_PF_R_128 4
+#endif
+#ifndef CFH_PF_R_64x128
+#define CFH_PF_R_64x128 6
+#endif
+#ifndef CFH_PF_R_64
+#define CFH_PF_R_64 8
+#endif
 enum PfTile { PF_256x256, PF_128x256, PF_128x128, PF_64x128, PF_64x64, PF_NTILES };
 constexpr int kPfTileM[PF_NTILES] = {256, 128, 128, 64, 64};
 constexpr int kPfTileN[PF_NTILES] = {256, 256, 128, 128, 64};
@@ -476,11 +495,11 @@ int pick_tile(int64_t M, int64_t N) {
 template <int FMT>
 void launch_fmt(const PfArgs &a, hipStream_t st) {
     switch (pick_tile(a.M, a.N)) {
-        case PF_256x256: launch_cfg<FMT, 256, 256, 2>(a, st); break;
-        case PF_128x256: launch_cfg<FMT, 128, 256, 2>(a, st); break;
-        case PF_128x128: launch_cfg<FMT, 128, 128, 2>(a, st); break;
-        case PF_64x128: launch_cfg<FMT, 64, 128, 2>(a, st); break;
-        default: launch_cfg<FMT, 64, 64, 2>(a, st); break;
+        case PF_256x256: launch_cfg<FMT, 256, 256, 2, CFH_PF_R_256>(a, st); break;
+        case PF_128x256: launch_cfg<FMT, 128, 256, 2, CFH_PF_R_128x256>(a, st); break;
+        case PF_128x128: launch_cfg<FMT, 128, 128, 2, CFH_PF_R_128>(a, st); break;
+        case PF_64x128: launch_cfg<FMT, 64, 128, 2, CFH_PF_R_64x128>(a, st); break;
+        default: launch_cfg<FMT, 64, 64, 2, CFH_PF_R_64>(a, st); break;
     }
 }
 
