@@ -33,7 +33,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kLdsBytesMax = 32768;    // activation stage per workgroup
+// x staged per workgroup and pass for M > 1 (fewer passes: each pass boundary drains the
+// weight loads in flight; 32 KB -> 64 KB took M = 8 / 16 from 48 / 65 to 42 / 55 us per block)
+#ifndef CFH_GEMV_LDS_MAX
+#define CFH_GEMV_LDS_MAX 65536
+#endif
+constexpr int kLdsBytesMax = CFH_GEMV_LDS_MAX;  // activation stage per workgroup
 constexpr int kLdsBytesSplit = 65536;  // the M = 1 split-K kernel's x slices per workgroup
 constexpr int kMaxProblems = 8;
 // rows-per-workgroup multiplier and chunks in flight per wave for M <= 4 (tuning knobs)
@@ -964,7 +969,8 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
             return;
         }
     }
-    const int R = m <= 4 ? CFH_GEMV_R_SMALL : 4;
+    // 16-row tiles up to M = 4, 32 rows up to M = 8, 64 rows beyond (x is shared by more rows)
+    const int R = m <= 4 ? CFH_GEMV_R_SMALL : m <= 8 ? 2 : 4;
     // longest K first: its workgroups run longest, so they start first
     std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
     Batch b{};
@@ -984,13 +990,16 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
     b.y_bf16 = y_bf16;
     if (tiles == 0) return;
     if (fmt == FMT_INT4) {
-        if (R != 4) launch_lw<FMT_INT4, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        if (R == CFH_GEMV_R_SMALL) launch_lw<FMT_INT4, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        else if (R == 2) launch_lw<FMT_INT4, 2>(lw, b, tiles, max_lds, st);
         else launch_lw<FMT_INT4, 4>(lw, b, tiles, max_lds, st);
     } else if (fmt == FMT_NF4) {
-        if (R != 4) launch_lw<FMT_NF4, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        if (R == CFH_GEMV_R_SMALL) launch_lw<FMT_NF4, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        else if (R == 2) launch_lw<FMT_NF4, 2>(lw, b, tiles, max_lds, st);
         else launch_lw<FMT_NF4, 4>(lw, b, tiles, max_lds, st);
     } else {
-        if (R != 4) launch_lw<FMT_INT8, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        if (R == CFH_GEMV_R_SMALL) launch_lw<FMT_INT8, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        else if (R == 2) launch_lw<FMT_INT8, 2>(lw, b, tiles, max_lds, st);
         else launch_lw<FMT_INT8, 4>(lw, b, tiles, max_lds, st);
     }
     check_launch("skinny_qgemm");
