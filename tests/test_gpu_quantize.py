@@ -92,6 +92,32 @@ def test_int4g_bit_exact(cuda, group, n, k):
     assert np.array_equal(d.view(np.uint32), d_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("group", [16, 128, 256])
+def test_int4g_exact_ties_every_scale_decade(cuda, group):
+    """Groups whose quotients x / s are exact halves (k + 0.5) and their neighbours one ulp
+    away, for scales s from f16 subnormals to 2^15: the kernel's reciprocal-and-correction
+    quotient must round every tie exactly as x / s does (round half to even)."""
+    rng = np.random.default_rng(5)
+    hs = np.concatenate([np.array([1, 2, 3, 0x3ff, 0x400, 0x3c00, 0x7bff], np.uint16),
+                         rng.integers(1, 0x7c00, 120).astype(np.uint16)])
+    svals = hs.view(np.float16).astype(np.float32)
+    rows = []
+    for sv in svals:
+        g = np.zeros(group, np.float32)
+        g[1] = np.float32(15) * sv                      # range 15 s: the scale is exactly s
+        ties = (np.arange(group - 2) % 15 + np.float32(0.5)).astype(np.float32) * sv
+        step = (np.arange(group - 2) % 3 - 1).astype(np.int32)  # -1, 0, +1 ulp
+        g[2:] = (ties.view(np.int32) + step).view(np.float32)
+        g[2:] = np.clip(g[2:], 0, g[1])
+        rows.append(np.tile(g, 2))
+    w = np.stack(rows).astype(np.float32)
+    c_ref, s_ref, z_ref = O.quantize_int4g(w, group)
+    p = ops.quantize_int4g(torch.from_numpy(w).to(cuda), group)
+    assert np.array_equal(_u32(p.codes), c_ref)
+    assert np.array_equal(p.scales.cpu().numpy().view(np.uint16), s_ref)
+    assert np.array_equal(_u32(p.zeros), z_ref)
+
+
 def test_int4g_edge_groups(cuda):
     w = np.zeros((4, 256), np.float32)
     w[1, :] = 0.25
