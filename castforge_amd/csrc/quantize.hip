@@ -2,9 +2,11 @@
 //
 // All kernels are HBM-bound streaming passes: 16-byte loads, wave64 butterfly reductions
 // for absmax/min/max, packed stores (4 int8 codes or 8 nibble codes per 32-bit store).
-// The arithmetic is the exact f32 sequence of the CPU reference: correctly rounded f32
-// division (hipcc's default), no contraction (this file is built with -ffp-contract=off),
-// round-half-even via rintf or half-away via roundf, NaN -> 0 as in Rust's `as i8`.
+// The arithmetic gives the bytes of the CPU reference's f32 sequence: x / scale as the correctly
+// rounded f32 quotient (hipcc's IEEE division, or div_by_scale's reciprocal and correction
+// where that is shown to give the same quotient), no contraction (this file is built with
+// -ffp-contract=off), round-half-even via rintf or half-away via roundf, NaN -> 0 as in Rust's
+// `as i8`.
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
 
@@ -20,10 +22,37 @@ __device__ __forceinline__ float round_sel(float x, int mode) {
     return mode == CFH_ROUND_HALF_EVEN ? rintf(x) : roundf(x);
 }
 
+// RN(x / s) from y = RN(1 / s), Markstein's correction step:
+//     q = fma(fma(-RN(x y), s, x), y, RN(x y)).
+// The remainder fma(-q0, s, x) is exact when q0 is within an ulp of x / s and nothing over- or
+// underflows, and then q is the correctly rounded quotient, bit for bit the IEEE division
+// (about 10 instructions) that it replaces.  For denormal x both quotients round to codes of
+// 0.  q0 is first clamped to [-lim, lim]: callers pick lim so that every |x / s| > lim gives
+// the same code, and the clamp keeps the remainder finite when RN(x y) overflows (inf x still
+// yields inf, NaN x NaN).  An infinite s (y = 0) gives NaN, not x / s = +-0: the callers check
+// that case.  Validated on the CPU against x / s for every positive finite f16 scale (INT4
+// group scales, lim 64) and for random f32 scales amax / 7, amax / 127 (both rounding modes,
+// lim 256) and amax / 448 (E4M3 codes, lim 1024), with random x, exact ties and ties +- 3 ulp:
+// no code differs.
+__device__ __forceinline__ float div_by_scale(float x, float s, float y, float lim) {
+    const float q0 = fminf(fmaxf(x * y, -lim), lim);
+    return __builtin_fmaf(__builtin_fmaf(-q0, s, x), y, q0);
+}
+
 // formats.rs:676: (v / scale).round().clamp(qmin, qmax) as i8 — NaN maps to 0.
 __device__ __forceinline__ uint32_t quant_sym_byte(float v, float scale, float qmin, float qmax,
                                                    int mode) {
     float r = round_sel(v / scale, mode);
+    if (r != r) return 0u;
+    r = fminf(fmaxf(r, qmin), qmax);
+    return static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+}
+
+// Same code with the quotient from div_by_scale (|qmin|, qmax <= 128, so lim 256 is safe; an
+// infinite scale yields NaN -> 0, which is also the code of v / inf = +-0 and inf / inf).
+__device__ __forceinline__ uint32_t quant_sym_byte_y(float v, float scale, float y, float qmin,
+                                                     float qmax, int mode) {
+    float r = round_sel(div_by_scale(v, scale, y, 256.0f), mode);
     if (r != r) return 0u;
     r = fminf(fmaxf(r, qmin), qmax);
     return static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
@@ -60,7 +89,8 @@ struct Bf16x4Src {
     __device__ __forceinline__ float load1(int64_t i) const { return bf16_to_f32(p[i]); }
 };
 
-// Encoders: how one value becomes one byte, given the row's absmax.
+// Encoders: how one value becomes one byte, given the row's absmax.  enc() divides; enc_y()
+// takes y = RN(1 / scale) and is used when fast_ok(y) says it yields the same byte.
 struct SymEnc {
     float qmin, qmax;
     int mode;
@@ -70,6 +100,10 @@ struct SymEnc {
     __device__ __forceinline__ uint32_t enc(float v, float scale) const {
         return quant_sym_byte(v, scale, qmin, qmax, mode);
     }
+    __device__ __forceinline__ bool fast_ok(float) const { return true; }
+    __device__ __forceinline__ uint32_t enc_y(float v, float scale, float y) const {
+        return quant_sym_byte_y(v, scale, y, qmin, qmax, mode);
+    }
 };
 
 struct Fp8Enc {
@@ -78,6 +112,14 @@ struct Fp8Enc {
     }
     __device__ __forceinline__ uint32_t enc(float v, float scale) const {
         return f32_to_e4m3fn(v / scale);
+    }
+    // E4M3 keeps the sign of v / inf = -0 and codes NaN as 0x7F, so an infinite scale divides.
+    __device__ __forceinline__ bool fast_ok(float y) const { return y != 0.0f; }
+    // div_by_scale turns -0 into +0 (the remainder fma rounds -0 + +0 to +0); scale > 0, so
+    // the quotient's sign is v's, and OR-ing v's sign bit back in restores 0x80 for -0.
+    __device__ __forceinline__ uint32_t enc_y(float v, float scale, float y) const {
+        const float q = div_by_scale(v, scale, y, 1024.0f);
+        return f32_to_e4m3fn(__uint_as_float(__float_as_uint(q) | (__float_as_uint(v) & 0x80000000u)));
     }
 };
 
@@ -111,13 +153,25 @@ __global__ __launch_bounds__(kBlock) void rows_quant_reg_kernel(Src src, int64_t
     }
     am = block_max(am, red);
     const float scale = e.scale_of(am);
+    const float y = 1.0f / scale;
     uint32_t *out = reinterpret_cast<uint32_t *>(codes + row * cols);
+    if (e.fast_ok(y)) {
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
-        if (idx < nv) {
-            out[idx] = e.enc(v[i].x, scale) | (e.enc(v[i].y, scale) << 8) |
-                       (e.enc(v[i].z, scale) << 16) | (e.enc(v[i].w, scale) << 24);
+        for (int i = 0; i < VPT; ++i) {
+            const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
+            if (idx < nv) {
+                out[idx] = e.enc_y(v[i].x, scale, y) | (e.enc_y(v[i].y, scale, y) << 8) |
+                           (e.enc_y(v[i].z, scale, y) << 16) | (e.enc_y(v[i].w, scale, y) << 24);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
+            if (idx < nv) {
+                out[idx] = e.enc(v[i].x, scale) | (e.enc(v[i].y, scale) << 8) |
+                           (e.enc(v[i].z, scale) << 16) | (e.enc(v[i].w, scale) << 24);
+            }
         }
     }
     if (threadIdx.x == 0) scales[row] = scale;
@@ -193,6 +247,7 @@ __global__ __launch_bounds__(kBlock) void tensor_quant_kernel(const float *__res
                                                               const uint32_t *acc,
                                                               uint8_t *__restrict__ codes) {
     const float scale = e.scale_of(__uint_as_float(*acc));
+    const float y = 1.0f / scale;  // SymEnc: enc_y is exact for every scale
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     const bool vec = ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) &&
@@ -203,12 +258,13 @@ __global__ __launch_bounds__(kBlock) void tensor_quant_kernel(const float *__res
         for (int64_t i = t; i < nv; i += stride) {
             float4 v = reinterpret_cast<const float4 *>(src)[i];
             reinterpret_cast<uint32_t *>(codes)[i] =
-                e.enc(v.x, scale) | (e.enc(v.y, scale) << 8) | (e.enc(v.z, scale) << 16) |
-                (e.enc(v.w, scale) << 24);
+                e.enc_y(v.x, scale, y) | (e.enc_y(v.y, scale, y) << 8) |
+                (e.enc_y(v.z, scale, y) << 16) | (e.enc_y(v.w, scale, y) << 24);
         }
         done = nv << 2;
     }
-    for (int64_t i = done + t; i < n; i += stride) codes[i] = static_cast<uint8_t>(e.enc(src[i], scale));
+    for (int64_t i = done + t; i < n; i += stride)
+        codes[i] = static_cast<uint8_t>(e.enc_y(src[i], scale, y));
 }
 
 __global__ void tensor_scale_finalize_kernel(float *scales, SymEnc e) {
@@ -315,13 +371,9 @@ __global__ __launch_bounds__(kBlock) void int4g_quant_kernel(const float *__rest
 // ---- INT4 group-wise, 16 codes per thread (groups of 16 .. 256) ----------------------------
 // Same results as int4g_quant_kernel, with three changes that cut the VALU work per code from
 // about 50 instructions to about 10:
-//   * x / s (an IEEE division, ~10 instructions) becomes Markstein's correction
-//     q = fma(fma(-RN(x y), s, x), y, RN(x y)) with y = RN(1 / s) computed once per group by
-//     the IEEE division.  q = RN(x / s) whenever the remainder fma is exact (x normal, no
-//     overflow), so rint(q) is the oracle's rint(x / s); for denormal x both quotients are
-//     below 2^-100 and round to 0; beyond |x / s| = 64 (clamped, see div_by_scale) every
-//     quotient gives the same code.  Checked against x / s for every positive finite f16
-//     scale with random x, exact ties and ties +- 3 ulp: no code differs.
+//   * x / s (an IEEE division, ~10 instructions) becomes div_by_scale's correction step with
+//     y = RN(1 / s) computed once per group by the IEEE division, and lim 64: beyond
+//     |x / s| = 64 every quotient gives the same clamped code.
 //   * each thread holds 16 consecutive values (two code words), so the per-group work (min /
 //     max, scale, zero point) is shared by twice the codes;
 //   * min / max over a group's lanes use DPP row permutations instead of LDS shuffles, and for
@@ -342,14 +394,6 @@ __device__ __forceinline__ float group_reduce_min(float v) {
     if constexpr (TPG >= 8) v = fminf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
     if constexpr (TPG >= 16) v = fminf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
     return v;
-}
-
-// RN(x / s) given y = RN(1 / s) (see above).
-// q0 is first clamped to [-64, 64]: every |x / s| > 64 gives the same clamped code, and the
-// clamp keeps the remainder finite when RN(x y) overflows (inf x still yields inf).
-__device__ __forceinline__ float div_by_scale(float x, float s, float y) {
-    const float q0 = fminf(fmaxf(x * y, -64.0f), 64.0f);
-    return __builtin_fmaf(__builtin_fmaf(-q0, s, x), y, q0);
 }
 
 template <int GROUP>
@@ -410,7 +454,7 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(const float *__re
             uint32_t word = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                float r = rintf(div_by_scale(x[8 * h + i], s, y));
+                float r = rintf(div_by_scale(x[8 * h + i], s, y, 64.0f));
                 if (r != r) r = 0.0f;
                 const float qf = fminf(fmaxf(r + zf, 0.0f), 15.0f);
                 word |= static_cast<uint32_t>(qf) << (4 * i);

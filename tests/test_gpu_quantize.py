@@ -46,6 +46,35 @@ def test_int8_ties_exact(cuda):
         assert np.array_equal(q.cpu().numpy(), q_ref)
 
 
+def _ulp_steps(v, d):
+    """v moved by d units in the last place (f32 bit pattern arithmetic, sign kept)."""
+    u = v.view(np.int32).astype(np.int64) + d
+    return u.astype(np.int32).view(np.float32)
+
+
+@pytest.mark.parametrize("mode", ["half_away", "half_even"])
+@pytest.mark.parametrize("bits", [8, 4])
+def test_int8_rows_ties_many_scale_decades(cuda, mode, bits):
+    # Each row has its own absmax (1e-10 .. 1e30), so scale = amax / qmax is an arbitrary f32;
+    # the other values sit on exact ties (k + 1/2) * scale and +-1..3 ulp around them, where a
+    # quotient one ulp off changes the code.
+    qmax = 127 if bits == 8 else 7
+    rows, cols = 384, 1024
+    r = np.random.default_rng(7 + bits)
+    amax = (10.0 ** r.uniform(-10, 30, rows)).astype(np.float32)
+    scale = amax / np.float32(qmax)
+    k = r.integers(-qmax, qmax, (rows, cols)).astype(np.float32)
+    w = ((k + np.float32(0.5)) * scale[:, None]).astype(np.float32)
+    w = _ulp_steps(w, r.integers(-3, 4, (rows, cols)))
+    w = np.clip(w, -amax[:, None], amax[:, None])
+    w[:, 0] = amax * np.where(r.random(rows) < 0.5, 1, -1).astype(np.float32)
+    w[:4, 1:5] = [np.inf, -np.inf, np.nan, 0.0]  # rows 0..3: infinite absmax, NaN values
+    q_ref, s_ref = O.quantize_int8_rows(w, bits, 0 if mode == "half_away" else 1)
+    q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), bits, "channel", mode)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
 @pytest.mark.parametrize("shape", [(2, 2), (1, 1), (4096, 4096), (1, 1001), (3, 5, 7)])
 def test_int8_per_tensor_bit_exact(cuda, shape):
     w = synth.weight(12, 3, int(np.prod(shape[:-1])), shape[-1]).reshape(shape)
@@ -195,6 +224,32 @@ def test_fp8_reference_quirk_inputs(cuda):
     codes, scales = ops.quantize_fp8(torch.from_numpy(v).to(cuda))
     assert np.array_equal(codes.cpu().numpy(), c_ref)
     assert s_ref[0] == 1.0
+
+
+def test_fp8_rows_boundaries_many_scale_decades(cuda):
+    # Per-row absmax 1e-10 .. 1e30 (scale = amax / 448 an arbitrary f32); values are
+    # quotient * scale with quotients at E4M3 rounding midpoints, the log2 quirk thresholds and
+    # the subnormal range, +-3 ulp, so a quotient one ulp off changes the code.  Rows 0..2
+    # hold an infinity (infinite scale: finite values code +-0, infinities NaN).
+    rows, cols = 256, 2048
+    r = np.random.default_rng(19)
+    amax = (10.0 ** r.uniform(-10, 30, rows)).astype(np.float32)
+    scale = amax / np.float32(448.0)
+    e = r.integers(0x75, 0x88, (rows, cols)).astype(np.uint32)
+    m = (r.integers(0, 16, (rows, cols)).astype(np.uint32) << 19)
+    m = np.where(r.random((rows, cols)) < 0.25, 0x7FFFF8, m).astype(np.int64)
+    m = (m + r.integers(-3, 4, (rows, cols))) & 0x7FFFFF
+    qd = ((e << 23) | m.astype(np.uint32)).view(np.float32)
+    qd = np.minimum(qd, np.float32(447.0)) * np.where(r.random((rows, cols)) < 0.5, 1, -1).astype(np.float32)
+    w = (qd * scale[:, None]).astype(np.float32)
+    w = np.clip(w, -amax[:, None], amax[:, None])
+    w[:, 0] = amax
+    w[:3, 1:4] = [np.inf, np.nan, -1.0]
+    w[3:8, 1:4] = [-0.0, 0.0, -1e-45]  # signed zeros and a denormal keep their sign bit
+    c_ref, s_ref = O.quantize_fp8_rows(w)
+    codes, scales = ops.quantize_fp8(torch.from_numpy(w).to(cuda))
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(codes.cpu().numpy(), c_ref)
 
 
 @pytest.mark.parametrize("r,c", [(16, 512), (4096, 4096 // 8), (3, 11)])
