@@ -248,11 +248,13 @@ def main():
         # quantize over the f32 block (809 MB in, > MALL)
         nel = sum(n * k for (_, n, k) in synth.LLAMA7B_BLOCK)
         nrows = sum(n for (_, n, k) in synth.LLAMA7B_BLOCK)
-        st = time_steps(lambda i: [ops.quantize_int4g(w, 128) for w in block_f32], 10, 2)
+        # the batched entry points: one launch per column count over the block (the same codes
+        # as one call per matrix)
+        st = time_steps(lambda i: ops.quantize_int4g_batched(block_f32, 128), 10, 2)
         q4_bytes = nel * 4 + nel // 2 + sum(n * (((k + 127) // 128 + 7) // 8) * (16 + 4)
                                             for (_, n, k) in synth.LLAMA7B_BLOCK)
         components["quantize_int4g128_GBps"] = round(q4_bytes / (st * 1e-3) / 1e9, 1)
-        st = time_steps(lambda i: [ops.quantize_int8(w, 8, "channel", "half_even") for w in block_f32], 10, 2)
+        st = time_steps(lambda i: ops.quantize_int8_batched(block_f32, 8, "half_even"), 10, 2)
         components["quantize_int8_channel_GBps"] = round((nel * 5 + nrows * 4) / (st * 1e-3) / 1e9, 1)
         log(f"[bench] quantize int4g {components['quantize_int4g128_GBps']} GB/s, "
             f"int8 {components['quantize_int8_channel_GBps']} GB/s")

@@ -71,7 +71,45 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return r;
 }
 
+// Up to kQSets matrices with the same column count, quantized by one launch: their rows are
+// concatenated in launch order and each workgroup finds its matrix from its row.
+constexpr int kQSets = 8;
+template <class T>
+struct RowSets {
+    const T *src[kQSets];
+    const float *in_scale[kQSets];  // INT4: AWQ per-column pre-scale, or null
+    void *codes[kQSets];
+    void *scales[kQSets];
+    uint32_t *zeros[kQSets];        // INT4
+    int64_t row_end[kQSets];        // rows of matrices 0..i
+    int count;
+    // matrix of launch row r, and r's row within it
+    __device__ __forceinline__ int find(int64_t r, int64_t &local) const {
+        int p = 0;
+#pragma unroll
+        for (int i = 1; i < kQSets; ++i)
+            if (i < count && r >= row_end[i - 1]) p = i;
+        local = r - (p > 0 ? row_end[p - 1] : 0);
+        return p;
+    }
+};
+
+template <class T>
+RowSets<T> one_set(const T *src, const float *in_scale, void *codes, void *scales, uint32_t *zeros,
+                   int64_t rows) {
+    RowSets<T> s{};
+    s.src[0] = src;
+    s.in_scale[0] = in_scale;
+    s.codes[0] = codes;
+    s.scales[0] = scales;
+    s.zeros[0] = zeros;
+    s.row_end[0] = rows;
+    s.count = 1;
+    return s;
+}
+
 struct F32x4Src {
+    using elem = float;
     const float *p;
     __device__ __forceinline__ float4 load4(int64_t i) const {
         return reinterpret_cast<const float4 *>(p)[i];
@@ -80,6 +118,7 @@ struct F32x4Src {
 };
 
 struct Bf16x4Src {
+    using elem = uint16_t;
     const uint16_t *p;
     __device__ __forceinline__ float4 load4(int64_t i) const {
         uint2 u = reinterpret_cast<const uint2 *>(p)[i];
@@ -134,11 +173,14 @@ __device__ __forceinline__ float amax4(float a, float4 v) {
 // One workgroup per row; the row stays in registers (VPT float4 per thread), so HBM sees
 // each input byte once.  Requires cols % 4 == 0 and 16-byte aligned rows.
 template <int VPT, class Src, class Enc>
-__global__ __launch_bounds__(kBlock) void rows_quant_reg_kernel(Src src, int64_t cols, Enc e,
-                                                                 uint8_t *__restrict__ codes,
-                                                                 float *__restrict__ scales) {
+__global__ __launch_bounds__(kBlock) void rows_quant_reg_kernel(RowSets<typename Src::elem> sets,
+                                                                 int64_t cols, Enc e) {
     __shared__ float red[kBlock / 64];
-    const int64_t row = blockIdx.x;
+    int64_t row;
+    const int set = sets.find(blockIdx.x, row);
+    const Src src{sets.src[set]};
+    uint8_t *__restrict__ codes = static_cast<uint8_t *>(sets.codes[set]);
+    float *__restrict__ scales = static_cast<float *>(sets.scales[set]);
     const int64_t nv = cols >> 2;
     const int64_t base = row * nv;
     float4 v[VPT];
@@ -194,27 +236,41 @@ __global__ __launch_bounds__(kBlock) void rows_quant_generic_kernel(Src src, int
     if (threadIdx.x == 0) scales[row] = scale;
 }
 
+// The register kernel over a set of matrices (cols % 4 == 0, every row 16-byte aligned).
+template <class Src, class Enc>
+void launch_rows_quant_sets(const RowSets<typename Src::elem> &sets, int64_t rows, int64_t cols,
+                            Enc e, hipStream_t st) {
+    if (rows == 0) return;
+    require(rows <= 0x7fffffff, "too many rows for one launch");
+    const int64_t nv = cols / 4;
+    require(nv <= 16 * kBlock, "row too long for the register kernel");
+    dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
+    if (nv <= 1 * kBlock)
+        rows_quant_reg_kernel<1, Src><<<grid, block, 0, st>>>(sets, cols, e);
+    else if (nv <= 2 * kBlock)
+        rows_quant_reg_kernel<2, Src><<<grid, block, 0, st>>>(sets, cols, e);
+    else if (nv <= 4 * kBlock)
+        rows_quant_reg_kernel<4, Src><<<grid, block, 0, st>>>(sets, cols, e);
+    else if (nv <= 8 * kBlock)
+        rows_quant_reg_kernel<8, Src><<<grid, block, 0, st>>>(sets, cols, e);
+    else if (nv <= 12 * kBlock)
+        rows_quant_reg_kernel<12, Src><<<grid, block, 0, st>>>(sets, cols, e);
+    else
+        rows_quant_reg_kernel<16, Src><<<grid, block, 0, st>>>(sets, cols, e);
+    check_launch("rows_quant");
+}
+
 template <class Src, class Enc>
 void launch_rows_quant(Src src, bool vec_ok, int64_t rows, int64_t cols, Enc e, uint8_t *codes,
                        float *scales, hipStream_t st) {
     if (rows == 0) return;
     require(rows <= 0x7fffffff, "too many rows for one launch");
-    const int64_t nv = cols / 4;
+    if (vec_ok && cols / 4 <= 16 * kBlock) {
+        launch_rows_quant_sets<Src>(one_set(src.p, nullptr, codes, scales, nullptr, rows), rows, cols, e, st);
+        return;
+    }
     dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
-    if (vec_ok && nv <= 1 * kBlock)
-        rows_quant_reg_kernel<1><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
-    else if (vec_ok && nv <= 2 * kBlock)
-        rows_quant_reg_kernel<2><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
-    else if (vec_ok && nv <= 4 * kBlock)
-        rows_quant_reg_kernel<4><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
-    else if (vec_ok && nv <= 8 * kBlock)
-        rows_quant_reg_kernel<8><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
-    else if (vec_ok && nv <= 12 * kBlock)
-        rows_quant_reg_kernel<12><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
-    else if (vec_ok && nv <= 16 * kBlock)
-        rows_quant_reg_kernel<16><<<grid, block, 0, st>>>(src, cols, e, codes, scales);
-    else
-        rows_quant_generic_kernel<<<grid, block, 0, st>>>(src, cols, e, codes, scales);
+    rows_quant_generic_kernel<<<grid, block, 0, st>>>(src, cols, e, codes, scales);
     check_launch("rows_quant");
 }
 
@@ -397,18 +453,19 @@ __device__ __forceinline__ float group_reduce_min(float v) {
 }
 
 template <int GROUP>
-__global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(const float *__restrict__ src,
-                                                               const float *__restrict__ in_scale,
-                                                               int64_t cols,
-                                                               uint32_t *__restrict__ codes,
-                                                               uint16_t *__restrict__ scales,
-                                                               uint32_t *__restrict__ zeros) {
+__global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> sets, int64_t cols) {
     constexpr int TPG = GROUP / 16;   // threads per group
     constexpr int T = 8 * TPG;        // threads per task (8 groups: one zero-point word)
     constexpr int TPB = kBlock / T;   // tasks per block
     __shared__ uint32_t zpart[kBlock / 64];
     // one row per grid row: the row's bases are uniform and every offset below is 32-bit
-    const int64_t row = blockIdx.y;
+    int64_t row;
+    const int set = sets.find(blockIdx.y, row);
+    const float *__restrict__ src = sets.src[set];
+    const float *__restrict__ in_scale = sets.in_scale[set];
+    uint32_t *__restrict__ codes = static_cast<uint32_t *>(sets.codes[set]);
+    uint16_t *__restrict__ scales = static_cast<uint16_t *>(sets.scales[set]);
+    uint32_t *__restrict__ zeros = sets.zeros[set];
     const uint32_t KW = static_cast<uint32_t>(cols >> 3);
     const uint32_t G = static_cast<uint32_t>((cols + GROUP - 1) / GROUP), ZW = (G + 7) >> 3, GP = ZW * 8;
     const float *rsrc = src + row * cols;
@@ -632,7 +689,8 @@ int32_t castforge_hip_quantize_int8(const float *src, int64_t rows, int64_t cols
                 "granularity must be CFH_GRAN_TENSOR or CFH_GRAN_CHANNEL");
         require(round_mode == CFH_ROUND_HALF_AWAY || round_mode == CFH_ROUND_HALF_EVEN,
                 "round_mode must be CFH_ROUND_HALF_AWAY or CFH_ROUND_HALF_EVEN");
-        require(scales != nullptr, "scales must not be NULL");
+        // per channel, zero rows have no scales to write
+        require(scales != nullptr || (granularity == CFH_GRAN_CHANNEL && rows == 0), "scales must not be NULL");
         const int64_t n = rows * cols;
         require(n == 0 || (src && codes), "src and codes must not be NULL");
         // formats.rs:654-660: bits == 4 -> [-8, 7], anything else -> [-128, 127]
@@ -679,6 +737,22 @@ int32_t castforge_hip_dequantize_int8(const int8_t *codes, const float *scales, 
 
 namespace cfh {
 namespace {
+// int4g_quant16_kernel over a set of matrices (rows <= 65535 in total, group 16..256).
+void launch_int4g16(const RowSets<float> &sets, int64_t rows, int64_t cols, int64_t group, hipStream_t st) {
+    // 16 codes per thread: a task (8 groups) takes group / 2 threads; one grid row per row
+    const int64_t G = (cols + group - 1) / group, ZW = (G + 7) / 8;
+    const int64_t tpb = kBlock / (group / 2);
+    dim3 g(static_cast<unsigned>((ZW + tpb - 1) / tpb), static_cast<unsigned>(rows)), b(kBlock);
+    switch (group) {
+    case 16: int4g_quant16_kernel<16><<<g, b, 0, st>>>(sets, cols); break;
+    case 32: int4g_quant16_kernel<32><<<g, b, 0, st>>>(sets, cols); break;
+    case 64: int4g_quant16_kernel<64><<<g, b, 0, st>>>(sets, cols); break;
+    case 128: int4g_quant16_kernel<128><<<g, b, 0, st>>>(sets, cols); break;
+    default: int4g_quant16_kernel<256><<<g, b, 0, st>>>(sets, cols); break;
+    }
+    check_launch("int4g_quant16");
+}
+
 void quantize_int4g_impl(const float *src, const float *in_scale, int64_t rows, int64_t cols, int64_t group,
                          uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros, void *stream) {
     check_shape(rows, cols);
@@ -695,17 +769,7 @@ void quantize_int4g_impl(const float *src, const float *in_scale, int64_t rows, 
     hipStream_t st = static_cast<hipStream_t>(stream);
     dim3 b(kBlock);
     if (group >= 16 && CFH_INT4Q16 && rows <= 65535 && cols < (int64_t{1} << 31)) {
-        // 16 codes per thread: a task (8 groups) takes group / 2 threads; one grid row per row
-        const int64_t tpb = kBlock / (group / 2);
-        dim3 g(static_cast<unsigned>((ZW + tpb - 1) / tpb), static_cast<unsigned>(rows));
-        switch (group) {
-        case 16: int4g_quant16_kernel<16><<<g, b, 0, st>>>(src, in_scale, cols, codes, scales_f16, zeros); break;
-        case 32: int4g_quant16_kernel<32><<<g, b, 0, st>>>(src, in_scale, cols, codes, scales_f16, zeros); break;
-        case 64: int4g_quant16_kernel<64><<<g, b, 0, st>>>(src, in_scale, cols, codes, scales_f16, zeros); break;
-        case 128: int4g_quant16_kernel<128><<<g, b, 0, st>>>(src, in_scale, cols, codes, scales_f16, zeros); break;
-        default: int4g_quant16_kernel<256><<<g, b, 0, st>>>(src, in_scale, cols, codes, scales_f16, zeros); break;
-        }
-        check_launch("int4g_quant16");
+        launch_int4g16(one_set(src, in_scale, codes, scales_f16, zeros, rows), rows, cols, group, st);
         return;
     }
     const int64_t tpb = kBlock / group;
@@ -721,6 +785,85 @@ void quantize_int4g_impl(const float *src, const float *in_scale, int64_t rows, 
     default: int4g_quant_kernel<256><<<g, b, 0, st>>>(src, in_scale, rows, cols, codes, scales_f16, zeros); break;
     }
     check_launch("int4g_quant");
+}
+
+// INT8 symmetric per-channel of one matrix (the castforge_hip_quantize_int8 channel path).
+void quantize_int8_rows(const float *src, int64_t rows, int64_t cols, SymEnc e, int8_t *codes,
+                        float *scales, hipStream_t st) {
+    const bool vec = (cols % 4 == 0) && aligned(src, 16) && aligned(codes, 4);
+    launch_rows_quant(F32x4Src{src}, vec, rows, cols, e, reinterpret_cast<uint8_t *>(codes), scales, st);
+}
+
+// Batched quantize: the problems are grouped by column count (in order of first appearance);
+// each group is quantized by as few launches as possible (at most kQSets matrices, and for
+// INT4 at most 65535 rows, per launch).  A matrix the batched kernels cannot take (alignment,
+// row length, group size) is quantized on its own by the single-matrix path.
+void quantize_batched(const cfh_quant_problem_t *ps, int32_t count, bool int4, int64_t group,
+                      SymEnc e, hipStream_t st) {
+    require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
+    require(count == 0 || ps != nullptr, "problems must not be NULL");
+    if (int4) require(pow2_in(group, 8, 256), "group must be a power of two in [8, 256]");
+    for (int i = 0; i < count; ++i) {
+        const cfh_quant_problem_t &q = ps[i];
+        check_shape(q.rows, q.cols);
+        require(q.rows == 0 || q.cols == 0 || (q.src && q.codes && q.scales), "problem buffers must not be NULL");
+        if (int4) {
+            require(q.cols % 8 == 0, "cols must be a multiple of 8 (8 codes per 32-bit word)");
+            require(q.rows == 0 || q.cols == 0 || q.zeros, "zeros must not be NULL");
+        } else {
+            require(q.rows == 0 || q.scales, "scales must not be NULL");
+        }
+    }
+    bool done[CFH_MAX_BATCH] = {};
+    for (int i = 0; i < count; ++i) {
+        if (done[i]) continue;
+        const int64_t cols = ps[i].cols;
+        RowSets<float> sets{};
+        int64_t rows = 0;
+        auto flush = [&]() {
+            if (sets.count > 0) {
+                if (int4) launch_int4g16(sets, rows, cols, group, st);
+                else launch_rows_quant_sets<F32x4Src>(sets, rows, cols, e, st);
+            }
+            sets = RowSets<float>{};
+            rows = 0;
+        };
+        for (int j = i; j < count; ++j) {
+            const cfh_quant_problem_t &q = ps[j];
+            if (done[j] || q.cols != cols) continue;
+            done[j] = true;
+            if (int4 && q.rows > 0 && cols > 0) {
+                const bool ok = group >= 16 && CFH_INT4Q16 && q.rows <= 65535 && cols < (int64_t{1} << 31) &&
+                                aligned(q.src, 16) && aligned(q.codes, 4) && aligned(q.scales, 2) && aligned(q.zeros, 4);
+                if (!ok) {
+                    quantize_int4g_impl(q.src, nullptr, q.rows, cols, group, static_cast<uint32_t *>(q.codes),
+                                        static_cast<uint16_t *>(q.scales), q.zeros, st);
+                    continue;
+                }
+                if (rows + q.rows > 65535) flush();
+            } else if (!int4 && q.rows > 0) {
+                const bool ok = cols > 0 && cols % 4 == 0 && cols / 4 <= 16 * kBlock && aligned(q.src, 16) &&
+                                aligned(q.codes, 4) && rows + q.rows <= 0x7fffffff;
+                if (!ok) {
+                    quantize_int8_rows(q.src, q.rows, cols, e, static_cast<int8_t *>(q.codes),
+                                       static_cast<float *>(q.scales), st);
+                    continue;
+                }
+            } else {
+                continue;  // nothing to quantize
+            }
+            if (sets.count == kQSets) flush();
+            sets.src[sets.count] = q.src;
+            sets.in_scale[sets.count] = nullptr;
+            sets.codes[sets.count] = q.codes;
+            sets.scales[sets.count] = q.scales;
+            sets.zeros[sets.count] = q.zeros;
+            rows += q.rows;
+            sets.row_end[sets.count] = rows;
+            ++sets.count;
+        }
+        flush();
+    }
 }
 }  // namespace
 }  // namespace cfh
@@ -835,6 +978,29 @@ int32_t castforge_hip_dequantize_fp8(const uint8_t *codes, const float *scales, 
         dequant_fp8_kernel<<<grid_for(n, kBlock, kGridCap), kBlock, 0, static_cast<hipStream_t>(stream)>>>(
             codes, scales, rows, cols, out);
         check_launch("dequant_fp8");
+    });
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int32_t castforge_hip_quantize_int4g_batched(const cfh_quant_problem_t *problems, int32_t count,
+                                             int64_t group, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        quantize_batched(problems, count, true, group, SymEnc{}, static_cast<hipStream_t>(stream));
+    });
+}
+
+int32_t castforge_hip_quantize_int8_batched(const cfh_quant_problem_t *problems, int32_t count,
+                                            int32_t bits, int32_t round_mode, void *stream,
+                                            char **out_error) {
+    return guarded(out_error, [&] {
+        require(round_mode == CFH_ROUND_HALF_AWAY || round_mode == CFH_ROUND_HALF_EVEN,
+                "round_mode must be CFH_ROUND_HALF_AWAY or CFH_ROUND_HALF_EVEN");
+        // formats.rs:654-660: bits == 4 -> [-8, 7], anything else -> [-128, 127]
+        SymEnc e{bits == 4 ? -8.0f : -128.0f, bits == 4 ? 7.0f : 127.0f, round_mode};
+        quantize_batched(problems, count, false, 0, e, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -34,6 +34,17 @@ class CastForgeHipError(RuntimeError):
         self.message = message
 
 
+class QuantProblem(ctypes.Structure):
+    _fields_ = [
+        ("src", c_void_p),
+        ("rows", c_int64),
+        ("cols", c_int64),
+        ("codes", c_void_p),
+        ("scales", c_void_p),
+        ("zeros", c_void_p),
+    ]
+
+
 class W4A16Problem(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p),
@@ -67,6 +78,8 @@ SIGNATURES = {
     "castforge_hip_gemv_w8a16": (c_int32, [_P, c_int64, c_int64, c_int64, _P, _P, c_int32, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_nf4": (c_int32, [_P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_w4a16_batched": (c_int32, [POINTER(W4A16Problem), c_int32, c_int64, c_int32, _P, _E]),
+    "castforge_hip_quantize_int4g_batched": (c_int32, [POINTER(QuantProblem), c_int32, c_int64, _P, _E]),
+    "castforge_hip_quantize_int8_batched": (c_int32, [POINTER(QuantProblem), c_int32, c_int32, c_int32, _P, _E]),
     "castforge_hip_gemm_fp8": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, c_int32, _P, _E]),
     "castforge_hip_quantize_groupwise": (c_int32, [_P, c_int64, c_int32, c_int64, c_int32, ctypes.c_float, c_int32,
                                                    _P, _P, _P, POINTER(c_int64), _P, _E]),

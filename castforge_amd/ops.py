@@ -5,6 +5,7 @@ streams; every computation happens in libcastforge_hip.so.
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass
 
 import torch
@@ -47,7 +48,7 @@ def quantize_int8(w: torch.Tensor, bits: int = 8, granularity: str = "channel",
     w = _dev(w)
     if w.dtype != torch.float32:
         raise ValueError("quantize_int8 takes float32 weights")
-    rows, cols = (w.shape[0], w[0].numel()) if w.dim() >= 2 else (1, w.numel())
+    rows, cols = (w.shape[0], math.prod(w.shape[1:])) if w.dim() >= 2 else (1, w.numel())
     codes = torch.empty(w.shape, dtype=torch.int8, device=w.device)
     scales = torch.empty(rows if granularity == "channel" else 1, dtype=torch.float32, device=w.device)
     if granularity == "tensor":
@@ -104,6 +105,49 @@ def quantize_int4g(w: torch.Tensor, group: int = 128, in_scale: torch.Tensor | N
         ffi.call("castforge_hip_quantize_int4g_awq", _ptr(w), _ptr(in_scale), n, k, group, _ptr(codes),
                  _ptr(scales), _ptr(zeros), _stream(w))
     return Int4Packed(codes, scales, zeros, n, k, group)
+
+
+def _quant_batch(ws: list[torch.Tensor]) -> list[torch.Tensor]:
+    if len(ws) > ffi.MAX_BATCH:
+        raise ValueError(f"at most {ffi.MAX_BATCH} matrices per batched call")
+    ws = [_dev(w) for w in ws]
+    for w in ws:
+        if w.dtype != torch.float32 or w.dim() != 2:
+            raise ValueError("batched quantize takes 2-D float32 [N, K] weights")
+    return ws
+
+
+def quantize_int4g_batched(ws: list[torch.Tensor], group: int = 128) -> list[Int4Packed]:
+    """quantize_int4g over several matrices in one launch per column count (bit-identical)."""
+    ws = _quant_batch(ws)
+    out, arr = [], (ffi.QuantProblem * max(1, len(ws)))()
+    for i, w in enumerate(ws):
+        n, k = w.shape
+        g = (k + group - 1) // group
+        codes = torch.empty((n, k // 8), dtype=torch.int32, device=w.device)
+        scales = torch.empty((n, (g + 7) // 8 * 8), dtype=torch.float16, device=w.device)
+        zeros = torch.empty((n, (g + 7) // 8), dtype=torch.int32, device=w.device)
+        arr[i] = ffi.QuantProblem(_ptr(w), n, k, _ptr(codes), _ptr(scales), _ptr(zeros))
+        out.append(Int4Packed(codes, scales, zeros, n, k, group))
+    if ws:
+        ffi.call("castforge_hip_quantize_int4g_batched", arr, len(ws), group, _stream(ws[0]))
+    return out
+
+
+def quantize_int8_batched(ws: list[torch.Tensor], bits: int = 8, round: str = "half_even"
+                          ) -> list[tuple[torch.Tensor, torch.Tensor]]:
+    """quantize_int8(granularity="channel") over several matrices in one launch per column count."""
+    ws = _quant_batch(ws)
+    out, arr = [], (ffi.QuantProblem * max(1, len(ws)))()
+    for i, w in enumerate(ws):
+        n, k = w.shape
+        codes = torch.empty((n, k), dtype=torch.int8, device=w.device)
+        scales = torch.empty(n, dtype=torch.float32, device=w.device)
+        arr[i] = ffi.QuantProblem(_ptr(w), n, k, _ptr(codes), _ptr(scales), None)
+        out.append((codes, scales))
+    if ws:
+        ffi.call("castforge_hip_quantize_int8_batched", arr, len(ws), bits, _ROUND[round], _stream(ws[0]))
+    return out
 
 
 def dequantize_int4g(p: Int4Packed) -> torch.Tensor:

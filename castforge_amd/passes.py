@@ -32,7 +32,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import ops
+from . import ffi, ops
 from .ir import Dense, Module, QuantPacked, QuantUniform, TensorRef, TensorType, format_scale
 from .tensor_store import QuantizedI8, QuantizedPacked, TensorEntry
 
@@ -290,8 +290,37 @@ class QuantizePackedPass(Pass):
             return k % 8 == 0
         return True
 
+    def _quantize_many(self, ws: list[torch.Tensor]) -> list:
+        """int8_channel / int4_asym: the batched entry points (one launch per column count);
+        the results are bit-identical to _quantize per matrix."""
+        if self.fmt == "int8_channel":
+            return [QuantizedPacked(self.fmt, c, s, None, 0, tuple(w.shape))
+                    for w, (c, s) in zip(ws, ops.quantize_int8_batched(ws, 8, self.round))]
+        if self.fmt == "int4_asym":
+            return [QuantizedPacked(self.fmt, p.codes, p.scales, p.zeros, self.group, tuple(w.shape))
+                    for w, p in zip(ws, ops.quantize_int4g_batched(ws, self.group))]
+        return [self._quantize(w) for w in ws]
+
     def run(self, module: Module) -> PassResult:
         modified = created = 0
+        pending = []  # (oid, op, val, ty, attr, f32 values), quantized ffi.MAX_BATCH at a time
+
+        def flush():
+            nonlocal modified, created
+            packed = self._quantize_many([v for (*_, v) in pending])
+            for (oid, op, val, ty, attr, _), b in zip(pending, packed):
+                qty = TensorType(ty.shape, QuantPacked(self.fmt, "f32", b.group))
+                key = attr.key if isinstance(attr, TensorRef) else (val.ssa_name or f"q_weight_{modified}")
+                module.tensor_store.insert(TensorEntry(key, qty, b))
+                val.ty = qty
+                op.attributes["value"] = TensorRef(key)
+                modified += 1
+                deq = module.add_op("stablehlo.uniform_dequantize", [val.id], [ty], {},
+                                    [f"{val.ssa_name}_deq" if val.ssa_name else None], after=oid)
+                module.replace_uses(val.id, deq.results[0], skip_op=deq.id)
+                created += 1
+            pending.clear()
+
         for oid, op in list(_const_ops(module)):
             val = module.values[op.results[0]]
             ty = val.ty
@@ -301,17 +330,10 @@ class QuantizePackedPass(Pass):
             vals = module.tensor_store.resolve_f32_attr(attr, ty.num_elements())
             if vals is None:
                 continue
-            b = self._quantize(vals.reshape(ty.shape).contiguous())
-            qty = TensorType(ty.shape, QuantPacked(self.fmt, "f32", b.group))
-            key = attr.key if isinstance(attr, TensorRef) else (val.ssa_name or f"q_weight_{modified}")
-            module.tensor_store.insert(TensorEntry(key, qty, b))
-            val.ty = qty
-            op.attributes["value"] = TensorRef(key)
-            modified += 1
-            deq = module.add_op("stablehlo.uniform_dequantize", [val.id], [ty], {},
-                                [f"{val.ssa_name}_deq" if val.ssa_name else None], after=oid)
-            module.replace_uses(val.id, deq.results[0], skip_op=deq.id)
-            created += 1
+            pending.append((oid, op, val, ty, attr, vals.reshape(ty.shape).contiguous()))
+            if len(pending) == ffi.MAX_BATCH:
+                flush()
+        flush()
         return PassResult(self.name, modified > 0, 0, modified, created)
 
 

@@ -140,6 +140,28 @@ int32_t castforge_hip_quantize_groupwise(const float *src, int64_t n, int32_t bi
 int32_t castforge_hip_quantize_fp8_grid(const float *src, int64_t n, int32_t e5m2, int32_t mxfp8,
                                         int64_t block_size, float *deq, void *stream, char **out_error);
 
+/* Several matrices in as few launches as possible: one per column count (at most 8 matrices,
+ * and for INT4 at most 65535 rows, per launch), e.g. every projection of a decoder block.
+ * Codes, scales and zero points are bit-identical to one castforge_hip_quantize_int4g /
+ * castforge_hip_quantize_int8 (CFH_GRAN_CHANNEL) call per matrix, with the same validation;
+ * a matrix the batched kernels cannot take (alignment, row length) is quantized on its own.
+ * The reference's QuantizeWeightsPass quantizes every constant of the module in turn
+ * (passes/quantize/schemes.rs:301-453); this is that loop in one or two launches. */
+typedef struct cfh_quant_problem_t {
+    const float *src;  /* f32 [rows, cols] */
+    int64_t rows, cols;
+    void *codes;       /* INT4: u32 [rows, cols/8]; INT8: i8 [rows, cols] */
+    void *scales;      /* INT4: f16 [rows, GP]; INT8: f32 [rows] */
+    uint32_t *zeros;   /* INT4: u32 [rows, ceil(G/8)]; INT8: unused */
+} cfh_quant_problem_t;
+
+int32_t castforge_hip_quantize_int4g_batched(const cfh_quant_problem_t *problems, int32_t count,
+                                             int64_t group, void *stream, char **out_error);
+
+int32_t castforge_hip_quantize_int8_batched(const cfh_quant_problem_t *problems, int32_t count,
+                                            int32_t bits, int32_t round_mode, void *stream,
+                                            char **out_error);
+
 /* ---- dequant-fused matmul ----------------------------------------------------------------- */
 /* y[m, n] = sum_k x[m, k] * dequant(W)[n, k]; x bf16 [M, K]; y f32 or bf16 [M, N].
  * Replaces the evaluation of `castforge.fused_qmatmul` (passes/fuse/epilogue.rs:10-94,

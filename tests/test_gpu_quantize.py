@@ -278,3 +278,56 @@ def test_block_int8_channel_and_int4g128_full_size(cuda, name, n, k):
     assert np.array_equal(_u32(p.codes), c_ref)
     assert np.array_equal(p.scales.cpu().numpy().view(np.uint16), sc_ref)
     assert np.array_equal(_u32(p.zeros), z_ref)
+
+
+# --------------------------------------------------------------- batched quantize ----
+def _batch_inputs(cuda):
+    shapes = [(37, 512), (100, 1024), (5, 512), (0, 512), (64, 2048), (3, 11008), (300, 1024)]
+    ws = [torch.from_numpy(_w(200 + i, n, k, specials=(n * k >= 200))).to(cuda) for i, (n, k) in enumerate(shapes)]
+    # one matrix that is not 16-byte aligned (a view one row and 4 columns in): quantized alone
+    base = torch.from_numpy(_w(250, 9, 516)).to(cuda)
+    ws.append(base.view(-1)[4:4 + 8 * 512].view(8, 512))
+    return ws
+
+
+def test_int4g_batched_matches_single(cuda):
+    ws = _batch_inputs(cuda)
+    batched = ops.quantize_int4g_batched(ws, 128)
+    for w, b in zip(ws, batched):
+        s = ops.quantize_int4g(w, 128)
+        assert torch.equal(s.codes, b.codes) and torch.equal(s.zeros, b.zeros)
+        assert torch.equal(s.scales.view(torch.int16), b.scales.view(torch.int16))
+        if w.numel():
+            codes, scales, zeros = O.quantize_int4g(w.cpu().numpy(), 128)
+            assert np.array_equal(b.codes.cpu().numpy().view(np.uint32), codes)
+
+
+@pytest.mark.parametrize("mode", ["half_away", "half_even"])
+def test_int8_batched_matches_single(cuda, mode):
+    ws = _batch_inputs(cuda)
+    batched = ops.quantize_int8_batched(ws, 8, mode)
+    for w, (q, s) in zip(ws, batched):
+        q1, s1 = ops.quantize_int8(w, 8, "channel", mode)
+        assert torch.equal(q, q1)
+        assert torch.equal(s.view(torch.int32), s1.view(torch.int32))
+        if w.numel():
+            q_ref, s_ref = O.quantize_int8_rows(w.cpu().numpy(), 8, 0 if mode == "half_away" else 1)
+            assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_int4g_batched_block_rows_over_grid_limit(cuda):
+    """The 7 block projections: the K = 4096 group has 38400 rows (one launch); splitting at
+    65535 rows is exercised by five 16384-row matrices of the same K."""
+    ws = [torch.from_numpy(synth.weight(300, i, 16384, 256)).to(cuda) for i in range(5)]
+    for w, b in zip(ws, ops.quantize_int4g_batched(ws, 128)):
+        s = ops.quantize_int4g(w, 128)
+        assert torch.equal(s.codes, b.codes) and torch.equal(s.zeros, b.zeros)
+        assert torch.equal(s.scales.view(torch.int16), b.scales.view(torch.int16))
+
+
+def test_batched_quantize_rejects_bad_input(cuda):
+    w = torch.zeros((4, 12), device=cuda)
+    with pytest.raises(Exception, match="multiple of 8"):
+        ops.quantize_int4g_batched([w], 128)
+    with pytest.raises(Exception, match="at most"):
+        ops.quantize_int8_batched([torch.zeros((2, 8), device=cuda)] * 9)
