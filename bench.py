@@ -265,11 +265,8 @@ def main():
         xs8 = [x_for(1, k, tid) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)]
         ys8 = [torch.empty((1, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
 
-        def w8_step(i):
-            for x, (q, s), y in zip(xs8, q8c[i % len(q8c)], ys8):
-                ffi.call("castforge_hip_gemv_w8a16", x.data_ptr(), 1, q.shape[0], q.shape[1], q.data_ptr(),
-                         s.data_ptr(), ffi.GRAN_CHANNEL, y.data_ptr(), ffi.DTYPE_BF16,
-                         torch.cuda.current_stream().cuda_stream)
+        def w8_step(i):  # the 7 projections in one launch, like the W4A16 headline
+            ops.gemv_w8a16_batched(xs8, q8c[i % len(q8c)], ys8, "channel")
         st = time_steps(w8_step, 50, 5)
         w8_bytes = nel + nrows * 4 + sum(2 * k + 2 * n for (_, n, k) in synth.LLAMA7B_BLOCK)
         components["w8a16_gemv_m1_GBps"] = round(w8_bytes / (st * 1e-3) / 1e9, 1)
@@ -282,11 +279,8 @@ def main():
         xsn = [x_for(1, p.k, 4 + j) for j, p in enumerate(nf)]
         ysn = [torch.empty((1, p.n), dtype=torch.bfloat16, device=dev) for p in nf]
 
-        def nf_step(i):
-            for x, p, y in zip(xsn, nfc[i % len(nfc)], ysn):
-                ffi.call("castforge_hip_gemv_nf4", x.data_ptr(), 1, p.n, p.k, p.block, p.codes.data_ptr(),
-                         p.absmax.data_ptr(), y.data_ptr(), ffi.DTYPE_BF16,
-                         torch.cuda.current_stream().cuda_stream)
+        def nf_step(i):  # W_gate / W_up / W_down in one launch
+            ops.gemv_nf4_batched(xsn, nfc[i % len(nfc)], ysn)
         st = time_steps(nf_step, 50, 5)
         nf_bytes = sum(p.nbytes() + 2 * p.k + 2 * p.n for p in nf)
         components["nf4_gemv_m1_GBps"] = round(nf_bytes / (st * 1e-3) / 1e9, 1)

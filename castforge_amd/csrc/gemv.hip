@@ -1131,4 +1131,55 @@ int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, in
     });
 }
 
+int32_t castforge_hip_gemv_w8a16_batched(const cfh_w8a16_problem_t *problems, int32_t count,
+                                         int64_t m, int32_t y_dtype, void *stream,
+                                         char **out_error) {
+    return guarded(out_error, [&] {
+        require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
+        require(count == 0 || problems != nullptr, "problems must not be NULL");
+        require(m >= 1 && m <= 16, "batched GEMV requires 1 <= m <= 16");
+        require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+        Problem ps[kMaxProblems];
+        int used = 0;
+        for (int i = 0; i < count; ++i) {
+            const cfh_w8a16_problem_t &q = problems[i];
+            common_checks(q.x, m, q.n, q.k, q.codes, q.y, y_dtype);
+            require(q.granularity == CFH_GRAN_TENSOR || q.granularity == CFH_GRAN_CHANNEL,
+                    "granularity must be CFH_GRAN_TENSOR or CFH_GRAN_CHANNEL");
+            if (q.n == 0) continue;
+            require(q.k > 0 && q.scales, "problem buffers must not be NULL");
+            Problem p{q.x, q.codes, q.scales, nullptr, q.y, q.n, q.k, 0,
+                      q.granularity == CFH_GRAN_CHANNEL ? 1 : 0, 0, 0};
+            require(skinny_ok(FMT_INT8, p, m), "batched GEMV needs k % 64 == 0 and 16-byte aligned x/codes");
+            ps[used++] = p;
+        }
+        if (used) launch_skinny(FMT_INT8, ps, used, m, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
+    });
+}
+
+int32_t castforge_hip_gemv_nf4_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_t m,
+                                       int32_t y_dtype, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
+        require(count == 0 || problems != nullptr, "problems must not be NULL");
+        require(m >= 1 && m <= 16, "batched GEMV requires 1 <= m <= 16");
+        require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+        Problem ps[kMaxProblems];
+        int used = 0;
+        for (int i = 0; i < count; ++i) {
+            const cfh_nf4_problem_t &q = problems[i];
+            common_checks(q.x, m, q.n, q.k, q.codes, q.y, y_dtype);
+            require(q.block == problems[0].block, "batched problems must share the block size");
+            if (q.n == 0) continue;
+            require(q.k > 0 && q.absmax, "problem buffers must not be NULL");
+            Problem p{q.x, q.codes, q.absmax, nullptr, q.y, q.n, q.k, static_cast<int32_t>(q.block), 1, 0, 0};
+            require(q.block >= 32 && skinny_ok(FMT_NF4, p, m),
+                    "batched GEMV needs block 32, 64 or a power-of-two multiple of 128, k a multiple "
+                    "of the chunk (block 32: 32, 64: 64, else 128) and 16-byte aligned x/codes");
+            ps[used++] = p;
+        }
+        if (used) launch_skinny(FMT_NF4, ps, used, m, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
+    });
+}
+
 }  // extern "C"

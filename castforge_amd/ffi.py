@@ -45,6 +45,30 @@ class QuantProblem(ctypes.Structure):
     ]
 
 
+class W8A16Problem(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p),
+        ("codes", c_void_p),
+        ("scales", c_void_p),
+        ("y", c_void_p),
+        ("n", c_int64),
+        ("k", c_int64),
+        ("granularity", c_int32),
+    ]
+
+
+class Nf4Problem(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p),
+        ("codes", c_void_p),
+        ("absmax", c_void_p),
+        ("y", c_void_p),
+        ("n", c_int64),
+        ("k", c_int64),
+        ("block", c_int64),
+    ]
+
+
 class W4A16Problem(ctypes.Structure):
     _fields_ = [
         ("x", c_void_p),
@@ -78,6 +102,8 @@ SIGNATURES = {
     "castforge_hip_gemv_w8a16": (c_int32, [_P, c_int64, c_int64, c_int64, _P, _P, c_int32, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_nf4": (c_int32, [_P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_w4a16_batched": (c_int32, [POINTER(W4A16Problem), c_int32, c_int64, c_int32, _P, _E]),
+    "castforge_hip_gemv_w8a16_batched": (c_int32, [POINTER(W8A16Problem), c_int32, c_int64, c_int32, _P, _E]),
+    "castforge_hip_gemv_nf4_batched": (c_int32, [POINTER(Nf4Problem), c_int32, c_int64, c_int32, _P, _E]),
     "castforge_hip_quantize_int4g_batched": (c_int32, [POINTER(QuantProblem), c_int32, c_int64, _P, _E]),
     "castforge_hip_quantize_int8_batched": (c_int32, [POINTER(QuantProblem), c_int32, c_int32, c_int32, _P, _E]),
     "castforge_hip_gemm_fp8": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, c_int32, _P, _E]),

@@ -282,6 +282,38 @@ def gemv_w4a16_batched(xs: list[torch.Tensor], ps: list[Int4Packed], ys: list[to
     ffi.call("castforge_hip_gemv_w4a16_batched", arr, len(ps), m, yd, _stream(xs[0]))
 
 
+def gemv_w8a16_batched(xs: list[torch.Tensor], qs: list[tuple[torch.Tensor, torch.Tensor]],
+                       ys: list[torch.Tensor], granularity: str = "channel") -> None:
+    """One launch for several W8A16 problems (codes i8 [n, k], scales f32) with the same M."""
+    if not (len(xs) == len(qs) == len(ys)) or len(qs) > ffi.MAX_BATCH:
+        raise ValueError("xs, qs, ys must have the same length <= 8")
+    m = xs[0].shape[0] if xs else 1
+    arr = (ffi.W8A16Problem * max(1, len(qs)))()
+    for i, (x, (q, s), y) in enumerate(zip(xs, qs, ys)):
+        n, k = q.shape
+        _check_x(x, k)
+        if x.shape[0] != m or y.shape != (m, n):
+            raise ValueError("all problems must share M and y must be [M, n]")
+        arr[i] = ffi.W8A16Problem(_ptr(x), _ptr(q), _ptr(_dev(s)), _ptr(y), n, k, _GRAN[granularity])
+    if qs:
+        ffi.call("castforge_hip_gemv_w8a16_batched", arr, len(qs), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
+
+
+def gemv_nf4_batched(xs: list[torch.Tensor], ps: list["Nf4Packed"], ys: list[torch.Tensor]) -> None:
+    """One launch for several NF4 problems with the same M and block size."""
+    if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
+        raise ValueError("xs, ps, ys must have the same length <= 8")
+    m = xs[0].shape[0] if xs else 1
+    arr = (ffi.Nf4Problem * max(1, len(ps)))()
+    for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
+        _check_x(x, p.k)
+        if x.shape[0] != m or y.shape != (m, p.n):
+            raise ValueError("all problems must share M and y must be [M, n]")
+        arr[i] = ffi.Nf4Problem(_ptr(x), _ptr(p.codes), _ptr(p.absmax), _ptr(y), p.n, p.k, p.block)
+    if ps:
+        ffi.call("castforge_hip_gemv_nf4_batched", arr, len(ps), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
+
+
 # ------------------------------------------------------- reference write-back quantizers ----
 def quantize_groupwise(w: torch.Tensor, bits: int = 4, group_size: int = 32, awq_salient: bool = True,
                        salient_ratio: float = 0.01, round: str = "half_away"

@@ -196,6 +196,32 @@ int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, in
                                          int64_t m, int32_t y_dtype, void *stream,
                                          char **out_error);
 
+/* The same for INT8 (per-channel or per-tensor scales, k % 64 == 0) and NF4 weights (one block
+ * size for the whole batch), e.g. the INT8 block of config 1 or the NF4 MLP of config 3. */
+typedef struct cfh_w8a16_problem_t {
+    const uint16_t *x;     /* bf16 [M, k] */
+    const int8_t *codes;   /* i8 [n, k] */
+    const float *scales;   /* f32 [n] (CFH_GRAN_CHANNEL) or [1] (CFH_GRAN_TENSOR) */
+    void *y;               /* [M, n] */
+    int64_t n, k;
+    int32_t granularity;
+} cfh_w8a16_problem_t;
+
+int32_t castforge_hip_gemv_w8a16_batched(const cfh_w8a16_problem_t *problems, int32_t count,
+                                         int64_t m, int32_t y_dtype, void *stream,
+                                         char **out_error);
+
+typedef struct cfh_nf4_problem_t {
+    const uint16_t *x;      /* bf16 [M, k] */
+    const uint32_t *codes;  /* u32 [n, k/8] */
+    const float *absmax;    /* f32 [n, ceil(k/block)] */
+    void *y;                /* [M, n] */
+    int64_t n, k, block;
+} cfh_nf4_problem_t;
+
+int32_t castforge_hip_gemv_nf4_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_t m,
+                                       int32_t y_dtype, void *stream, char **out_error);
+
 /* FP8 E4M3 W8A8 GEMM: y[m, n] = (sum_k e4m3(qa[m,k]) * e4m3(qw[n,k])) * sa[m] * sw[n], stored
  * as bf16 (RNE) or f32 per y_dtype.
  * qa/sa come from castforge_hip_quantize_fp8 on the activations (per token), qw/sw on the

@@ -105,3 +105,52 @@ def test_empty_and_degenerate(cuda):
     p = ops.quantize_int4g(w, 128)
     y = ops.gemm_w4a16(torch.ones((1, 256), dtype=torch.bfloat16, device=cuda), p, torch.float32)
     assert torch.all(y == 0)
+
+
+@pytest.mark.parametrize("gran", ["channel", "tensor"])
+@pytest.mark.parametrize("m", [1, 4])
+def test_w8a16_batched(cuda, gran, m):
+    """One launch over several INT8 problems: same bits as one call per problem, oracle tolerance."""
+    shapes = [(40, 192), (4096, 4096), (33, 11008), (100, 64)]
+    xs, qs, ys, singles, refs = [], [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        w = synth.weight(400 + i, 1, n, k)
+        xb, x = _x(410 + i, m, k, cuda)
+        q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, gran, "half_even")
+        xs.append(x)
+        qs.append((q, s))
+        ys.append(torch.empty((m, n), dtype=torch.float32, device=cuda))
+        singles.append(ops.gemm_w8a16(x, q, s, gran, torch.float32))
+        sc = s.cpu().numpy()
+        refs.append(O.gemm_w8a16(xb, q.cpu().numpy(), sc if gran == "channel" else np.full(n, sc[0], np.float32)))
+    ops.gemv_w8a16_batched(xs, qs, ys, gran)
+    for y, y1, ref in zip(ys, singles, refs):
+        assert torch.equal(y, y1)
+        _close(y, ref)
+
+
+@pytest.mark.parametrize("block", [64, 32])
+def test_nf4_batched(cuda, block):
+    shapes = [(96, 1024), (11008, 4096), (4096, 11008), (7, 512)]
+    xs, ps, ys, singles, refs = [], [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        w = synth.weight(420 + i, 1, n, k)
+        xb, x = _x(430 + i, 1, k, cuda)
+        p = ops.quantize_nf4(torch.from_numpy(w).to(cuda), block)
+        xs.append(x)
+        ps.append(p)
+        ys.append(torch.empty((1, n), dtype=torch.float32, device=cuda))
+        singles.append(ops.gemm_nf4(x, p, torch.float32))
+        refs.append(O.gemm_nf4(xb, p.codes.cpu().numpy().view(np.uint32), p.absmax.cpu().numpy(), n, k, block))
+    ops.gemv_nf4_batched(xs, ps, ys)
+    for y, y1, ref in zip(ys, singles, refs):
+        assert torch.equal(y, y1)
+        _close(y, ref)
+
+
+def test_nf4_batched_rejects_mixed_blocks(cuda):
+    ps = [ops.quantize_nf4(torch.zeros((16, 256), device=cuda), b) for b in (64, 32)]
+    xs = [torch.zeros((1, 256), dtype=torch.bfloat16, device=cuda)] * 2
+    ys = [torch.empty((1, 16), dtype=torch.float32, device=cuda) for _ in ps]
+    with pytest.raises(Exception, match="block size"):
+        ops.gemv_nf4_batched(xs, ps, ys)
