@@ -511,6 +511,19 @@ __device__ __forceinline__ uint32_t meta_lds_off(uint32_t b, int r) {
     return (p >> 2) * 1024u + ((p & 3u) * 16u + static_cast<uint32_t>(r)) * 16u + (b & 15u);
 }
 
+// Sum over aligned groups of N lanes (N = 4 or 8), every lane of a group receiving it: DPP
+// quad permutations (xor 1, xor 2) and the half-row mirror (lane i <-> 7 - i within 8 lanes,
+// which pairs each quad with the other quad of its 8) instead of LDS permutes.
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    static_assert(N == 4 || N == 8, "group of 4 or 8 lanes");
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    if constexpr (N == 8)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    return v;
+}
+
 // waves per SIMD the split kernel's register budget is sized for (0: the compiler's choice)
 #ifndef CFH_GEMV_SPLIT_WPE
 #define CFH_GEMV_SPLIT_WPE 5
@@ -670,11 +683,8 @@ void skinny_m1_split_kernel(Batch b) {
             }
             *reinterpret_cast<uint4 *>(xw + it * 16) = make_uint4(o[0], o[1], o[2], o[3]);
             *reinterpret_cast<uint4 *>(xw + it * 16 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-#pragma unroll
-            for (int m = 1; m < GPC; m <<= 1) {
-                slo += __shfl_xor(slo, m);
-                shi += __shfl_xor(shi, m);
-            }
+            slo = lane_group_sum<GPC>(slo);
+            shi = lane_group_sum<GPC>(shi);
             if (it % GPC == 0) xsum[it / GPC] = make_float2(1024.0f * slo + 64.0f * shi, slo + shi);
         }
     } else {
