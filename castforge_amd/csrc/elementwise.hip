@@ -97,6 +97,18 @@ unsigned grid_for(int64_t n) {
     return static_cast<unsigned>(b < 8192 ? (b > 0 ? b : 1) : 8192);
 }
 
+// castforge.static_quantize (codegen/eval.rs:1369-1382): (x / sc).round().clamp(-qmax, qmax) * sc
+// in f32; Rust's round is half away from zero (roundf) and its clamp lets NaN through.
+__global__ __launch_bounds__(kBlock) void static_quantize_kernel(const float *__restrict__ x, int64_t n, float sc,
+                                                                 float qmax, float *__restrict__ y) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const float r = roundf(x[i] / sc);
+        const float c = r != r ? r : fminf(fmaxf(r, -qmax), qmax);
+        y[i] = c * sc;
+    }
+}
+
 }  // namespace
 }  // namespace cfh
 
@@ -116,6 +128,19 @@ int32_t castforge_hip_qmatmul_epilogue(float *y, int64_t count, const float *bia
         epilogue_kernel<<<grid_for(count), kBlock, 0, static_cast<hipStream_t>(stream)>>>(y, count, bias, bias_len,
                                                                                         z, z_len, kind);
         check_launch("epilogue");
+    });
+}
+
+int32_t castforge_hip_static_quantize(const float *x, int64_t n, float scale, int32_t bits, float *y,
+                                      void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(n >= 0, "n must be non-negative");
+        require(scale > 0.0f && scale <= 3.4028235e38f, "scale must be positive and finite");
+        if (n == 0) return;
+        require(x && y, "x and y must not be NULL");
+        static_quantize_kernel<<<grid_for(n), kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+            x, n, scale, bits == 4 ? 7.0f : 127.0f, y);
+        check_launch("static_quantize");
     });
 }
 

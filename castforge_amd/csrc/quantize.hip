@@ -744,6 +744,21 @@ int32_t castforge_hip_quantize_int8(const float *src, int64_t rows, int64_t cols
     });
 }
 
+int32_t castforge_hip_absmax_f32(const float *src, int64_t n, float *out, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(n >= 0, "n must be non-negative");
+        require(out != nullptr && (n == 0 || src != nullptr), "buffers must not be NULL");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        uint32_t *acc = reinterpret_cast<uint32_t *>(out);
+        fill_u32_kernel<<<1, 1, 0, st>>>(acc, 0u);
+        check_launch("fill_u32");
+        if (n > 0) {
+            tensor_absmax_kernel<<<grid_for(n / 4 + 1, kBlock, kGridCap), kBlock, 0, st>>>(src, n, acc);
+            check_launch("tensor_absmax");
+        }
+    });
+}
+
 int32_t castforge_hip_dequantize_int8(const int8_t *codes, const float *scales, int64_t rows,
                                       int64_t cols, int32_t granularity, float *out, void *stream,
                                       char **out_error) {

@@ -22,6 +22,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import ops
@@ -173,6 +174,17 @@ class _Evaluator:
                                              bool(op.attributes.get("packed_rhs", False))).reshape(ty.shape)
             elif op.is_op("stablehlo", "composite") and op.attributes.get("name") == "castforge.fused_qmatmul":
                 self.env[res] = self._epilogue(op, self._fused(op)).reshape(ty.shape)
+            elif op.is_op("stablehlo", "composite") and op.attributes.get("name") == "castforge.static_quantize":
+                # eval.rs:1369-1382: a positive float scale attribute as f32, else 1/127; bits
+                # defaults to 8
+                sc = op.attributes.get("scale")
+                if isinstance(sc, float) and not isinstance(sc, bool) and sc > 0.0:
+                    scf = float(np.float32(sc))
+                else:
+                    scf = float(np.float32(1.0) / np.float32(127.0))
+                bits = op.attributes.get("bits", 8)
+                bits = bits if isinstance(bits, int) and not isinstance(bits, bool) else 8
+                self.env[res] = ops.static_quantize(self.env[op.operands[0]].float(), scf, bits).reshape(ty.shape)
             elif op.is_op("stablehlo", "composite") and op.attributes.get("name") == "castforge.fused_matmul_epilogue":
                 rhs = op.operands[1]
                 mm = self._matmul(op.operands[0], self.env[rhs], m.values[rhs].ty.shape,

@@ -111,6 +111,8 @@ SIGNATURES = {
                                                    _P, _P, _P, POINTER(c_int64), _P, _E]),
     "castforge_hip_quantize_fp8_grid": (c_int32, [_P, c_int64, c_int32, c_int32, c_int64, _P, _P, _E]),
     "castforge_hip_qmatmul_epilogue": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, c_int32, _P, _E]),
+    "castforge_hip_static_quantize": (c_int32, [_P, c_int64, ctypes.c_float, c_int32, _P, _P, _E]),
+    "castforge_hip_absmax_f32": (c_int32, [_P, c_int64, _P, _P, _E]),
     "castforge_hip_convert_f32_to_bf16": (c_int32, [_P, c_int64, _P, _P, _E]),
     "castforge_hip_convert_bf16_to_f32": (c_int32, [_P, c_int64, _P, _P, _E]),
     "castforge_hip_transpose": (c_int32, [_P, c_int64, c_int64, c_int32, _P, _P, _E]),

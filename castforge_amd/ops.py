@@ -314,6 +314,30 @@ def gemv_nf4_batched(xs: list[torch.Tensor], ps: list["Nf4Packed"], ys: list[tor
         ffi.call("castforge_hip_gemv_nf4_batched", arr, len(ps), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
 
 
+# ------------------------------------------------------------- static W8A8 (calibrate) ----
+def static_quantize(x: torch.Tensor, scale: float, bits: int = 8) -> torch.Tensor:
+    """castforge.static_quantize (eval.rs:1369-1382): clamp(round(x / scale), +-qmax) * scale
+    in f32 with scale already resolved to f32 (> 0); qmax = 7 for bits == 4, else 127."""
+    x = _dev(x)
+    if x.dtype != torch.float32:
+        raise ValueError("static_quantize takes float32 values")
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    ffi.call("castforge_hip_static_quantize", _ptr(x), x.numel(), float(scale), int(bits), _ptr(y), _stream(x))
+    return y
+
+
+def absmax(x: torch.Tensor) -> float:
+    """max |x| over the non-NaN elements of a float32 tensor (0.0 when empty)."""
+    x = _dev(x)
+    if x.dtype != torch.float32:
+        raise ValueError("absmax takes float32 values")
+    x = x.contiguous()
+    out = torch.empty(1, dtype=torch.float32, device=x.device)
+    ffi.call("castforge_hip_absmax_f32", _ptr(x), x.numel(), _ptr(out), _stream(x))
+    return float(out.item())
+
+
 # ------------------------------------------------------- reference write-back quantizers ----
 def quantize_groupwise(w: torch.Tensor, bits: int = 4, group_size: int = 32, awq_salient: bool = True,
                        salient_ratio: float = 0.01, round: str = "half_away"

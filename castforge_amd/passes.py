@@ -28,6 +28,7 @@ messages.
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import torch
@@ -83,6 +84,7 @@ CATALOG = {
     "fuse-gemm": ["kind"],
     "fuse-dequant-matmul": [],
     "pack-weights": [],
+    "calibrate-quantize": ["bits", "samples"],
 }
 
 
@@ -451,6 +453,91 @@ class LowerMixedPrecisionPass(Pass):
         return PassResult(self.name, created > 0 or modified > 0, 0, modified, created)
 
 
+def calibrate_value_ranges(module: Module, num_samples: int) -> dict[int, float]:
+    """formats.rs:115-182: a static bound on max |value| per SSA value.  Function arguments get
+    the largest synthetic sample scale (0.5 + s / n, at least 0.8); constants their max |x|
+    (at least 1e-5, from the device values); add / subtract add the bounds, multiply multiplies
+    them, dot_general multiplies them by sqrt(K) (K = the lhs's last dimension), tanh gives 1,
+    anything else passes its first operand's bound; every bound is at least 1e-5, and a missing
+    operand bound counts as 1.  f64 throughout, as in the reference."""
+    n = max(num_samples, 1)
+    peak = 0.8
+    for s_ in range(num_samples):
+        peak = max(peak, 0.5 + s_ / n)
+    max_abs: dict[int, float] = {a: peak for a in module.args}
+    for oid in module.block_ops():
+        op = module.ops[oid]
+        if not op.results:
+            continue
+        res = op.results[0]
+        if op.is_op("stablehlo", "constant"):
+            ty = module.values[res].ty
+            attr = op.attributes.get("value")
+            vals = module.tensor_store.resolve_f32_attr(attr, ty.num_elements()) if attr is not None else None
+            max_abs[res] = max(1e-5, ops.absmax(vals.reshape(-1).float())) if vals is not None else 1.0
+            continue
+        in0 = max_abs.get(op.operands[0], 1.0) if op.operands else 1.0
+        in1 = max_abs.get(op.operands[1], 1.0) if len(op.operands) > 1 else 1.0
+        if op.name in ("stablehlo.add", "stablehlo.subtract"):
+            est = in0 + in1
+        elif op.name == "stablehlo.multiply":
+            est = in0 * in1
+        elif op.name == "stablehlo.dot_general" and op.operands:
+            shape = module.values[op.operands[0]].ty.shape
+            k = float(max(int(shape[-1]), 1)) if shape and isinstance(shape[-1], int) else 4.0
+            est = in0 * in1 * math.sqrt(k)
+        elif op.name == "stablehlo.tanh":
+            est = 1.0
+        else:
+            est = in0
+        max_abs[res] = max(est, 1e-5)
+    return max_abs
+
+
+class CalibrateQuantizePass(Pass):
+    """formats.rs:15-113 (`calibrate-quantize`, `quantize(scheme=w8a8|calibrate|static)`): for
+    every dot_general / convolution not yet tagged, whose lhs is f32 / f16 / bf16, a
+    `castforge.static_quantize` composite (scale = lhs bound / qmax, the calibrated bits) is
+    inserted before the op on its lhs, and the op is tagged quant_mode = "w{b}a{b}_static",
+    lhs_scale, rhs_scale, calibration_samples.  The inserted op runs on the GPU
+    (castforge_hip_static_quantize) when the module is evaluated."""
+    name = "calibrate-quantize"
+    description = "Calibrates activation dynamic ranges and inserts static W8A8 quantization scales"
+
+    def __init__(self, bits: int = 8, num_samples: int = 4):
+        self.bits, self.num_samples = bits, num_samples
+
+    def run(self, module: Module) -> PassResult:
+        eff_bits, qmax = (4, 7.0) if self.bits == 4 else (8, 127.0)  # formats.rs:654-660
+        ranges = calibrate_value_ranges(module, max(self.num_samples, 1))
+        created = modified = 0
+        for oid in module.block_ops():
+            op = module.ops.get(oid)
+            if op is None or "quant_mode" in op.attributes:
+                continue
+            if not (op.is_op("stablehlo", "dot_general") or op.is_op("stablehlo", "convolution")):
+                continue
+            if len(op.operands) < 2:
+                continue
+            lhs, rhs = op.operands[0], op.operands[1]
+            lty = module.values[lhs].ty
+            if not isinstance(lty.dtype, str) or lty.dtype not in ("f32", "f16", "bf16"):
+                continue
+            lhs_scale = max(ranges.get(lhs, 1.0), 1e-5) / qmax
+            rhs_scale = max(ranges.get(rhs, 1.0), 1e-5) / qmax
+            q = module.add_op("stablehlo.composite", [lhs], [lty],
+                              {"name": "castforge.static_quantize", "decomposition": "static_quantize_impl",
+                               "scale": lhs_scale, "bits": eff_bits}, before=oid)
+            op.operands[0] = q.results[0]
+            op.attributes["quant_mode"] = f"w{eff_bits}a{eff_bits}_static"
+            op.attributes["lhs_scale"] = lhs_scale
+            op.attributes["rhs_scale"] = rhs_scale
+            op.attributes["calibration_samples"] = int(self.num_samples)
+            created += 1
+            modified += 1
+        return PassResult(self.name, created > 0 or modified > 0, 0, modified, created)
+
+
 class QuantizePass(Pass):
     """schemes.rs:85-153 dispatch."""
     name = "quantize"
@@ -458,7 +545,7 @@ class QuantizePass(Pass):
 
     def __init__(self, scheme="weight", bits=8, min_elements=2, group_size=32, awq_salient=True,
                  salient_ratio=0.01, format="e4m3", mxfp8=True, block_size=32, hadamard=False,
-                 round=None, granularity="tensor", group_given=False, block_given=False):
+                 round=None, granularity="tensor", group_given=False, block_given=False, samples=4):
         self.__dict__.update(locals())
         del self.__dict__["self"]
 
@@ -484,8 +571,9 @@ class QuantizePass(Pass):
                                    min_elements=self.min_elements).run(module)
         elif s in ("fp8_row", "w8a8_fp8"):
             r = QuantizePackedPass("fp8_row", min_elements=self.min_elements).run(module)
-        elif s in ("fp4", "mxfp4", "nvfp4", "e2m1", "w8a8", "calibrate", "static", "smoothquant", "smooth",
-                   "qat", "qat_ste", "ste"):
+        elif s in ("w8a8", "calibrate", "static"):
+            r = CalibrateQuantizePass(self.bits, self.samples).run(module)
+        elif s in ("fp4", "mxfp4", "nvfp4", "e2m1", "smoothquant", "smooth", "qat", "qat_ste", "ste"):
             raise ValueError(f"quantize: scheme `{s}` is not part of the HIP quantized-weight path")
         elif self.granularity in ("channel", "per_channel"):
             r = QuantizePackedPass("int8_channel", 0, self.round or "half_even", self.min_elements).run(module)
@@ -534,6 +622,7 @@ def _quantize_factory(opts: dict[str, str]) -> QuantizePass:
         granularity=opts.get("granularity", "tensor"),
         group_given=group is not None and _usize(group, -1) > 0,
         block_given=block is not None and _usize(block, -1) > 0,
+        samples=_usize(_first(opts, "samples", "num_samples"), 4),
     )
 
 
@@ -674,4 +763,7 @@ def default_registry() -> PassRegistry:
     reg.register("fuse-gemm", FuseGemmPass.description, lambda o: FuseGemmPass(o.get("kind", "all")))
     reg.register("fuse-dequant-matmul", FuseDequantMatmulPass.description, lambda o: FuseDequantMatmulPass())
     reg.register("pack-weights", PackWeightsPass.description, lambda o: PackWeightsPass())
+    reg.register("calibrate-quantize", "Profile-guided static W8A8/W4A8 calibration and quantization",
+                 lambda o: CalibrateQuantizePass(_u8(o.get("bits"), 8),
+                                                 _usize(_first(o, "samples", "num_samples"), 4)))
     return reg

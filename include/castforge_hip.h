@@ -254,6 +254,18 @@ int32_t castforge_hip_convert_f32_to_bf16(const float *src, int64_t n, uint16_t 
 int32_t castforge_hip_convert_bf16_to_f32(const uint16_t *src, int64_t n, float *dst, void *stream,
                                           char **out_error);
 
+/* y[i] = clamp(round_half_away(x[i] / scale), -qmax, qmax) * scale in f32, qmax = 7 for bits == 4
+ * and 127 otherwise, NaN kept: the `castforge.static_quantize` op that calibrate-quantize
+ * (quantize(scheme=w8a8), passes/quantize/formats.rs:15-113) inserts before each matmul's
+ * activations, evaluated as codegen/eval.rs:1369-1382 does.  scale is the attribute already
+ * resolved to f32 (> 0). */
+int32_t castforge_hip_static_quantize(const float *x, int64_t n, float scale, int32_t bits, float *y,
+                                      void *stream, char **out_error);
+
+/* *out = max |src[i]| over the non-NaN elements (0 for n == 0), written on the device: the
+ * constant ranges of calibrate-quantize's calibrate_value_ranges (formats.rs:135-150). */
+int32_t castforge_hip_absmax_f32(const float *src, int64_t n, float *out, void *stream, char **out_error);
+
 /* dst[c, r] = src[r, c] for [rows, cols] elements of elem_bytes (1, 2 or 4): the [K, N] ->
  * [N, K] transpose of PackWeightsPass (passes/weights/fold.rs:549-554). */
 int32_t castforge_hip_transpose(const void *src, int64_t rows, int64_t cols, int32_t elem_bytes, void *dst,

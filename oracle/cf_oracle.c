@@ -613,3 +613,11 @@ double orc_now_seconds(void) {
     clock_gettime(CLOCK_MONOTONIC, &ts);
     return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
 }
+
+/* codegen/eval.rs:1369-1382, castforge.static_quantize with its scale attribute resolved to f32
+ * (> 0) and bits: qmax = bits == 4 ? 7 : 127; y = clamp(round(x / sc), -qmax, qmax) * sc with
+ * Rust's round (half away from zero) and clamp (NaN passes). */
+void orc_static_quantize(const float *x, int64_t n, float sc, int bits, float *y) {
+    const float qmax = bits == 4 ? 7.0f : 127.0f;
+    for (int64_t i = 0; i < n; ++i) y[i] = rust_clamp(roundf(x[i] / sc), -qmax, qmax) * sc;
+}

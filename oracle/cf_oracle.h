@@ -105,6 +105,9 @@ void orc_gemm_w4a16(const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t 
                     float *out);
 void orc_gemm_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t block,
                   const uint32_t *codes, const float *absmax, float *out);
+/* codegen/eval.rs:1369-1382: castforge.static_quantize (fake quant of a matmul's activations) */
+void orc_static_quantize(const float *x, int64_t n, float sc, int bits, float *y);
+
 void orc_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *qw,
                   const float *sw, int64_t n, int64_t k, float *out);
 

@@ -59,6 +59,7 @@ def lib() -> ctypes.CDLL:
             "orc_mx_scale_exp_model": (c_int, [c_float]),
             "orc_quantize_int4g_awq": (None, [P, P, I64, I64, I64, P, P, P]),
             "orc_mx_scale_crosscheck": (I64, [c_uint32, c_uint32, P]),
+            "orc_static_quantize": (None, [P, I64, c_float, c_int, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(l, name)
@@ -83,6 +84,13 @@ def quantize_symmetric(v: np.ndarray, bits: int = 8, round_mode: int = 0):
     q = np.zeros(v.shape, np.int8)
     s = lib().orc_quantize_symmetric(_p(v), v.size, bits, round_mode, _p(q))
     return q, np.float32(s)
+
+
+def static_quantize(x: np.ndarray, scale: float, bits: int = 8) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_static_quantize(_p(x), x.size, np.float32(scale), bits, _p(y))
+    return y
 
 
 def scale_string(scale: float) -> str:

@@ -328,3 +328,66 @@ def test_quantize_channel_granularity_option(cuda):
     q, s = O.quantize_int8_rows(w, 8, 1)
     assert np.array_equal(b.codes.cpu().numpy(), q)
     assert np.array_equal(b.scales.cpu().numpy().view(np.uint32), s.view(np.uint32))
+
+
+# ------------------------------------------------------------ static W8A8 (calibrate) ----
+@pytest.mark.parametrize("bits", [8, 4])
+def test_static_quantize_kernel_matches_oracle(cuda, bits):
+    r = np.random.default_rng(bits)
+    for sc in (np.float32(1.25 / 127), np.float32(0.5), np.float32(3.0e-6), np.float32(7.0)):
+        x = (r.standard_normal(5000) * float(sc) * r.choice([1, 10, 200], 5000)).astype(np.float32)
+        x[:12] = [np.nan, np.inf, -np.inf, 0.0, -0.0, 0.5 * sc, -0.5 * sc, 1.5 * sc, -2.5 * sc,
+                  127.5 * sc, -127.5 * sc, 1e30]
+        y = ops.static_quantize(_t(x, cuda), float(sc), bits).cpu().numpy()
+        ref = O.static_quantize(x, sc, bits)
+        assert np.array_equal(np.isnan(y), np.isnan(ref))
+        ok = ~np.isnan(ref)
+        assert np.array_equal(y[ok].view(np.uint32), ref[ok].view(np.uint32))
+
+
+def test_absmax_kernel(cuda):
+    r = np.random.default_rng(3)
+    for n in (0, 1, 7, 4096, 100003):
+        x = r.standard_normal(n).astype(np.float32)
+        if n > 10:
+            x[5] = np.nan
+            x[9] = -37.5
+        got = ops.absmax(_t(x, cuda))
+        want = float(np.nanmax(np.abs(x))) if n else 0.0
+        assert got == want
+    x = np.array([1.0, -np.inf, np.nan], np.float32)
+    assert ops.absmax(_t(x, cuda)) == np.inf
+    # an unaligned start (scalar path of the reduction)
+    x = _t(r.standard_normal(1001).astype(np.float32), cuda)
+    assert ops.absmax(x[1:]) == float(x[1:].abs().max().item())
+
+
+def test_calibrate_w8a8_reference_case(cuda):
+    """codegen_tests.rs:252-285 (the quantize part): quantize(scheme=w8a8,bits=8,samples=4) on two
+    matmuls of one activation inserts castforge.static_quantize and the module stays within 2e-2
+    of the original.  Here the two matmul results are the outputs (the reference adds them; this
+    evaluator covers the quantized-weight path's ops only)."""
+    mod = Module("parallel_branches")
+    x = mod.add_argument(TensorType((2, 4), "f32"), "x")
+    w0 = mod.add_argument(TensorType((4, 4), "f32"), "w0")
+    w1 = mod.add_argument(TensorType((4, 4), "f32"), "w1")
+    mod.set_results(mod.dot_general(x, w0, name="b0"), mod.dot_general(x, w1, name="b1"))
+    before = mod.clone()
+    res = PassManager.from_pipeline_str(default_registry(), "quantize(scheme=w8a8,bits=8,samples=4)").run(mod)
+    assert res[0].changed
+    assert "castforge.static_quantize" in mod.print_mlir()
+    rep = verify_module_numerics(before, mod, 2e-2, cuda)
+    assert rep.passed, rep.max_abs_diff
+    assert rep.max_abs_diff > 0  # the activations really were quantized
+
+
+def test_calibrate_constant_weight_range(cuda):
+    """A constant rhs's bound is its max |w| (at least 1e-5), read on the device."""
+    w = synth.weight(77, 1, 64, 32, 0.5)
+    w[3, 4] = -2.75
+    mod = _mlp_module(cuda, w)
+    before = mod.clone()
+    PassManager.from_pipeline_str(default_registry(), "calibrate-quantize").run(mod)
+    d = [mod.ops[o] for o in mod.block_ops() if mod.ops[o].is_op("stablehlo", "dot_general")][0]
+    assert d.attributes["rhs_scale"] == 2.75 / 127.0 and d.attributes["lhs_scale"] == 1.25 / 127.0
+    assert verify_module_numerics(before, mod, 0.2, cuda).passed
