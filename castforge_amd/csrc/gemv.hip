@@ -57,7 +57,13 @@ constexpr int kMaxProblems = 8;
 #define CFH_GEMV_CPOL 0
 #endif
 
-enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2 };
+// FMT_Q4_0 / FMT_Q8_0: GGUF planes (gguf.hip), 32-element blocks with an f16 d, M = 1 only
+// on the MFMA path
+enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2, FMT_Q4_0 = 3, FMT_Q8_0 = 4 };
+
+constexpr bool is_gguf(int fmt) { return fmt == FMT_Q4_0 || fmt == FMT_Q8_0; }
+// blocks per chunk of the GGUF planes (a chunk is 64 bytes of a row)
+constexpr int gguf_bpc(int fmt) { return fmt == FMT_Q4_0 ? 4 : 2; }
 
 struct Problem {
     const uint16_t *x;      // bf16 [M, K]
@@ -81,14 +87,14 @@ struct Batch {
     int32_t y_bf16;
 };
 
-template <int FMT> constexpr int codes_per_byte() { return FMT == FMT_INT8 ? 1 : 2; }
+template <int FMT> constexpr int codes_per_byte() { return FMT == FMT_INT8 || FMT == FMT_Q8_0 ? 1 : 2; }
 
 // Position, within each 8-element k-run, of the element the extraction places in f16 slot i.
 // INT4: (n0,n4),(n1,n5),(n2,n6),(n3,n7); INT8 (two words): (b0,b2),(b1,b3) of each word;
 // NF4: the table gives natural-order pairs.
 __device__ __forceinline__ int perm_src(int fmt, int i) {
-    if (fmt == FMT_INT4) return (i >> 1) + ((i & 1) << 2);
-    if (fmt == FMT_INT8) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
+    if (fmt == FMT_INT4 || fmt == FMT_Q4_0) return (i >> 1) + ((i & 1) << 2);
+    if (fmt == FMT_INT8 || fmt == FMT_Q8_0) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
     return i;
 }
 
@@ -564,7 +570,7 @@ void skinny_m1_split_kernel(Batch b) {
     const int64_t grp = FMT == FMT_INT8 ? CK : P.group;  // INT8 has no groups (group 0)
     const uint32_t Gr = static_cast<uint32_t>(uni(static_cast<int>((K + grp - 1) / grp)));
     const uint32_t ZW = (Gr + 7) / 8, GP = ZW * 8;
-    const int gshift = uni(__builtin_ctz(static_cast<uint32_t>(grp / CK)));
+    const int gshift = is_gguf(FMT) ? 0 : uni(__builtin_ctz(static_cast<uint32_t>(grp / CK)));
     const uint32_t code_off = static_cast<uint32_t>(lr) * row_bytes + part * LW;
 
     // this wave's units [u0, u1) and chunks [c_lo, c_hi)
@@ -617,6 +623,10 @@ void skinny_m1_split_kernel(Batch b) {
         } else if constexpr (FMT == FMT_NF4) {
             s_lo = (static_cast<uint32_t>(c_lo >> gshift) * 4u) & ~15u;
             copy_span(P.scales, Gr * 4, s_lo, static_cast<uint32_t>(((c_hi - 1) >> gshift) + 1) * 4u, ms);
+        } else if constexpr (is_gguf(FMT)) {
+            constexpr uint32_t SB = 2 * gguf_bpc(FMT);  // scale bytes per chunk
+            s_lo = (static_cast<uint32_t>(c_lo) * SB) & ~15u;
+            copy_span(P.scales, GP * 2, s_lo, static_cast<uint32_t>(c_hi) * SB, ms);
         }
     }
     // x slice: bf16 x[c_lo * CK, c_hi * CK) copied straight into the region
@@ -773,6 +783,38 @@ void skinny_m1_split_kernel(Batch b) {
                 const float am = *reinterpret_cast<const float *>(
                     ms + meta_lds_off(static_cast<uint32_t>(c >> gshift) * 4u - s_lo, lr));
                 acc += pacc[0] * (live ? am : 0.0f);
+            } else if constexpr (is_gguf(FMT)) {
+                // One MFMA per 32-element block: the four parts of a row hold elements 8p..8p+7
+                // of each block of the chunk, so the MFMA's K sum is that block's exact-code dot
+                // product, scaled in f32 by the block's d.  Q4_0 codes decode to q - 8 exactly.
+                constexpr int BPC = gguf_bpc(FMT);
+                const uint8_t *sp = ms + meta_lds_off(static_cast<uint32_t>(c) * (2u * BPC) - s_lo, lr);
+                uint32_t sv[BPC / 2];
+                if constexpr (BPC == 4) {
+                    const uint2 s2 = *reinterpret_cast<const uint2 *>(sp);
+                    sv[0] = s2.x;
+                    sv[1] = s2.y;
+                } else {
+                    sv[0] = *reinterpret_cast<const uint32_t *>(sp);
+                }
+                const _Float16 *xc = xw + (c - c_lo) * CK + 8 * part;
+#pragma unroll
+                for (int q = 0; q < BPC; ++q) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xc + 32 * q);
+                    floatx4 pb = floatx4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (FMT == FMT_Q4_0) {
+                        uint32_t hb[4];
+                        int4_word_to_h(u.wq[j][q], as_h2(0xE408E408u), as_h2(0xD480D480u), i4k, hb);  // -1032, -72
+                        pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(hb[0], hb[1], hb[2], hb[3]), pb, 0, 0, 0);
+                    } else {
+                        uint32_t h0[2], h1[2];
+                        int8_word_to_h(u.wq[j][2 * q], h0);
+                        int8_word_to_h(u.wq[j][2 * q + 1], h1);
+                        pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]), pb, 0, 0, 0);
+                    }
+                    const float d = f16_to_f32(static_cast<uint16_t>(sv[q >> 1] >> (16 * (q & 1))));
+                    acc += pb[0] * (live ? d : 0.0f);
+                }
             } else {
 #pragma unroll
                 for (int q = 0; q < WPL / 2; ++q) {
@@ -828,9 +870,23 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     const int64_t G = (FMT == FMT_INT4) ? (K + P.group - 1) / P.group : 0, ZW = (G + 7) / 8, GP = ZW * 8;
     const int64_t NBLK = (FMT == FMT_NF4) ? (K + P.group - 1) / P.group : 0;
+    const int64_t GPg = (K / 32 + 7) / 8 * 8;  // GGUF planes: scale row stride
     for (int64_t k = lane; k < K; k += 64) {
         float w;
-        if constexpr (FMT == FMT_INT8) {
+        if constexpr (is_gguf(FMT)) {
+            // element k sits in chunk k / CKg, block q, part p, slot i of the GGUF planes
+            constexpr int BPC = gguf_bpc(FMT), CKg = 32 * BPC;
+            const int64_t c = k / CKg;
+            const int r = static_cast<int>(k % CKg), q = r >> 5, p = (r & 31) >> 3, i = r & 7;
+            const uint8_t *row = static_cast<const uint8_t *>(P.codes) + n * (FMT == FMT_Q4_0 ? K / 2 : K);
+            const float d = f16_to_f32(static_cast<const uint16_t *>(P.scales)[n * GPg + (k >> 5)]);
+            if constexpr (FMT == FMT_Q4_0) {
+                const uint32_t b = row[c * 64 + 16 * p + 4 * q + (i >> 1)];
+                w = static_cast<float>(static_cast<int32_t>((b >> (4 * (i & 1))) & 15u) - 8) * d;
+            } else {
+                w = static_cast<float>(static_cast<const int8_t *>(static_cast<const void *>(row))[c * 64 + 16 * p + 8 * q + i]) * d;
+            }
+        } else if constexpr (FMT == FMT_INT8) {
             w = static_cast<float>(static_cast<const int8_t *>(P.codes)[n * K + k]);
         } else {
             const uint32_t word = static_cast<const uint32_t *>(P.codes)[n * (K / 8) + k / 8];
@@ -870,6 +926,7 @@ __global__ __launch_bounds__(64) void generic_qgemm_kernel(Problem P, int M, int
 // Bytes each lane loads per chunk for this format / group (0 = no MFMA path).
 int lw_for(int fmt, int64_t group) {
     if (fmt == FMT_INT8) return 16;
+    if (is_gguf(fmt)) return group == 32 ? 16 : 0;
     // the chunk index maps to the group by a shift: group / chunk must be a power of two
     if (group >= 128 && group % 128 == 0 && ((group / 128) & (group / 128 - 1)) == 0) return 16;
     if (group == 64) return 8;
@@ -877,9 +934,44 @@ int lw_for(int fmt, int64_t group) {
     return 0;
 }
 
-int chunk_k(int fmt, int lw) { return 4 * lw * (fmt == FMT_INT8 ? 1 : 2); }
+int chunk_k(int fmt, int lw) { return 4 * lw * (fmt == FMT_INT8 || fmt == FMT_Q8_0 ? 1 : 2); }
+
+// LDS bytes of one wave of the M = 1 split-K kernel: its x slice, then its groups' scale and
+// zero-point pieces (1 KB per copy of 4 pieces of 16 bytes per row); bounds over the waves'
+// ranges.  Sets the problem's region offsets.
+int64_t split_region(int fmt, int lw, Problem &p) {
+    const int ck = chunk_k(fmt, lw);
+    auto copies = [](int64_t span) { return ((span + 15) / 16 + 3) / 4; };
+    const int64_t nunits = (p.k / ck + CFH_GEMV_NB_SPLIT - 1) / CFH_GEMV_NB_SPLIT;
+    const int64_t cw = (nunits + kWaves - 1) / kWaves * CFH_GEMV_NB_SPLIT;  // chunks per wave, at most
+    const int64_t xbytes = (cw * ck * 2 + 255) / 256 * 256;
+    const int64_t tbytes = fmt == FMT_INT4 && lw >= 8 ? (cw * 8 + 255) / 256 * 256 : 0;  // x sums
+    int64_t sbytes = 0, zbytes = 0;
+    if (fmt == FMT_INT4) {
+        sbytes = 1024 * copies(2 * cw + 14);
+        zbytes = 1024 * copies(4 * ((cw + 7) / 8 + 1) + 12);
+    } else if (fmt == FMT_NF4) {
+        const int64_t cpb = p.group / ck;  // chunks per absmax block
+        sbytes = 1024 * copies(4 * ((cw + cpb - 1) / cpb + 1) + 12);
+    } else if (is_gguf(fmt)) {
+        sbytes = 1024 * copies(2 * gguf_bpc(fmt) * cw + 14);
+    }
+    p.kc = static_cast<int32_t>(xbytes + tbytes + sbytes + zbytes);
+    p.xsoff = static_cast<int32_t>(xbytes);
+    p.soff = static_cast<int32_t>(xbytes + tbytes);
+    p.zoff = static_cast<int32_t>(xbytes + tbytes + sbytes);
+    return xbytes + tbytes + sbytes + zbytes;
+}
 
 bool skinny_ok(int fmt, const Problem &p, int64_t m) {
+    if (is_gguf(fmt)) {
+        // the GGUF planes have a kernel for M = 1 only, and only while a wave's LDS region fits
+        if (m != 1 || !CFH_GEMV_SPLIT || p.group != 32) return false;
+        Problem q = p;
+        if (p.k % chunk_k(fmt, 16) != 0 || p.k >= (int64_t{1} << 24)) return false;
+        if (split_region(fmt, 16, q) * kWaves > kLdsBytesSplit) return false;
+        return aligned(p.x, 16) && aligned(p.codes, 16) && aligned(p.scales, 16);
+    }
     if (m < 1 || m > 16) return false;
     const int lw = lw_for(fmt, p.group);
     if (lw == 0) return false;
@@ -933,28 +1025,11 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
         std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
         Batch b{};
         int64_t region_max = 0, tiles = 0;
-        auto copies = [](int64_t span) { return ((span + 15) / 16 + 3) / 4; };
         for (int i = 0; i < count; ++i) {
             require(lw_for(fmt, ps[i].group) == lw, "batched problems must share the group size class");
-            const int64_t nunits = (ps[i].k / ck + CFH_GEMV_NB_SPLIT - 1) / CFH_GEMV_NB_SPLIT;
-            const int64_t cw = (nunits + kWaves - 1) / kWaves * CFH_GEMV_NB_SPLIT;  // chunks per wave, at most
-            const int64_t xbytes = (cw * ck * 2 + 255) / 256 * 256;
-            const int64_t tbytes = fmt == FMT_INT4 && lw >= 8 ? (cw * 8 + 255) / 256 * 256 : 0;  // x sums
-            int64_t sbytes = 0, zbytes = 0;
-            if (fmt == FMT_INT4) {
-                sbytes = 1024 * copies(2 * cw + 14);
-                zbytes = 1024 * copies(4 * ((cw + 7) / 8 + 1) + 12);
-            } else if (fmt == FMT_NF4) {
-                const int64_t cpb = ps[i].group / ck;  // chunks per absmax block
-                sbytes = 1024 * copies(4 * ((cw + cpb - 1) / cpb + 1) + 12);
-            }
             b.p[i] = ps[i];
             b.p[i].tile_begin = static_cast<int32_t>(tiles);
-            b.p[i].kc = static_cast<int32_t>(xbytes + tbytes + sbytes + zbytes);
-            b.p[i].xsoff = static_cast<int32_t>(xbytes);
-            b.p[i].soff = static_cast<int32_t>(xbytes + tbytes);
-            b.p[i].zoff = static_cast<int32_t>(xbytes + tbytes + sbytes);
-            region_max = std::max(region_max, xbytes + tbytes + sbytes + zbytes);
+            region_max = std::max(region_max, split_region(fmt, lw, b.p[i]));
             tiles += (ps[i].n + 15) / 16;
         }
         if (region_max * kWaves <= kLdsBytesSplit) {
@@ -972,6 +1047,10 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
                 if (lw == 16) launch_split<FMT_NF4, 16>(b, tiles, lds, st);
                 else if (lw == 8) launch_split<FMT_NF4, 8>(b, tiles, lds, st);
                 else launch_split<FMT_NF4, 4>(b, tiles, lds, st);
+            } else if (fmt == FMT_Q4_0) {
+                launch_split<FMT_Q4_0, 16>(b, tiles, lds, st);
+            } else if (fmt == FMT_Q8_0) {
+                launch_split<FMT_Q8_0, 16>(b, tiles, lds, st);
             } else {
                 launch_split<FMT_INT8, 16>(b, tiles, lds, st);
             }
@@ -979,6 +1058,7 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
             return;
         }
     }
+    require(!is_gguf(fmt), "GGUF planes have no MFMA kernel for this shape");
     // 16-row tiles up to M = 4, 32 rows up to M = 8, 64 rows beyond (x is shared by more rows)
     const int R = m <= 4 ? CFH_GEMV_R_SMALL : m <= 8 ? 2 : 4;
     // longest K first: its workgroups run longest, so they start first
@@ -1056,6 +1136,8 @@ void gemv_generic(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, i
     Problem p{x, codes, scales, zeros, y, n, k, static_cast<int32_t>(group), per_row, 0, 0};
     if (fmt == FMT_INT4) launch_generic<FMT_INT4>(p, m, y_bf16, st);
     else if (fmt == FMT_INT8) launch_generic<FMT_INT8>(p, m, y_bf16, st);
+    else if (fmt == FMT_Q4_0) launch_generic<FMT_Q4_0>(p, m, y_bf16, st);
+    else if (fmt == FMT_Q8_0) launch_generic<FMT_Q8_0>(p, m, y_bf16, st);
     else launch_generic<FMT_NF4>(p, m, y_bf16, st);
 }
 
@@ -1112,6 +1194,52 @@ int32_t castforge_hip_gemv_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t 
         if (!gemv_try_skinny(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st) &&
             !prefill_try(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st))
             gemv_generic(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st);
+    });
+}
+
+int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m, int64_t n, int64_t k,
+                                const void *codes, const uint16_t *scales_f16, void *y, int32_t y_dtype,
+                                void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(ggml_type == CFH_GGML_Q4_0 || ggml_type == CFH_GGML_Q8_0,
+                "ggml_type must be CFH_GGML_Q4_0 or CFH_GGML_Q8_0");
+        common_checks(x, m, n, k, codes, y, y_dtype);
+        const int fmt = ggml_type == CFH_GGML_Q4_0 ? FMT_Q4_0 : FMT_Q8_0;
+        require(k % chunk_k(fmt, 16) == 0, fmt == FMT_Q4_0 ? "Q4_0 planes need k % 128 == 0"
+                                                           : "Q8_0 planes need k % 64 == 0");
+        if (m == 0 || n == 0) return;
+        require(k == 0 || scales_f16, "scales must not be NULL");
+        require(aligned(codes, 16) && aligned(scales_f16, 16), "codes and scales must be 16-byte aligned");
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        const int yb = y_dtype == CFH_DTYPE_BF16;
+        if (!gemv_try_skinny(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st))
+            gemv_generic(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st);
+    });
+}
+
+int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_problem_t *problems, int32_t count,
+                                        int32_t y_dtype, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(ggml_type == CFH_GGML_Q4_0 || ggml_type == CFH_GGML_Q8_0,
+                "ggml_type must be CFH_GGML_Q4_0 or CFH_GGML_Q8_0");
+        require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
+        require(count == 0 || problems != nullptr, "problems must not be NULL");
+        require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+        const int fmt = ggml_type == CFH_GGML_Q4_0 ? FMT_Q4_0 : FMT_Q8_0;
+        Problem ps[kMaxProblems];
+        int used = 0;
+        for (int i = 0; i < count; ++i) {
+            const cfh_gguf_problem_t &q = problems[i];
+            common_checks(q.x, 1, q.n, q.k, q.codes, q.y, y_dtype);
+            if (q.n == 0) continue;
+            require(q.k > 0 && q.scales_f16, "problem buffers must not be NULL");
+            Problem p{q.x, q.codes, q.scales_f16, nullptr, q.y, q.n, q.k, 32, 1, 0, 0};
+            require(skinny_ok(fmt, p, 1),
+                    "batched GGUF GEMV needs k % 128 == 0 (Q4_0) or k % 64 == 0 (Q8_0), k below the "
+                    "split kernel's LDS bound and 16-byte aligned x / codes / scales");
+            ps[used++] = p;
+        }
+        if (used) launch_skinny(fmt, ps, used, 1, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -162,7 +162,9 @@ __device__ __forceinline__ bool e4m3_special(float v) {
     return a >= 0x43e00000u || (a & 0x7ffffeu) == 0x7ffffeu;
 }
 __device__ __forceinline__ uint32_t e4m3x4(float v0, float v1, float v2, float v3) {
-    if (e4m3_special(v0) | e4m3_special(v1) | e4m3_special(v2) | e4m3_special(v3))
+    // one test of the OR of the four flags (no short-circuit branches)
+    if (static_cast<int>(e4m3_special(v0)) | static_cast<int>(e4m3_special(v1)) |
+        static_cast<int>(e4m3_special(v2)) | static_cast<int>(e4m3_special(v3)))
         return f32_to_e4m3fn(v0) | (f32_to_e4m3fn(v1) << 8) | (f32_to_e4m3fn(v2) << 16) |
                (static_cast<uint32_t>(f32_to_e4m3fn(v3)) << 24);
     const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);

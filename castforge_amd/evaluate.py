@@ -120,6 +120,9 @@ class _Evaluator:
             if b.format == "fp8_row":
                 qa, sa = ops.quantize_fp8(x)  # per-token dynamic E4M3 activations (W8A8)
                 return ops.gemm_fp8(qa, sa, b.codes, b.scales, out_dtype=torch.float32)
+            if b.format in ("gguf_q4_0", "gguf_q8_0"):
+                ty = ops.GGML_TYPES["Q4_0" if b.format == "gguf_q4_0" else "Q8_0"]
+                return ops.gemm_gguf(x, ops.GgufPacked(ty, b.codes, b.scales, n, k), torch.float32)
         # an f32 weight (not quantized): plain matmul
         return self._matmul(lhs, self.env[wq], wty.shape, packed)
 

@@ -23,6 +23,7 @@ DTYPE_F32, DTYPE_BF16 = 0, 1
 MAX_BATCH = 8
 GROUPWISE_WORKSPACE_BYTES = 2048
 EPI_BIAS, EPI_RELU, EPI_TANH, EPI_SILU, EPI_GELU, EPI_SCALE = range(6)
+GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_BF16 = 0, 1, 2, 8, 30
 
 
 class CastForgeHipError(RuntimeError):
@@ -82,6 +83,17 @@ class W4A16Problem(ctypes.Structure):
     ]
 
 
+class GgufProblem(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p),
+        ("codes", c_void_p),
+        ("scales_f16", c_void_p),
+        ("y", c_void_p),
+        ("n", c_int64),
+        ("k", c_int64),
+    ]
+
+
 _P = c_void_p
 _E = POINTER(c_char_p)
 # name -> (restype, argtypes) for every entry point of the header
@@ -117,6 +129,14 @@ SIGNATURES = {
     "castforge_hip_convert_bf16_to_f32": (c_int32, [_P, c_int64, _P, _P, _E]),
     "castforge_hip_transpose": (c_int32, [_P, c_int64, c_int64, c_int32, _P, _P, _E]),
     "castforge_hip_matmul_f32": (c_int32, [_P, c_int64, c_int64, _P, c_int64, c_int32, _P, _P, _E]),
+    "castforge_hip_gguf_payload_bytes": (c_int32, [c_int32, c_int64, POINTER(c_int64), _E]),
+    "castforge_hip_gguf_decode": (c_int32, [c_int32, _P, c_int64, _P, _P, _E]),
+    "castforge_hip_gguf_encode": (c_int32, [c_int32, _P, c_int64, ctypes.c_float, _P, _P, _E]),
+    "castforge_hip_gguf_repack": (c_int32, [c_int32, _P, c_int64, c_int64, _P, _P, _P, _E]),
+    "castforge_hip_gguf_unpack": (c_int32, [c_int32, _P, _P, c_int64, c_int64, _P, _P, _E]),
+    "castforge_hip_dequantize_gguf": (c_int32, [c_int32, _P, _P, c_int64, c_int64, _P, _P, _E]),
+    "castforge_hip_gemv_gguf": (c_int32, [c_int32, _P, c_int64, c_int64, c_int64, _P, _P, _P, c_int32, _P, _E]),
+    "castforge_hip_gemv_gguf_batched": (c_int32, [c_int32, POINTER(GgufProblem), c_int32, c_int32, _P, _E]),
 }
 
 _lib = None

@@ -39,7 +39,8 @@ class QuantUniform:
 @dataclass(frozen=True)
 class QuantPacked:
     """Packed low-bit weights of this library: format in {int8_channel, int4_asym, nf4,
-    fp8_row}; group is the INT4 group / NF4 block (0 when not grouped)."""
+    fp8_row, gguf_q4_0, gguf_q8_0}; group is the INT4 group / NF4 block / GGUF block (0 when
+    not grouped)."""
     format: str
     expressed: str
     group: int

@@ -314,6 +314,133 @@ def gemv_nf4_batched(xs: list[torch.Tensor], ps: list["Nf4Packed"], ys: list[tor
         ffi.call("castforge_hip_gemv_nf4_batched", arr, len(ps), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
 
 
+# ----------------------------------------------------------------------------- GGUF ----
+GGML_TYPES = {"F32": ffi.GGML_F32, "F16": ffi.GGML_F16, "Q4_0": ffi.GGML_Q4_0, "Q8_0": ffi.GGML_Q8_0,
+              "BF16": ffi.GGML_BF16}
+
+
+def _ggml(t) -> int:
+    if isinstance(t, str):
+        if t not in GGML_TYPES:
+            raise ValueError(f"unknown GGML type {t!r}")
+        return GGML_TYPES[t]
+    return int(t)
+
+
+def gguf_payload_bytes(ggml_type, num_elems: int) -> int:
+    """Bytes of a GGUF tensor payload of num_elems elements (gguf.rs:491-550)."""
+    out = ctypes.c_int64()
+    ffi.call("castforge_hip_gguf_payload_bytes", _ggml(ggml_type), num_elems, ctypes.byref(out))
+    return out.value
+
+
+def gguf_decode(ggml_type, raw: torch.Tensor, num_elems: int) -> torch.Tensor:
+    """f32 [num_elems] of a GGUF payload held in a device uint8 tensor (gguf.rs:486-550)."""
+    raw = _dev(raw)
+    t = _ggml(ggml_type)
+    need = gguf_payload_bytes(t, num_elems)
+    if raw.dtype != torch.uint8 or raw.numel() < need:
+        raise ValueError(f"raw must be a uint8 tensor of at least {need} bytes")
+    out = torch.empty(num_elems, dtype=torch.float32, device=raw.device)
+    ffi.call("castforge_hip_gguf_decode", t, _ptr(raw), num_elems, _ptr(out), _stream(raw))
+    return out
+
+
+def gguf_encode(ggml_type, src: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """GGUF payload (device uint8) of a tensor: Q8_0 from int8 codes and their one scale
+    (gguf.rs:283-296), F16 / BF16 / F32 from float32 values (gguf.rs:298-318)."""
+    src = _dev(src)
+    t = _ggml(ggml_type)
+    n = src.numel()
+    if t == ffi.GGML_Q8_0:
+        if src.dtype != torch.int8:
+            raise ValueError("Q8_0 export takes int8 codes")
+        nbytes = (max(n, 1) + 31) // 32 * 34
+    else:
+        if src.dtype != torch.float32:
+            raise ValueError("F32 / F16 / BF16 export takes float32 values")
+        nbytes = gguf_payload_bytes(t, n)
+    out = torch.empty(nbytes, dtype=torch.uint8, device=src.device)
+    ffi.call("castforge_hip_gguf_encode", t, _ptr(src), n, ctypes.c_float(scale), _ptr(out), _stream(src))
+    return out
+
+
+@dataclass
+class GgufPacked:
+    """GGUF planes of a Q4_0 / Q8_0 matrix [n, k] (blocks of 32 along k): codes uint8
+    [n, k/2] (Q4_0) or int8 [n, k] (Q8_0), scales f16 [n, GP]."""
+    ggml_type: int
+    codes: torch.Tensor
+    scales: torch.Tensor
+    n: int
+    k: int
+
+    def nbytes(self) -> int:
+        return self.codes.numel() * self.codes.element_size() + self.scales.numel() * 2
+
+    def payload_bytes(self) -> int:
+        return gguf_payload_bytes(self.ggml_type, self.n * self.k)
+
+
+def gguf_planes_ok(ggml_type, k: int) -> bool:
+    t = _ggml(ggml_type)
+    return t in (ffi.GGML_Q4_0, ffi.GGML_Q8_0) and k % (128 if t == ffi.GGML_Q4_0 else 64) == 0
+
+
+def gguf_repack(ggml_type, raw: torch.Tensor, n: int, k: int) -> GgufPacked:
+    """Q4_0 / Q8_0 blocks of a row-major [n, k] tensor -> the planes the GEMV reads."""
+    raw = _dev(raw)
+    t = _ggml(ggml_type)
+    if raw.dtype != torch.uint8 or raw.numel() < gguf_payload_bytes(t, n * k):
+        raise ValueError("raw must be a uint8 tensor holding the tensor's blocks")
+    gp = (k // 32 + 7) // 8 * 8
+    codes = torch.empty((n, k // 2 if t == ffi.GGML_Q4_0 else k),
+                        dtype=torch.uint8 if t == ffi.GGML_Q4_0 else torch.int8, device=raw.device)
+    scales = torch.empty((n, gp), dtype=torch.float16, device=raw.device)
+    ffi.call("castforge_hip_gguf_repack", t, _ptr(raw), n, k, _ptr(codes), _ptr(scales), _stream(raw))
+    return GgufPacked(t, codes, scales, n, k)
+
+
+def gguf_unpack(p: GgufPacked) -> torch.Tensor:
+    """The block payload (device uint8) of GGUF planes."""
+    out = torch.empty(p.payload_bytes(), dtype=torch.uint8, device=p.codes.device)
+    ffi.call("castforge_hip_gguf_unpack", p.ggml_type, _ptr(p.codes), _ptr(p.scales), p.n, p.k, _ptr(out),
+             _stream(p.codes))
+    return out
+
+
+def dequantize_gguf(p: GgufPacked) -> torch.Tensor:
+    out = torch.empty((p.n, p.k), dtype=torch.float32, device=p.codes.device)
+    ffi.call("castforge_hip_dequantize_gguf", p.ggml_type, _ptr(p.codes), _ptr(p.scales), p.n, p.k, _ptr(out),
+             _stream(p.codes))
+    return out
+
+
+def gemm_gguf(x: torch.Tensor, p: GgufPacked, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """y [M, n] = x [M, k] (bf16) times decode(W)^T over GGUF planes."""
+    x = _check_x(x, p.k)
+    y = torch.empty((x.shape[0], p.n), dtype=out_dtype, device=x.device)
+    ffi.call("castforge_hip_gemv_gguf", p.ggml_type, _ptr(x), x.shape[0], p.n, p.k, _ptr(p.codes),
+             _ptr(p.scales), _ptr(y), _out_dtype(out_dtype), _stream(x))
+    return y
+
+
+def gemv_gguf_batched(xs: list[torch.Tensor], ps: list[GgufPacked], ys: list[torch.Tensor]) -> None:
+    """One M = 1 launch for up to 8 GGUF matrices of one type; outputs preallocated."""
+    if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
+        raise ValueError("xs, ps, ys must have the same length <= 8")
+    if not ps:
+        return
+    t = ps[0].ggml_type
+    arr = (ffi.GgufProblem * len(ps))()
+    for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
+        _check_x(x, p.k)
+        if p.ggml_type != t or x.shape[0] != 1 or y.shape != (1, p.n):
+            raise ValueError("problems must share the GGML type, with x [1, k] and y [1, n]")
+        arr[i] = ffi.GgufProblem(_ptr(x), _ptr(p.codes), _ptr(p.scales), _ptr(y), p.n, p.k)
+    ffi.call("castforge_hip_gemv_gguf_batched", t, arr, len(ps), _out_dtype(ys[0].dtype), _stream(xs[0]))
+
+
 # ------------------------------------------------------------- static W8A8 (calibrate) ----
 def static_quantize(x: torch.Tensor, scale: float, bits: int = 8) -> torch.Tensor:
     """castforge.static_quantize (eval.rs:1369-1382): clamp(round(x / scale), +-qmax) * scale

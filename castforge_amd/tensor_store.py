@@ -39,7 +39,8 @@ class QuantizedI8:
 
 @dataclass
 class QuantizedPacked:
-    """format: int8_channel | int4_asym | nf4 | fp8_row; shape [N, K]."""
+    """format: int8_channel | int4_asym | nf4 | fp8_row | gguf_q4_0 | gguf_q8_0; shape [N, K]
+    (gguf_*: GGUF planes, codes + f16 scales, no zeros)."""
     format: str
     codes: Any
     scales: Any
@@ -215,4 +216,7 @@ def dequantize_packed(b: QuantizedPacked):
         return ops.dequantize_int8(b.codes, b.scales, "channel")
     if b.format == "fp8_row":
         return ops.dequantize_fp8(b.codes, b.scales)
+    if b.format in ("gguf_q4_0", "gguf_q8_0"):
+        ty = ops.GGML_TYPES["Q4_0" if b.format == "gguf_q4_0" else "Q8_0"]
+        return ops.dequantize_gguf(ops.GgufPacked(ty, b.codes, b.scales, n, k))
     raise ValueError(f"unknown packed format {b.format}")

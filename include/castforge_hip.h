@@ -262,6 +262,72 @@ int32_t castforge_hip_convert_bf16_to_f32(const uint16_t *src, int64_t n, float 
 int32_t castforge_hip_static_quantize(const float *x, int64_t n, float scale, int32_t bits, float *y,
                                       void *stream, char **out_error);
 
+/* ---- GGUF payloads (ir/formats/gguf.rs) --------------------------------------------------- */
+
+/* GgmlType ids of the reference's GGUF reader / writer (gguf.rs:16-37). */
+enum { CFH_GGML_F32 = 0, CFH_GGML_F16 = 1, CFH_GGML_Q4_0 = 2, CFH_GGML_Q8_0 = 8, CFH_GGML_BF16 = 30 };
+
+/* One matrix of castforge_hip_gemv_gguf_batched: x bf16 [1, k], GGUF planes of W [n, k], y [1, n]. */
+typedef struct {
+    const uint16_t *x;
+    const void *codes;
+    const uint16_t *scales_f16;
+    void *y;
+    int64_t n, k;
+} cfh_gguf_problem_t;
+
+/* Payload bytes of num_elems elements (gguf.rs:491-550: F32 4 B, F16 / BF16 2 B, Q4_0 18 B and
+ * Q8_0 34 B per started block of 32).  Unknown ids fail with the reference's message. */
+int32_t castforge_hip_gguf_payload_bytes(int32_t ggml_type, int64_t num_elems, int64_t *out_bytes,
+                                         char **out_error);
+
+/* Replaces decode_ggml_tensor (gguf.rs:486-550): num_elems f32 values of a tensor payload.
+ * Q4_0: blocks of f16 d + 16 bytes, element 2j = low nibble of byte j, 2j+1 = high nibble,
+ * value (nibble - 8) * d; Q8_0: f16 d + 32 int8, value q * d; F16 exactly as
+ * f16_bits_to_f32 (ir/tensor_store.rs:59-82); BF16 as bits << 16.  Blocks run over the
+ * flattened tensor and the last one may be partial.  raw: device, 4-byte (F32) or 2-byte
+ * aligned, holding payload_bytes(type, num_elems) bytes. */
+int32_t castforge_hip_gguf_decode(int32_t ggml_type, const void *raw, int64_t num_elems, float *out,
+                                  void *stream, char **out_error);
+
+/* Replaces the payload loop of export_gguf_bytes (gguf.rs:280-322).  Q8_0: src = int8 codes of a
+ * QuantizedI8 tensor and `scale` its one scale, written into every block as
+ * f32_to_f16_bits(scale) (truncating, tensor_store.rs:84-102), codes past num_elems 0, and
+ * ceil(max(num_elems, 1) / 32) blocks (gguf.rs:283-296).  F16 / BF16: src = f32 values, by the
+ * truncating converters (tensor_store.rs:84-111).  F32: a copy.  scale is ignored but for Q8_0. */
+int32_t castforge_hip_gguf_encode(int32_t ggml_type, const void *src, int64_t num_elems, float scale,
+                                  void *raw_out, void *stream, char **out_error);
+
+/* GGUF planes: the layout castforge_hip_gemv_gguf reads, for a Q4_0 / Q8_0 matrix [rows, k] whose
+ * blocks run along k (row-major after the reader's dimension reversal, gguf.rs:117-122).
+ * codes: rows x (k/2) bytes (Q4_0) or rows x k (Q8_0); each row is cut into chunks of 128
+ * (Q4_0) / 64 (Q8_0) elements = 64 bytes, stored as four 16-byte parts, part p holding
+ * elements 8p..8p+7 of each block of the chunk (Q4_0: 4 bytes per block in the block's nibble
+ * order; Q8_0: 8 bytes per block).  scales_f16: the blocks' d bits [rows, GP],
+ * GP = 8 * ceil(k/32 / 8), pad slots 0.  Needs k % 128 == 0 (Q4_0) or k % 64 == 0 (Q8_0) and
+ * 16-byte aligned planes.  No reference counterpart: the reference decodes to f32 on import. */
+int32_t castforge_hip_gguf_repack(int32_t ggml_type, const void *raw, int64_t rows, int64_t k, void *codes,
+                                  uint16_t *scales_f16, void *stream, char **out_error);
+/* Planes back to the block payload (the inverse of castforge_hip_gguf_repack). */
+int32_t castforge_hip_gguf_unpack(int32_t ggml_type, const void *codes, const uint16_t *scales_f16, int64_t rows,
+                                  int64_t k, void *raw_out, void *stream, char **out_error);
+/* Planes to f32 [rows, k]: the values decode_ggml_tensor gives for the same blocks. */
+int32_t castforge_hip_dequantize_gguf(int32_t ggml_type, const void *codes, const uint16_t *scales_f16,
+                                      int64_t rows, int64_t k, float *out, void *stream, char **out_error);
+
+/* y[m, n] = sum_k x[m, k] * decode(W)[n, k] over GGUF planes of a Q4_0 / Q8_0 matrix W [n, k]
+ * (contraction along the blocked dimension, as GGUF producers store linear weights).  The
+ * dequant-GEMV of a GGUF weight: the reference decodes it to f32 (gguf.rs:513-550) and
+ * evaluates the matmul (codegen/eval.rs:1465-1507).  x bf16 [m, k] 16-byte aligned; y f32 or
+ * bf16.  M = 1 runs the split-K MFMA kernel (one MFMA per block, scaled in f32 by its d);
+ * larger M a generic kernel. */
+int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m, int64_t n, int64_t k,
+                                const void *codes, const uint16_t *scales_f16, void *y, int32_t y_dtype,
+                                void *stream, char **out_error);
+/* Up to CFH_MAX_BATCH matrices of one type at M = 1 in one launch. */
+int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_problem_t *problems, int32_t count,
+                                        int32_t y_dtype, void *stream, char **out_error);
+
 /* *out = max |src[i]| over the non-NaN elements (0 for n == 0), written on the device: the
  * constant ranges of calibrate-quantize's calibrate_value_ranges (formats.rs:135-150). */
 int32_t castforge_hip_absmax_f32(const float *src, int64_t n, float *out, void *stream, char **out_error);

@@ -621,3 +621,73 @@ void orc_static_quantize(const float *x, int64_t n, float sc, int bits, float *y
     const float qmax = bits == 4 ? 7.0f : 127.0f;
     for (int64_t i = 0; i < n; ++i) y[i] = rust_clamp(roundf(x[i] / sc), -qmax, qmax) * sc;
 }
+
+/* ---- GGUF tensor payloads ---------------------------------------------------------------- */
+/* gguf.rs:486-550 (decode_ggml_tensor): F32 / F16 / BF16 element arrays and the 32-element
+ * blocks Q4_0 (f16 d, then 16 bytes: element 2j = low nibble of byte j, 2j+1 = high nibble,
+ * value (nibble - 8) * d) and Q8_0 (f16 d, then 32 int8: value q * d).  Blocks run over the
+ * flattened tensor; the last block's elements past num_elems are dropped.  Returns the payload
+ * bytes read, or -1 for an unknown type. */
+int64_t orc_gguf_decode(int type, const uint8_t *raw, int64_t num_elems, float *out) {
+    switch (type) {
+    case ORC_GGML_F32:
+        for (int64_t i = 0; i < num_elems; ++i) {
+            uint32_t u = (uint32_t)raw[4 * i] | ((uint32_t)raw[4 * i + 1] << 8) |
+                         ((uint32_t)raw[4 * i + 2] << 16) | ((uint32_t)raw[4 * i + 3] << 24);
+            out[i] = u2f(u);
+        }
+        return num_elems * 4;
+    case ORC_GGML_F16:
+    case ORC_GGML_BF16:
+        for (int64_t i = 0; i < num_elems; ++i) {
+            uint16_t h = (uint16_t)(raw[2 * i] | (raw[2 * i + 1] << 8));
+            out[i] = type == ORC_GGML_F16 ? orc_f16_to_f32(h) : orc_bf16_to_f32(h);
+        }
+        return num_elems * 2;
+    case ORC_GGML_Q4_0: {
+        const int64_t blocks = (num_elems + 31) / 32;
+        int64_t o = 0;
+        for (int64_t b = 0; b < blocks; ++b) {
+            const uint8_t *blk = raw + 18 * b;
+            const float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+            for (int j = 2; j < 18; ++j) {
+                if (o < num_elems) out[o++] = (float)((int32_t)(blk[j] & 0x0f) - 8) * d;
+                if (o < num_elems) out[o++] = (float)((int32_t)((blk[j] >> 4) & 0x0f) - 8) * d;
+            }
+        }
+        return blocks * 18;
+    }
+    case ORC_GGML_Q8_0: {
+        const int64_t blocks = (num_elems + 31) / 32;
+        int64_t o = 0;
+        for (int64_t b = 0; b < blocks; ++b) {
+            const uint8_t *blk = raw + 34 * b;
+            const float d = orc_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+            for (int j = 2; j < 34; ++j)
+                if (o < num_elems) out[o++] = (float)(int8_t)blk[j] * d;
+        }
+        return blocks * 34;
+    }
+    default:
+        return -1;
+    }
+}
+
+/* gguf.rs:283-296: a QuantizedI8 tensor (n int8 codes, one f32 scale) as Q8_0 blocks: every
+ * block repeats f32_to_f16_bits(scale) (tensor_store.rs:84-102, truncating) and the codes of its
+ * 32 elements, zero past n; max(n, 1) elements make ceil(max(n,1) / 32) blocks.  Returns the
+ * bytes written. */
+int64_t orc_gguf_encode_q8_0(const int8_t *codes, int64_t n, float scale, uint8_t *out) {
+    const int64_t blocks = ((n > 1 ? n : 1) + 31) / 32;
+    const uint16_t h = orc_f32_to_f16_trunc(scale);
+    for (int64_t b = 0; b < blocks; ++b) {
+        uint8_t *blk = out + 34 * b;
+        blk[0] = (uint8_t)(h & 0xff);
+        blk[1] = (uint8_t)(h >> 8);
+        for (int j = 0; j < 32; ++j) {
+            const int64_t i = 32 * b + j;
+            blk[2 + j] = (uint8_t)(i < n ? codes[i] : 0);
+        }
+    }
+    return blocks * 34;
+}

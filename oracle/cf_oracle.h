@@ -108,6 +108,11 @@ void orc_gemm_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t bl
 /* codegen/eval.rs:1369-1382: castforge.static_quantize (fake quant of a matmul's activations) */
 void orc_static_quantize(const float *x, int64_t n, float sc, int bits, float *y);
 
+/* gguf.rs:16-23 (GgmlType ids) and gguf.rs:486-550 / 283-296 (payload decode, Q8_0 encode) */
+enum { ORC_GGML_F32 = 0, ORC_GGML_F16 = 1, ORC_GGML_Q4_0 = 2, ORC_GGML_Q8_0 = 8, ORC_GGML_BF16 = 30 };
+int64_t orc_gguf_decode(int type, const uint8_t *raw, int64_t num_elems, float *out);
+int64_t orc_gguf_encode_q8_0(const int8_t *codes, int64_t n, float scale, uint8_t *out);
+
 void orc_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *qw,
                   const float *sw, int64_t n, int64_t k, float *out);
 

@@ -60,6 +60,8 @@ def lib() -> ctypes.CDLL:
             "orc_quantize_int4g_awq": (None, [P, P, I64, I64, I64, P, P, P]),
             "orc_mx_scale_crosscheck": (I64, [c_uint32, c_uint32, P]),
             "orc_static_quantize": (None, [P, I64, c_float, c_int, P]),
+            "orc_gguf_decode": (I64, [c_int, P, I64, P]),
+            "orc_gguf_encode_q8_0": (I64, [P, I64, c_float, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(l, name)
@@ -185,6 +187,26 @@ def quantize_fp8_grid(v: np.ndarray, e5m2=False, mxfp8=True, block_size=32):
     deq = np.zeros_like(v)
     lib().orc_quantize_fp8_grid(_p(v), v.size, int(e5m2), int(mxfp8), block_size, _p(deq))
     return deq
+
+
+# ---------------------------------------------------------------------- GGUF ----
+GGML = {"F32": 0, "F16": 1, "Q4_0": 2, "Q8_0": 8, "BF16": 30}
+
+
+def gguf_decode(ggml_type: int, raw: np.ndarray, num_elems: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, np.uint8)
+    out = np.zeros(max(num_elems, 1), np.float32)
+    used = lib().orc_gguf_decode(ggml_type, _p(raw), num_elems, _p(out))
+    assert 0 <= used <= raw.size, (used, raw.size)
+    return out[:num_elems]
+
+
+def gguf_encode_q8_0(codes: np.ndarray, scale: float) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, np.int8).reshape(-1)
+    out = np.zeros((max(codes.size, 1) + 31) // 32 * 34, np.uint8)
+    n = lib().orc_gguf_encode_q8_0(_p(codes) if codes.size else 0, codes.size, np.float32(scale), _p(out))
+    assert n == out.size
+    return out
 
 
 # ---------------------------------------------------------------------- GEMMs ----
