@@ -287,6 +287,28 @@ def main():
         log(f"[bench] W8A16 M=1 {components['w8a16_gemv_m1_GBps']} GB/s, NF4 M=1 {components['nf4_gemv_m1_GBps']} GB/s")
         del nf, nfc
 
+        # GGUF Q4_0 / Q8_0 GEMV M=1 over the block (gguf.rs block formats, GEMV planes), seeded
+        # random blocks with f16 d ~ N(0, 0.003); rotating copies keep the set above the MALL
+        for ty, bb, tag, ncopy in ((2, 18, "q4_0", 8), (8, 34, "q8_0", 4)):
+            gc = []
+            for c in range(ncopy):
+                gg = torch.Generator(device=dev)
+                gg.manual_seed(1000 * ty + c)
+                row = []
+                for (_, n, k) in synth.LLAMA7B_BLOCK:
+                    raw = torch.randint(0, 256, (n * k // 32 * bb,), dtype=torch.uint8, device=dev, generator=gg)
+                    d = (torch.randn(n * k // 32, device=dev, generator=gg) * 0.003).half()
+                    raw.view(-1, bb)[:, 0:2] = d.view(torch.uint8).view(-1, 2)
+                    row.append(ops.gguf_repack(ty, raw, n, k))
+                    del raw, d
+                gc.append(row)
+            ysg = [torch.empty((1, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
+            st = time_steps(lambda i: ops.gemv_gguf_batched(xs8, gc[i % len(gc)], ysg), 50, 5)
+            gb = sum(p.nbytes() + 2 * p.k + 2 * p.n for p in gc[0])
+            components[f"gguf_{tag}_gemv_m1_GBps"] = round(gb / (st * 1e-3) / 1e9, 1)
+            log(f"[bench] GGUF {tag} GEMV M=1: {st * 1e3:.1f} us, {components[f'gguf_{tag}_gemv_m1_GBps']} GB/s")
+            del gc, ysg
+
         # prefill GEMMs on MFMA: W4A16 INT4 g128 at M=4096 (config 5 follow-on) and NF4 b64 at
         # M=64 / 512 over W_gate / W_up / W_down (config 3)
         for (name, n, k) in (synth.LLAMA7B_BLOCK[4], synth.LLAMA7B_BLOCK[6]):
