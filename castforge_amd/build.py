@@ -28,7 +28,7 @@ COMMON = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 # Sources whose arithmetic must round exactly like the CPU reference (no a*b+c contraction).
-EXACT = {"quantize.hip", "quantize_ref.hip", "elementwise.hip"}
+EXACT = {"quantize.hip", "quantize_ref.hip", "elementwise.hip", "rotate.hip"}
 
 
 def sources() -> list[Path]:

@@ -7,6 +7,8 @@
 // where that is shown to give the same quotient), no contraction (this file is built with
 // -ffp-contract=off), round-half-even via rintf or half-away via roundf, NaN -> 0 as in Rust's
 // `as i8`.
+#include <algorithm>
+
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
 
@@ -481,8 +483,41 @@ __device__ __forceinline__ float group_reduce_min(float v) {
     return v;
 }
 
+// Walsh-Hadamard rotation of the values of blocks of rot_b consecutive elements of a row, as
+// rotate-hadamard computes it (formats.rs:303-327: butterfly stages h = 1, 2, .., rot_b/2 in
+// order, then times norm): stages h < 16 inside a lane's 16 values, stages 16 <= h < rot_b
+// (<= 1024) against lane ^ (h / 16), the lower lane keeping x + y and the upper x - y.  The
+// lanes of a wave hold 1024 consecutive elements of one row, so every block lies in one wave.
+__device__ __forceinline__ void hadamard16_lanes(float (&x)[16], int rot_b, float norm) {
+#pragma unroll
+    for (int h = 1; h < 16; h *= 2) {
+        if (h >= rot_b) break;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2 * h)
+#pragma unroll
+            for (int j = i; j < i + h; ++j) {
+                const float a = x[j], b = x[j + h];
+                x[j] = a + b;
+                x[j + h] = a - b;
+            }
+    }
+    const int lane = threadIdx.x & 63;
+    for (int h = 16; h < rot_b; h *= 2) {  // wave-uniform
+        const int d = h >> 4;
+        const bool lower = (lane & d) == 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float p = __shfl_xor(x[i], d);
+            x[i] = lower ? x[i] + p : p - x[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] *= norm;
+}
+
 template <int GROUP>
-__global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> sets, int64_t cols) {
+__global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> sets, int64_t cols, int rot_b,
+                                                               float rot_norm) {
     constexpr int TPG = GROUP / 16;   // threads per group
     constexpr int T = 8 * TPG;        // threads per task (8 groups: one zero-point word)
     constexpr int TPB = kBlock / T;   // tasks per block
@@ -506,6 +541,8 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
     const uint32_t w0 = zw * (2 * T) + 2 * t;  // this thread's first code word
     const bool ok0 = task_ok && w0 < KW, ok1 = task_ok && w0 + 1 < KW;
     float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = 0.0f;
     float mx = -INFINITY, mn = INFINITY;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -521,8 +558,14 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
                 xx[0] *= c.x; xx[1] *= c.y; xx[2] *= c.z; xx[3] *= c.w;
                 xx[4] *= d.x; xx[5] *= d.y; xx[6] *= d.z; xx[7] *= d.w;
             }
+        }
+    }
+    if (rot_b > 1) hadamard16_lanes(x, rot_b, rot_norm);  // uniform: every lane takes part
 #pragma unroll
-            for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, xx[i]); mn = fminf(mn, xx[i]); }
+    for (int h = 0; h < 2; ++h) {
+        if (h == 0 ? ok0 : ok1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, x[8 * h + i]); mn = fminf(mn, x[8 * h + i]); }
         }
     }
     mx = group_reduce_max<TPG>(mx);
@@ -782,17 +825,18 @@ int32_t castforge_hip_dequantize_int8(const int8_t *codes, const float *scales, 
 namespace cfh {
 namespace {
 // int4g_quant16_kernel over a set of matrices (rows <= 65535 in total, group 16..256).
-void launch_int4g16(const RowSets<float> &sets, int64_t rows, int64_t cols, int64_t group, hipStream_t st) {
+void launch_int4g16(const RowSets<float> &sets, int64_t rows, int64_t cols, int64_t group, hipStream_t st,
+                    int rot_b = 0, float rot_norm = 1.0f) {
     // 16 codes per thread: a task (8 groups) takes group / 2 threads; one grid row per row
     const int64_t G = (cols + group - 1) / group, ZW = (G + 7) / 8;
     const int64_t tpb = kBlock / (group / 2);
     dim3 g(static_cast<unsigned>((ZW + tpb - 1) / tpb), static_cast<unsigned>(rows)), b(kBlock);
     switch (group) {
-    case 16: int4g_quant16_kernel<16><<<g, b, 0, st>>>(sets, cols); break;
-    case 32: int4g_quant16_kernel<32><<<g, b, 0, st>>>(sets, cols); break;
-    case 64: int4g_quant16_kernel<64><<<g, b, 0, st>>>(sets, cols); break;
-    case 128: int4g_quant16_kernel<128><<<g, b, 0, st>>>(sets, cols); break;
-    default: int4g_quant16_kernel<256><<<g, b, 0, st>>>(sets, cols); break;
+    case 16: int4g_quant16_kernel<16><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
+    case 32: int4g_quant16_kernel<32><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
+    case 64: int4g_quant16_kernel<64><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
+    case 128: int4g_quant16_kernel<128><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
+    default: int4g_quant16_kernel<256><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
     }
     check_launch("int4g_quant16");
 }
@@ -910,9 +954,38 @@ void quantize_batched(const cfh_quant_problem_t *ps, int32_t count, bool int4, i
     }
 }
 }  // namespace
+
+float hadamard_norm(int64_t b);  // rotate.hip: 1 / sqrt(b) as the reference computes it
+
 }  // namespace cfh
 
 extern "C" {
+
+int32_t castforge_hip_quantize_int4g_hadamard(const float *src, int64_t rows, int64_t cols, int64_t group,
+                                              int64_t block, uint32_t *codes, uint16_t *scales_f16,
+                                              uint32_t *zeros, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        check_shape(rows, cols);
+        require(pow2_in(group, 16, 256), "group must be a power of two in [16, 256]");
+        require(pow2_in(block, 2, 1024), "block must be a power of two in [2, 1024]");
+        require(cols % 8 == 0 && cols % block == 0, "cols must be a multiple of 8 and of block");
+        require(cols < (int64_t{1} << 31), "cols too large");
+        if (rows == 0 || cols == 0) return;
+        require(src && codes && scales_f16 && zeros, "buffers must not be NULL");
+        require(aligned(src, 16), "src must be 16-byte aligned");
+        require(aligned(codes, 4) && aligned(scales_f16, 2) && aligned(zeros, 4),
+                "codes/zeros must be 4-byte and scales 2-byte aligned");
+        const int64_t G = (cols + group - 1) / group, ZW = (G + 7) / 8, GP = ZW * 8;
+        const float norm = hadamard_norm(block);
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        for (int64_t r0 = 0; r0 < rows; r0 += 65535) {  // one grid row per matrix row
+            const int64_t nr = std::min<int64_t>(rows - r0, 65535);
+            launch_int4g16(one_set(src + r0 * cols, nullptr, codes + r0 * (cols / 8), scales_f16 + r0 * GP,
+                                   zeros + r0 * ZW, nr),
+                           nr, cols, group, st, static_cast<int>(block), norm);
+        }
+    });
+}
 
 int32_t castforge_hip_quantize_int4g(const float *src, int64_t rows, int64_t cols, int64_t group,
                                      uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros,

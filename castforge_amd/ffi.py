@@ -129,6 +129,10 @@ SIGNATURES = {
     "castforge_hip_convert_bf16_to_f32": (c_int32, [_P, c_int64, _P, _P, _E]),
     "castforge_hip_transpose": (c_int32, [_P, c_int64, c_int64, c_int32, _P, _P, _E]),
     "castforge_hip_matmul_f32": (c_int32, [_P, c_int64, c_int64, _P, c_int64, c_int32, _P, _P, _E]),
+    "castforge_hip_rotate_hadamard": (c_int32, [_P, c_int64, c_int64, c_int64, c_int32, _P, _P, _E]),
+    "castforge_hip_quantize_int4g_hadamard": (c_int32, [_P, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _E]),
+    "castforge_hip_smoothquant_scales": (c_int32, [ctypes.c_float, ctypes.c_float, ctypes.c_float, c_int32, _P, _E]),
+    "castforge_hip_smoothquant": (c_int32, [_P, c_int64, ctypes.c_float, ctypes.c_float, c_int32, _P, _P, _E]),
     "castforge_hip_gguf_payload_bytes": (c_int32, [c_int32, c_int64, POINTER(c_int64), _E]),
     "castforge_hip_gguf_decode": (c_int32, [c_int32, _P, c_int64, _P, _P, _E]),
     "castforge_hip_gguf_encode": (c_int32, [c_int32, _P, c_int64, ctypes.c_float, _P, _P, _E]),

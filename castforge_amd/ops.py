@@ -314,6 +314,53 @@ def gemv_nf4_batched(xs: list[torch.Tensor], ps: list["Nf4Packed"], ys: list[tor
         ffi.call("castforge_hip_gemv_nf4_batched", arr, len(ps), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
 
 
+# -------------------------------------------------------------- outlier suppression ----
+def rotate_hadamard(w: torch.Tensor, block: int, axis: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Walsh-Hadamard rotation of f32 [d0, d1] in blocks of `block` along `axis` (0: down the
+    columns, rotate-hadamard's order; 1: along rows).  out may be w (in place)."""
+    w = _dev(w)
+    if w.dtype != torch.float32 or w.dim() != 2:
+        raise ValueError("rotate_hadamard takes a float32 [d0, d1] tensor")
+    out = torch.empty_like(w) if out is None else _dev(out)
+    ffi.call("castforge_hip_rotate_hadamard", _ptr(w), w.shape[0], w.shape[1], block, axis, _ptr(out), _stream(w))
+    return out
+
+
+def quantize_int4g_hadamard(w: torch.Tensor, group: int = 128, block: int = 128) -> "Int4Packed":
+    """INT4g codes of the row-wise (K-axis) Hadamard rotation of w [N, K], in one pass."""
+    w = _dev(w)
+    if w.dtype != torch.float32 or w.dim() != 2:
+        raise ValueError("quantize_int4g_hadamard takes a float32 [N, K] tensor")
+    n, k = w.shape
+    g = (k + group - 1) // group
+    zw = (g + 7) // 8
+    codes = torch.empty((n, k // 8), dtype=torch.int32, device=w.device)
+    scales = torch.empty((n, zw * 8), dtype=torch.float16, device=w.device)
+    zeros = torch.empty((n, zw), dtype=torch.int32, device=w.device)
+    ffi.call("castforge_hip_quantize_int4g_hadamard", _ptr(w), n, k, group, block, _ptr(codes), _ptr(scales),
+             _ptr(zeros), _stream(w))
+    return Int4Packed(codes, scales, zeros, n, k, group)
+
+
+def smoothquant_scales(act_max: float, w_max: float, alpha: float, bits: int = 8) -> tuple[float, float]:
+    """(s, e) of schemes.rs:231-233 with the C library's powf (host arithmetic)."""
+    out = (ctypes.c_float * 2)()
+    ffi.call("castforge_hip_smoothquant_scales", ctypes.c_float(act_max), ctypes.c_float(w_max),
+             ctypes.c_float(alpha), bits, ctypes.addressof(out))
+    return float(out[0]), float(out[1])
+
+
+def smoothquant(w: torch.Tensor, smooth_scale: float, eff_qscale: float, bits: int = 8) -> torch.Tensor:
+    """SmoothQuant fake quantization of a float32 tensor with precomputed (s, e)."""
+    w = _dev(w)
+    if w.dtype != torch.float32:
+        raise ValueError("smoothquant takes float32 values")
+    out = torch.empty_like(w)
+    ffi.call("castforge_hip_smoothquant", _ptr(w), w.numel(), ctypes.c_float(smooth_scale),
+             ctypes.c_float(eff_qscale), bits, _ptr(out), _stream(w))
+    return out
+
+
 # ----------------------------------------------------------------------------- GGUF ----
 GGML_TYPES = {"F32": ffi.GGML_F32, "F16": ffi.GGML_F16, "Q4_0": ffi.GGML_Q4_0, "Q8_0": ffi.GGML_Q8_0,
               "BF16": ffi.GGML_BF16}

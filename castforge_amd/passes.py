@@ -31,11 +31,12 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import ffi, ops
 from .ir import Dense, Module, QuantPacked, QuantUniform, TensorRef, TensorType, format_scale
-from .tensor_store import QuantizedI8, QuantizedPacked, TensorEntry
+from .tensor_store import F32Data, QuantizedI8, QuantizedPacked, TensorEntry
 
 
 # ------------------------------------------------------------------------ framework ----
@@ -76,7 +77,7 @@ OPTION_ALIASES = frozenset({
 # config/passes.toml documented options (plus `round` and `granularity`, added by this build)
 CATALOG = {
     "quantize": ["scheme", "bits", "group_size", "salient_ratio", "format", "block_size", "alpha",
-                 "round", "granularity"],
+                 "round", "granularity", "hadamard_axis"],
     "quantize-weights": ["bits", "min_elements", "round", "granularity"],
     "quantize-groupwise": ["bits", "group_size", "awq_salient", "salient_ratio"],
     "quantize-fp8": ["format", "mxfp8", "block_size"],
@@ -85,6 +86,8 @@ CATALOG = {
     "fuse-dequant-matmul": [],
     "pack-weights": [],
     "calibrate-quantize": ["bits", "samples"],
+    "rotate-hadamard": ["block_size"],
+    "smooth-quantize": ["bits", "alpha", "samples"],
 }
 
 
@@ -266,8 +269,26 @@ class QuantizePackedPass(Pass):
     name = "quantize-packed"
     description = "Packed low-bit weights (int8_channel | int4_asym | nf4 | fp8_row) for the HIP kernels"
 
-    def __init__(self, fmt: str, group: int = 0, round: str = "half_even", min_elements: int = 2):
+    def __init__(self, fmt: str, group: int = 0, round: str = "half_even", min_elements: int = 2,
+                 hadamard: int = 0):
         self.fmt, self.group, self.round, self.min_elements = fmt, group, round, min_elements
+        # int4_asym only: rotate each row's K axis in Hadamard blocks first (the block rule of
+        # formats.rs:303 applied to K; no rotation when K % b != 0)
+        self.hadamard = hadamard
+        self.rotated = 0
+
+    def _hadamard_int4(self, w: torch.Tensor):
+        k = w.shape[1]
+        b = _hadamard_block(self.hadamard, k)
+        if k % b != 0:
+            p = ops.quantize_int4g(w, self.group)
+        elif b & (b - 1):
+            raise ValueError(f"quantize: Hadamard block {b} (K = {k}) is not a power of two")
+        elif b <= 1024 and self.group >= 16:
+            p = ops.quantize_int4g_hadamard(w, self.group, b)  # one pass: rotate in registers
+        else:
+            p = ops.quantize_int4g(ops.rotate_hadamard(w, b, 1), self.group)
+        return QuantizedPacked(self.fmt, p.codes, p.scales, p.zeros, self.group, tuple(w.shape)), b
 
     def _quantize(self, w: torch.Tensor):
         if self.fmt == "int8_channel":
@@ -295,6 +316,8 @@ class QuantizePackedPass(Pass):
     def _quantize_many(self, ws: list[torch.Tensor]) -> list:
         """int8_channel / int4_asym: the batched entry points (one launch per column count);
         the results are bit-identical to _quantize per matrix."""
+        if self.hadamard and self.fmt == "int4_asym":
+            return [self._hadamard_int4(w) for w in ws]
         if self.fmt == "int8_channel":
             return [QuantizedPacked(self.fmt, c, s, None, 0, tuple(w.shape))
                     for w, (c, s) in zip(ws, ops.quantize_int8_batched(ws, 8, self.round))]
@@ -311,6 +334,12 @@ class QuantizePackedPass(Pass):
             nonlocal modified, created
             packed = self._quantize_many([v for (*_, v) in pending])
             for (oid, op, val, ty, attr, _), b in zip(pending, packed):
+                if self.hadamard and self.fmt == "int4_asym":
+                    b, hb = b
+                    op.attributes["castforge.hadamard_rotated"] = True
+                    op.attributes["castforge.hadamard_axis"] = 1
+                    _mark_users(module, val.id, {"castforge.hadamard_rotated": True, "castforge.hadamard_block": hb})
+                    self.rotated += 1
                 qty = TensorType(ty.shape, QuantPacked(self.fmt, "f32", b.group))
                 key = attr.key if isinstance(attr, TensorRef) else (val.ssa_name or f"q_weight_{modified}")
                 module.tensor_store.insert(TensorEntry(key, qty, b))
@@ -337,6 +366,12 @@ class QuantizePackedPass(Pass):
                 flush()
         flush()
         return PassResult(self.name, modified > 0, 0, modified, created)
+
+    def run_steps(self, module: Module) -> list[PassResult]:
+        """The Hadamard-fused form as the two steps it replaces (rotate, then quantize)."""
+        self.rotated = 0
+        r = self.run(module)
+        return [PassResult("rotate-hadamard", self.rotated > 0, 0, self.rotated, 0), r]
 
 
 class QuantizeGroupwisePass(Pass):
@@ -538,6 +573,120 @@ class CalibrateQuantizePass(Pass):
         return PassResult(self.name, created > 0 or modified > 0, 0, modified, created)
 
 
+def _mark_users(module: Module, vid: int, attrs: dict) -> None:
+    for uop in module.ops.values():
+        if vid in uop.operands:
+            uop.attributes.update(attrs)
+
+
+def _hadamard_block(block_size: int, k: int) -> int:
+    """formats.rs:303: next_power_of_two(block_size).min(k).max(2)."""
+    p = 1
+    while p < block_size:
+        p <<= 1
+    return max(min(p, k), 2)
+
+
+class RotateHadamardPass(Pass):
+    """formats.rs:230-343 (`rotate-hadamard`): every 2-D constant [k, n] not yet tagged
+    castforge.hadamard_rotated, with k >= 2 and n > 0, is rotated down its columns in blocks
+    of b = next_power_of_two(block_size).min(k).max(2) when k % b == 0 (on the GPU,
+    castforge_hip_rotate_hadamard, bit-exact), and is tagged either way; its users get
+    castforge.hadamard_rotated and castforge.hadamard_block = b.  A b that is not a power of
+    two (k below the block and not a power of two) makes the reference's butterfly index past
+    its buffer and panic; here it raises ValueError."""
+    name = "rotate-hadamard"
+    description = "Applies orthogonal Walsh-Hadamard rotation (QuaRot/SpinQuant) to suppress outliers"
+
+    def __init__(self, block_size: int = 4):
+        self.block_size = block_size
+
+    def run(self, module: Module) -> PassResult:
+        modified = 0
+        for oid, op in list(_const_ops(module)):
+            if not op.results or op.attributes.get("castforge.hadamard_rotated") is True:
+                continue
+            res = op.results[0]
+            ty = module.values[res].ty
+            if len(ty.shape) != 2:
+                continue
+            k, n = int(ty.shape[0]), int(ty.shape[1])
+            if k < 2 or n == 0:
+                continue
+            attr = op.attributes.get("value")
+            if attr is None:
+                continue
+            vals = module.tensor_store.resolve_f32_attr(attr, k * n)
+            if vals is None:
+                continue
+            b = _hadamard_block(self.block_size, k)
+            w = vals.reshape(k, n).float().contiguous()
+            if k % b == 0:
+                if b & (b - 1):
+                    raise ValueError(f"rotate-hadamard: block {b} (k = {k}) is not a power of two; the "
+                                     f"reference's butterfly indexes past its buffer for it")
+                w = ops.rotate_hadamard(w, b, 0)
+            v = module.values[res]
+            op.attributes["value"] = module.tensor_store.update_f32_constant(v.ssa_name, attr, ty, w.reshape(-1))
+            op.attributes["castforge.hadamard_rotated"] = True
+            _mark_users(module, res, {"castforge.hadamard_rotated": True, "castforge.hadamard_block": b})
+            modified += 1
+        return PassResult(self.name, modified > 0, 0, modified, 0)
+
+
+class SmoothQuantizePass(Pass):
+    """schemes.rs:155-298 (`smooth-quantize`, `quantize(scheme=smoothquant|smooth)`): alpha
+    clamped to [0.05, 0.95]; for every constant of >= 2 elements, with act_max its calibrated
+    bound (calibrate_value_ranges, computed once before any rewrite) and w_max its max |w| (at
+    least 1e-5), the per-tensor scalars s and e (castforge_hip_smoothquant_scales, the C
+    library's powf) and the fake quantization (q e) / s of every element
+    (castforge_hip_smoothquant) replace its values; it and its users are tagged
+    castforge.quant_scheme = "smoothquant", castforge.smoothquant_alpha, castforge.quant_bits."""
+    name = "smooth-quantize"
+    description = "Migrates activation outlier difficulty into weights via SmoothQuant alpha scaling"
+
+    def __init__(self, bits: int = 8, alpha: float = 0.5, num_samples: int = 4):
+        self.bits, self.alpha, self.num_samples = bits, alpha, num_samples
+
+    def run(self, module: Module) -> PassResult:
+        a = np.float32(self.alpha)
+        alpha = a if a != a else np.float32(min(max(a, np.float32(0.05)), np.float32(0.95)))
+        bits = 4 if self.bits == 4 else 8  # formats.rs:654-660
+        ranges = calibrate_value_ranges(module, max(self.num_samples, 1))
+        modified = 0
+        tags = {"castforge.quant_scheme": "smoothquant", "castforge.smoothquant_alpha": float(alpha),
+                "castforge.quant_bits": bits}
+        for oid, op in list(_const_ops(module)):
+            if not op.results:
+                continue
+            res = op.results[0]
+            ty = module.values[res].ty
+            n = ty.num_elements()
+            if n < 2:
+                continue
+            attr = op.attributes.get("value")
+            if attr is None:
+                continue
+            vals = module.tensor_store.resolve_f32_attr(attr, n)
+            if vals is None:
+                continue
+            vals = vals.reshape(-1).float().contiguous()
+            act_max = float(np.float32(ranges.get(res, 1.0)))
+            w_max = max(float(np.float32(ops.absmax(vals))), float(np.float32(1e-5)))
+            sc, eq = ops.smoothquant_scales(act_max, w_max, float(alpha), bits)
+            new = ops.smoothquant(vals, sc, eq, bits)
+            if isinstance(attr, TensorRef):
+                e = module.tensor_store.get(attr.key)
+                if e is not None:
+                    module.tensor_store.insert(TensorEntry(attr.key, e.ty, F32Data(new)))
+            else:
+                op.attributes["value"] = Dense(new.reshape(ty.shape))
+            op.attributes.update(tags)
+            _mark_users(module, res, tags)
+            modified += 1
+        return PassResult("quantize", modified > 0, 0, modified, 0)
+
+
 class QuantizePass(Pass):
     """schemes.rs:85-153 dispatch."""
     name = "quantize"
@@ -545,7 +694,8 @@ class QuantizePass(Pass):
 
     def __init__(self, scheme="weight", bits=8, min_elements=2, group_size=32, awq_salient=True,
                  salient_ratio=0.01, format="e4m3", mxfp8=True, block_size=32, hadamard=False,
-                 round=None, granularity="tensor", group_given=False, block_given=False, samples=4):
+                 round=None, granularity="tensor", group_given=False, block_given=False, samples=4,
+                 alpha=0.5, hadamard_axis="0"):
         self.__dict__.update(locals())
         del self.__dict__["self"]
 
@@ -554,8 +704,18 @@ class QuantizePass(Pass):
         if s in ("f16", "bf16", "mixed_precision", "amp"):
             tgt = "bf16" if s == "bf16" or self.format.lower() == "bf16" else "f16"
             return LowerMixedPrecisionPass(tgt).run(module).with_name(self.name)
-        if s in ("hadamard", "quarot", "spinquant") or self.hadamard:
-            raise ValueError("quantize: Hadamard rotation is not part of the HIP quantized-weight path")
+        if s in ("hadamard", "quarot", "spinquant"):
+            return RotateHadamardPass(max(self.block_size, 2)).run(module).with_name(self.name)
+        steps = []
+        fused_k = self.hadamard and self.hadamard_axis in ("1", "k") and s in ("int4_asym", "int4g")
+        if self.hadamard and not fused_k:
+            steps.append(RotateHadamardPass(max(self.block_size, 2)).run(module))
+        if fused_k:
+            # this build's K-axis rotation of packed [N, K] weights, fused into the INT4g kernel
+            steps += QuantizePackedPass("int4_asym", self.group_size if self.group_given else 128,
+                                        min_elements=self.min_elements,
+                                        hadamard=max(self.block_size, 2)).run_steps(module)
+            return PassResult.aggregate(self.name, steps)
         if s in ("groupwise", "awq", "gptq"):
             r = QuantizeGroupwisePass(self.bits, self.group_size, self.awq_salient or s == "awq",
                                       self.salient_ratio).run(module)
@@ -573,13 +733,15 @@ class QuantizePass(Pass):
             r = QuantizePackedPass("fp8_row", min_elements=self.min_elements).run(module)
         elif s in ("w8a8", "calibrate", "static"):
             r = CalibrateQuantizePass(self.bits, self.samples).run(module)
-        elif s in ("fp4", "mxfp4", "nvfp4", "e2m1", "smoothquant", "smooth", "qat", "qat_ste", "ste"):
+        elif s in ("smoothquant", "smooth"):
+            r = SmoothQuantizePass(self.bits, self.alpha, self.samples).run(module)
+        elif s in ("fp4", "mxfp4", "nvfp4", "e2m1", "qat", "qat_ste", "ste"):
             raise ValueError(f"quantize: scheme `{s}` is not part of the HIP quantized-weight path")
         elif self.granularity in ("channel", "per_channel"):
             r = QuantizePackedPass("int8_channel", 0, self.round or "half_even", self.min_elements).run(module)
         else:
             r = QuantizeWeightsPass(self.bits, self.min_elements, self.round or "half_away").run(module)
-        return PassResult.aggregate(self.name, [r])
+        return PassResult.aggregate(self.name, steps + [r])
 
 
 def _quantize_factory(opts: dict[str, str]) -> QuantizePass:
@@ -623,6 +785,8 @@ def _quantize_factory(opts: dict[str, str]) -> QuantizePass:
         group_given=group is not None and _usize(group, -1) > 0,
         block_given=block is not None and _usize(block, -1) > 0,
         samples=_usize(_first(opts, "samples", "num_samples"), 4),
+        alpha=_f32(opts.get("alpha"), 0.5),
+        hadamard_axis=opts.get("hadamard_axis", "0"),
     )
 
 
@@ -763,6 +927,11 @@ def default_registry() -> PassRegistry:
     reg.register("fuse-gemm", FuseGemmPass.description, lambda o: FuseGemmPass(o.get("kind", "all")))
     reg.register("fuse-dequant-matmul", FuseDequantMatmulPass.description, lambda o: FuseDequantMatmulPass())
     reg.register("pack-weights", PackWeightsPass.description, lambda o: PackWeightsPass())
+    reg.register("rotate-hadamard", RotateHadamardPass.description,
+                 lambda o: RotateHadamardPass(_usize(_first(o, "block_size", "size"), 4)))
+    reg.register("smooth-quantize", SmoothQuantizePass.description,
+                 lambda o: SmoothQuantizePass(_u8(o.get("bits"), 8), _f32(o.get("alpha"), 0.5),
+                                              _usize(_first(o, "samples", "num_samples"), 4)))
     reg.register("calibrate-quantize", "Profile-guided static W8A8/W4A8 calibration and quantization",
                  lambda o: CalibrateQuantizePass(_u8(o.get("bits"), 8),
                                                  _usize(_first(o, "samples", "num_samples"), 4)))

@@ -262,6 +262,42 @@ int32_t castforge_hip_convert_bf16_to_f32(const uint16_t *src, int64_t n, float 
 int32_t castforge_hip_static_quantize(const float *x, int64_t n, float scale, int32_t bits, float *y,
                                       void *stream, char **out_error);
 
+/* ---- outlier suppression (passes/quantize/formats.rs:230-343, schemes.rs:155-298) ------------ */
+
+/* Replaces RotateHadamardPass::run's loop (formats.rs:303-327): dst = the Walsh-Hadamard
+ * rotation of f32 [d0, d1] in blocks of `block` consecutive elements along `axis`: each block
+ * through the radix-2 butterfly (x + y, x - y; stages h = 1, 2, .., block/2 in order), then
+ * times 1.0f / sqrtf(block).  axis 0 rotates down the columns as the reference does for a
+ * [k, n] constant; axis 1 along rows (the K axis of an [N, K] weight or of activations).
+ * block: a power of two >= 2 dividing the axis length (the pass resolves the reference's
+ * next_power_of_two(block_size).min(k).max(2) and skips the rotation when k % b != 0).
+ * dst may equal src.  Bit-exact with the reference's f32 loop. */
+int32_t castforge_hip_rotate_hadamard(const float *src, int64_t d0, int64_t d1, int64_t block, int32_t axis,
+                                      float *dst, void *stream, char **out_error);
+
+/* INT4g quantization of the row-wise Hadamard rotation of src [rows, cols] in one pass: the
+ * codes castforge_hip_quantize_int4g gives for castforge_hip_rotate_hadamard(src, rows, cols,
+ * block, axis 1), without writing the rotated f32 tensor.  This is the K-axis rotation of
+ * QuaRot on an [N, K] weight, equal to rotate-hadamard on the [K, N] form followed by
+ * pack-weights.  group: power of two in [16, 256]; block: power of two in [2, 1024]
+ * dividing cols. */
+int32_t castforge_hip_quantize_int4g_hadamard(const float *src, int64_t rows, int64_t cols, int64_t group,
+                                              int64_t block, uint32_t *codes, uint16_t *scales_f16,
+                                              uint32_t *zeros, void *stream, char **out_error);
+
+/* SmoothQuant scalars of schemes.rs:231-233 (host arithmetic, no device work), with act_max
+ * the constant's calibrated bound, w_max = max(max |w|, 1e-5) and alpha already clamped to
+ * [0.05, 0.95]: out_scales[0] = s = max(max(act_max, 1e-4)^alpha / w_max^(1 - alpha), 1e-4),
+ * out_scales[1] = e = max(w_max * s / qmax, 1e-6), qmax = 7 (bits 4) or 127; powf is the C
+ * library's, as f32::powf is in the reference. */
+int32_t castforge_hip_smoothquant_scales(float act_max, float w_max, float alpha, int32_t bits, float *out_scales,
+                                         char **out_error);
+/* Replaces the element loop of run_smoothquant (schemes.rs:234-238): out[i] =
+ * (clamp(round_half_away((w[i] * s) / e), qmin, qmax) * e) / s, NaN kept, [qmin, qmax] =
+ * [-8, 7] (bits 4) or [-128, 127].  out may equal w. */
+int32_t castforge_hip_smoothquant(const float *w, int64_t n, float smooth_scale, float eff_qscale, int32_t bits,
+                                  float *out, void *stream, char **out_error);
+
 /* ---- GGUF payloads (ir/formats/gguf.rs) --------------------------------------------------- */
 
 /* GgmlType ids of the reference's GGUF reader / writer (gguf.rs:16-37). */

@@ -691,3 +691,64 @@ int64_t orc_gguf_encode_q8_0(const int8_t *codes, int64_t n, float scale, uint8_
     }
     return blocks * 34;
 }
+
+/* ---- outlier suppression ----------------------------------------------------------------- */
+/* formats.rs:301-327 (RotateHadamardPass::run): w is a [k, n] constant; b =
+ * next_power_of_two(block_size).min(k).max(2); when k % b == 0, every column's blocks of b
+ * consecutive rows go through the butterfly stages h = 1, 2, .., b/2 (buf[j] = x + y,
+ * buf[j+h] = x - y) and are written back times norm = 1 / sqrt(b); otherwise w is unchanged.
+ * Returns b, or -1 when b is not a power of two (the reference's butterfly then indexes past
+ * its buffer and panics). */
+int64_t orc_rotate_hadamard(float *w, int64_t k, int64_t n, int64_t block_size) {
+    int64_t p = 1;
+    while (p < block_size) p <<= 1;
+    int64_t b = p < k ? p : k;
+    if (b < 2) b = 2;
+    if (k % b != 0) return b;
+    if ((b & (b - 1)) != 0) return -1;
+    const float norm = 1.0f / sqrtf((float)b);
+    float *buf = (float *)malloc(sizeof(float) * (size_t)b);
+    for (int64_t col = 0; col < n; ++col) {
+        for (int64_t kb = 0; kb < k; kb += b) {
+            for (int64_t i = 0; i < b; ++i) buf[i] = w[(kb + i) * n + col];
+            for (int64_t h = 1; h < b; h *= 2)
+                for (int64_t i = 0; i < b; i += 2 * h)
+                    for (int64_t j = i; j < i + h; ++j) {
+                        const float x = buf[j], y = buf[j + h];
+                        buf[j] = x + y;
+                        buf[j + h] = x - y;
+                    }
+            for (int64_t i = 0; i < b; ++i) w[(kb + i) * n + col] = buf[i] * norm;
+        }
+    }
+    free(buf);
+    return b;
+}
+
+static float rust_maxf(float a, float b) { return isnan(a) ? b : (isnan(b) ? a : (a > b ? a : b)); }
+
+/* schemes.rs:188-238 (run_smoothquant) for one constant of n elements with act_max its
+ * calibrated bound (as f32): alpha clamped to [0.05, 0.95]; w_max = max over |w| (NaN
+ * skipped), at least 1e-5; s = max(max(act_max, 1e-4)^alpha / w_max^(1 - alpha), 1e-4);
+ * e = max(w_max * s / qmax, 1e-6); w[i] = (clamp(round(w[i] * s / e), qmin, qmax) * e) / s.
+ * scales_out (may be NULL) receives s and e. */
+void orc_smoothquant(float *w, int64_t n, float act_max, float alpha, int bits, float *scales_out) {
+    int eff_bits;
+    float qmin, qmax;
+    orc_int_bounds(bits, &eff_bits, &qmin, &qmax);
+    alpha = rust_clamp(alpha, 0.05f, 0.95f);
+    float w_max = 0.0f;
+    for (int64_t i = 0; i < n; ++i) w_max = rust_maxf(w_max, fabsf(w[i]));
+    w_max = rust_maxf(w_max, 1e-5f);
+    const float s = rust_maxf(powf(rust_maxf(act_max, 1e-4f), alpha) / powf(w_max, 1.0f - alpha), 1e-4f);
+    const float e = rust_maxf(w_max * s / qmax, 1e-6f);
+    for (int64_t i = 0; i < n; ++i) {
+        const float migrated = w[i] * s;
+        const float q = rust_clamp(roundf(migrated / e), qmin, qmax);
+        w[i] = (q * e) / s;
+    }
+    if (scales_out) {
+        scales_out[0] = s;
+        scales_out[1] = e;
+    }
+}

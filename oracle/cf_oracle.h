@@ -113,6 +113,11 @@ enum { ORC_GGML_F32 = 0, ORC_GGML_F16 = 1, ORC_GGML_Q4_0 = 2, ORC_GGML_Q8_0 = 8,
 int64_t orc_gguf_decode(int type, const uint8_t *raw, int64_t num_elems, float *out);
 int64_t orc_gguf_encode_q8_0(const int8_t *codes, int64_t n, float scale, uint8_t *out);
 
+/* formats.rs:301-327 (rotate-hadamard of a [k, n] constant, in place; returns b or -1) and
+ * schemes.rs:188-238 (smooth-quantize of one constant, in place) */
+int64_t orc_rotate_hadamard(float *w, int64_t k, int64_t n, int64_t block_size);
+void orc_smoothquant(float *w, int64_t n, float act_max, float alpha, int bits, float *scales_out);
+
 void orc_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *qw,
                   const float *sw, int64_t n, int64_t k, float *out);
 

@@ -62,6 +62,8 @@ def lib() -> ctypes.CDLL:
             "orc_static_quantize": (None, [P, I64, c_float, c_int, P]),
             "orc_gguf_decode": (I64, [c_int, P, I64, P]),
             "orc_gguf_encode_q8_0": (I64, [P, I64, c_float, P]),
+            "orc_rotate_hadamard": (I64, [P, I64, I64, I64]),
+            "orc_smoothquant": (None, [P, I64, c_float, c_float, c_int, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(l, name)
@@ -207,6 +209,23 @@ def gguf_encode_q8_0(codes: np.ndarray, scale: float) -> np.ndarray:
     n = lib().orc_gguf_encode_q8_0(_p(codes) if codes.size else 0, codes.size, np.float32(scale), _p(out))
     assert n == out.size
     return out
+
+
+# ------------------------------------------------------------ outlier suppression ----
+def rotate_hadamard(w: np.ndarray, block_size: int):
+    """(rotated copy of a [k, n] array, the resolved block b or -1)."""
+    w = np.array(w, np.float32, order="C", copy=True)
+    k, n = w.shape
+    b = lib().orc_rotate_hadamard(_p(w), k, n, block_size)
+    return w, b
+
+
+def smoothquant(w: np.ndarray, act_max: float, alpha: float = 0.5, bits: int = 8):
+    """(fake-quantized copy, smoothing scale s, quantizer step e)."""
+    w = np.array(w, np.float32, order="C", copy=True)
+    sc = np.zeros(2, np.float32)
+    lib().orc_smoothquant(_p(w), w.size, np.float32(act_max), np.float32(alpha), bits, _p(sc))
+    return w, sc[0], sc[1]
 
 
 # ---------------------------------------------------------------------- GEMMs ----
