@@ -258,6 +258,15 @@ def main():
         components["quantize_int8_channel_GBps"] = round((nel * 5 + nrows * 4) / (st * 1e-3) / 1e9, 1)
         log(f"[bench] quantize int4g {components['quantize_int4g128_GBps']} GB/s, "
             f"int8 {components['quantize_int8_channel_GBps']} GB/s")
+        # QuaRot-style K-axis Hadamard (block 128) fused into the INT4 g128 quantizer (same
+        # bytes as plain quantize: the rotated f32 tensor is never written), and the rotation
+        # alone along K (f32 read + write)
+        st = time_steps(lambda i: [ops.quantize_int4g_hadamard(w, 128, 128) for w in block_f32], 10, 2)
+        components["quantize_int4g128_hadamard128_GBps"] = round(q4_bytes / (st * 1e-3) / 1e9, 1)
+        st = time_steps(lambda i: [ops.rotate_hadamard(w, 128, 1) for w in block_f32], 10, 2)
+        components["rotate_hadamard128_GBps"] = round(8 * nel / (st * 1e-3) / 1e9, 1)
+        log(f"[bench] hadamard128+int4g {components['quantize_int4g128_hadamard128_GBps']} GB/s, "
+            f"rotation {components['rotate_hadamard128_GBps']} GB/s")
 
         # W8A16 GEMV M=1 over rotating copies of the INT8 block (config 1)
         q8 = [ops.quantize_int8(w, 8, "channel", "half_even") for w in block_f32]
