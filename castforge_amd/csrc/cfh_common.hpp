@@ -93,6 +93,46 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float v) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
 }
 
+// The value of lane (lane ^ D) of the wave.  D = 1, 2: DPP quad permutations; D = 4: DPP row
+// shifts (lanes with bit 2 clear read lane + 4, the others lane - 4); D = 8: DPP row rotate by
+// 8; D = 16, 32: ds_bpermute.  DPP moves run on the VALU, without the LDS permute unit.
+template <int D>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    if constexpr (D == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+    else if constexpr (D == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+    else if constexpr (D == 4) {
+        const int up = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0xF, false);  // row_shl:4, lane + 4
+        const int dn = __builtin_amdgcn_mov_dpp(x, 0x114, 0xF, 0xF, false);  // row_shr:4, lane - 4
+        return __builtin_bit_cast(float, (threadIdx.x & 4) ? dn : up);
+    } else if constexpr (D == 8) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false));
+    else return __shfl_xor(v, D);
+}
+
+// One cross-lane butterfly stage over N values per lane against lane ^ D: the lane with bit D
+// clear holds position j and keeps x + y, its partner holds j + h and keeps x - y (x the lower
+// lane's value, y the upper's), exactly the reference's buf[j] / buf[j + h] update.
+template <int D, int N>
+__device__ __forceinline__ void lane_butterfly(float (&v)[N]) {
+    const bool lower = (threadIdx.x & D) == 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const float p = lane_xor<D>(v[i]);
+        v[i] = lower ? v[i] + p : p - v[i];
+    }
+}
+
+// Cross-lane stages for partner distances 1, 2, 4, .. below `lanes` (lanes <= 64).
+template <int N>
+__device__ __forceinline__ void lane_butterflies(float (&v)[N], int lanes) {
+    if (lanes > 1) lane_butterfly<1, N>(v);
+    if (lanes > 2) lane_butterfly<2, N>(v);
+    if (lanes > 4) lane_butterfly<4, N>(v);
+    if (lanes > 8) lane_butterfly<8, N>(v);
+    if (lanes > 16) lane_butterfly<16, N>(v);
+    if (lanes > 32) lane_butterfly<32, N>(v);
+}
+
 // OCP E4M3FN encode, bit-exact with the reference codec (mutable_loads.rs:367-411):
 // integer round-half-even with saturation to +-448 (0x7E/0xFE), NaN -> 0x7F, plus the 16
 // inputs just below a power of two where the reference's floor(log2f(|v|)) rounds up and it

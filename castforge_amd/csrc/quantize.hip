@@ -501,16 +501,7 @@ __device__ __forceinline__ void hadamard16_lanes(float (&x)[16], int rot_b, floa
                 x[j + h] = a - b;
             }
     }
-    const int lane = threadIdx.x & 63;
-    for (int h = 16; h < rot_b; h *= 2) {  // wave-uniform
-        const int d = h >> 4;
-        const bool lower = (lane & d) == 0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float p = __shfl_xor(x[i], d);
-            x[i] = lower ? x[i] + p : p - x[i];
-        }
-    }
+    lane_butterflies<16>(x, rot_b >> 4);  // stages h = 16 .. rot_b / 2 (wave-uniform)
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] *= norm;
 }

@@ -80,13 +80,12 @@ __global__ __launch_bounds__(kBlock) void fwht_strided_kernel(const float *src, 
 
 // First phase along contiguous rows: the flattened tensor in segments of 512 values, lane l
 // of a wave owning values 8l .. 8l+7 of its segment.  Stages h < 8 run in registers, stages
-// 8 <= h < ext (ext <= 512) against lane l ^ (h / 8): the lower lane keeps x + y, the upper
-// x - y with x the lower lane's value.  Blocks never straddle rows (b divides the row length).
+// 8 <= h < ext (ext <= 512) against lane l ^ (h / 8) (lane_butterflies).  Blocks never
+// straddle rows (b divides the row length).
 template <bool VEC>
 __global__ __launch_bounds__(kBlock) void fwht_rows_wave_kernel(const float *src, float *dst, int64_t n, int ext,
                                                                 float norm) {
     const int64_t e = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8;
-    const int lane = threadIdx.x & 63;
     float v[8];
     if (VEC && e + 8 <= n) {
         const float4 a = *reinterpret_cast<const float4 *>(src + e), b = *reinterpret_cast<const float4 *>(src + e + 4);
@@ -107,15 +106,7 @@ __global__ __launch_bounds__(kBlock) void fwht_rows_wave_kernel(const float *src
                 v[j + h] = x - y;
             }
     }
-    for (int h = 8; h < ext; h *= 2) {  // wave-uniform
-        const int d = h >> 3;
-        const bool lower = (lane & d) == 0;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float p = __shfl_xor(v[i], d);
-            v[i] = lower ? v[i] + p : p - v[i];
-        }
-    }
+    lane_butterflies<8>(v, ext >> 3);  // stages h = 8 .. ext / 2 (wave-uniform)
     if (norm != 0.0f) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] *= norm;
