@@ -252,7 +252,8 @@ def test_fp8_rows_boundaries_many_scale_decades(cuda):
     assert np.array_equal(codes.cpu().numpy(), c_ref)
 
 
-@pytest.mark.parametrize("r,c", [(16, 512), (4096, 4096 // 8), (3, 11)])
+@pytest.mark.parametrize("r,c", [(16, 512), (4096, 4096 // 8), (3, 11), (5, 4096), (7, 11008), (6, 520),
+                                 (2, 12288), (3, 12296), (4097, 64)])
 def test_fp8_rows_bf16_bit_exact(cuda, r, c):
     x = synth.activations_bf16(42, 1, r, c)
     c_ref, s_ref = O.quantize_fp8_rows(x)
@@ -262,6 +263,21 @@ def test_fp8_rows_bf16_bit_exact(cuda, r, c):
     d = ops.dequantize_fp8(codes, scales).cpu().numpy()
     dec = torch.from_numpy(c_ref).view(torch.float8_e4m3fn).float().numpy() * s_ref[:, None]
     assert np.array_equal(d, dec)
+
+
+def test_fp8_rows_bf16_special_values(cuda):
+    """bf16 rows with NaN, Inf, signed zeros, subnormals, values at the saturation edges and
+    an all-zero row, through the one-wave-per-row kernel (cols % 8 == 0)."""
+    x = synth.activations_bf16(43, 1, 6, 1024).copy()
+    f = np.array([np.nan, np.inf, -np.inf, -0.0, 0.0, 1e-40, -1e-40, 448.0, -464.0, 3e38], np.float32)
+    x[0, :f.size] = O.f32_to_bf16_bits(f)
+    x[1, :] = O.f32_to_bf16_bits(np.zeros(1024, np.float32))
+    x[2, 5] = O.f32_to_bf16_bits(np.array([np.inf], np.float32))[0]
+    x[3, 7] = O.f32_to_bf16_bits(np.array([1e-38], np.float32))[0]
+    c_ref, s_ref = O.quantize_fp8_rows(x)
+    codes, scales = ops.quantize_fp8(torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(cuda))
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(codes.cpu().numpy(), c_ref)
 
 
 # ------------------------------------------------------------- BASELINE block shapes ----
