@@ -1212,8 +1212,24 @@ int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m,
         require(aligned(codes, 16) && aligned(scales_f16, 16), "codes and scales must be 16-byte aligned");
         hipStream_t st = static_cast<hipStream_t>(stream);
         const int yb = y_dtype == CFH_DTYPE_BF16;
-        if (!gemv_try_skinny(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st))
-            gemv_generic(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st);
+        Problem p{x, codes, scales_f16, nullptr, y, n, k, 32, 1, 0, 0};
+        if (m <= 16 && skinny_ok(fmt, p, 1)) {
+            // each activation row is one M = 1 problem of the split-K kernel, up to 8 per launch;
+            // the rows re-read the same planes, which the MALL holds between them
+            const int esz = yb ? 2 : 4;
+            Problem ps[kMaxProblems];
+            for (int64_t r0 = 0; r0 < m; r0 += kMaxProblems) {
+                const int cnt = static_cast<int>(std::min<int64_t>(m - r0, kMaxProblems));
+                for (int i = 0; i < cnt; ++i) {
+                    ps[i] = p;
+                    ps[i].x = x + (r0 + i) * k;
+                    ps[i].y = static_cast<uint8_t *>(y) + (r0 + i) * n * esz;
+                }
+                launch_skinny(fmt, ps, cnt, 1, yb, st);
+            }
+            return;
+        }
+        gemv_generic(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st);
     });
 }
 
