@@ -239,6 +239,28 @@ __global__ __launch_bounds__(kBlock) void gguf_planes_dequant_kernel(const uint8
     }
 }
 
+// Q4_0 planes -> the INT4g layout (natural code order, group 32, zero point 8): one thread per
+// (row, chunk, part); part p's word j is word p of the chunk's block j, which INT4g keeps at
+// word 4j + p of the chunk.  The scale plane is shared as it is ([rows, GP] f16 in both).
+__global__ __launch_bounds__(kBlock) void gguf_q4_to_int4g_kernel(const uint8_t *codes, int64_t rows, int64_t k,
+                                                                  uint32_t *out, uint32_t *zeros) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t chunks = k / 128;
+    if (t >= rows * chunks * 4) return;
+    const int p = static_cast<int>(t & 3);
+    const int64_t c = (t >> 2) % chunks, r = (t >> 2) / chunks;
+    const uint4 v = *reinterpret_cast<const uint4 *>(codes + r * (k / 2) + c * 64 + 16 * p);
+    uint32_t *o = out + r * (k / 8) + c * 16 + p;
+    o[0] = v.x;
+    o[4] = v.y;
+    o[8] = v.z;
+    o[12] = v.w;
+    if (t % (chunks * 4) == 0) {
+        const int64_t zw = (k / 32 + 7) / 8;
+        for (int64_t i = 0; i < zw; ++i) zeros[r * zw + i] = 0x88888888u;
+    }
+}
+
 unsigned grid_for(int64_t threads) {
     const int64_t g = (threads + kBlock - 1) / kBlock;
     require(g <= 0x7fffffff, "tensor too large for one launch");
@@ -393,6 +415,20 @@ int32_t castforge_hip_gguf_unpack(int32_t ggml_type, const void *codes, const ui
         else
             gguf_unpack_kernel<CFH_GGML_Q8_0><<<g, kBlock, 0, st>>>(c, scales_f16, rows, k, static_cast<uint8_t *>(raw_out));
         check_launch("gguf_unpack");
+    });
+}
+
+int32_t castforge_hip_gguf_q4_0_to_int4g(const void *codes, int64_t rows, int64_t k, uint32_t *int4_codes,
+                                         uint32_t *zeros, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(rows >= 0 && k >= 0 && k % 128 == 0, "Q4_0 planes need k % 128 == 0");
+        if (rows == 0 || k == 0) return;
+        require(codes && int4_codes && zeros, "buffers must not be NULL");
+        require(aligned(codes, 16) && aligned(int4_codes, 4) && aligned(zeros, 4),
+                "codes must be 16-byte, int4_codes and zeros 4-byte aligned");
+        gguf_q4_to_int4g_kernel<<<grid_for(rows * (k / 128) * 4), kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+            static_cast<const uint8_t *>(codes), rows, k, int4_codes, zeros);
+        check_launch("gguf_q4_to_int4g");
     });
 }
 

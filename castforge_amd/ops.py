@@ -463,9 +463,24 @@ def dequantize_gguf(p: GgufPacked) -> torch.Tensor:
     return out
 
 
+def gguf_q4_0_to_int4g(p: GgufPacked) -> Int4Packed:
+    """The INT4g form (group 32, zero point 8) of Q4_0 planes; the scale plane is shared."""
+    if p.ggml_type != ffi.GGML_Q4_0:
+        raise ValueError("only Q4_0 planes have an INT4g form")
+    zw = (p.k // 32 + 7) // 8
+    codes = torch.empty((p.n, p.k // 8), dtype=torch.int32, device=p.codes.device)
+    zeros = torch.empty((p.n, zw), dtype=torch.int32, device=p.codes.device)
+    ffi.call("castforge_hip_gguf_q4_0_to_int4g", _ptr(p.codes), p.n, p.k, _ptr(codes), _ptr(zeros), _stream(p.codes))
+    return Int4Packed(codes, p.scales, zeros, p.n, p.k, 32)
+
+
 def gemm_gguf(x: torch.Tensor, p: GgufPacked, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """y [M, n] = x [M, k] (bf16) times decode(W)^T over GGUF planes."""
+    """y [M, n] = x [M, k] (bf16) times decode(W)^T over GGUF planes.  Q4_0 at M > 16 runs the
+    INT4g prefill MFMA kernel on a transient INT4g form of the planes (one pass over 0.56 B
+    per weight, small next to the GEMM)."""
     x = _check_x(x, p.k)
+    if x.shape[0] > 16 and p.ggml_type == ffi.GGML_Q4_0:
+        return gemm_w4a16(x, gguf_q4_0_to_int4g(p), out_dtype)
     y = torch.empty((x.shape[0], p.n), dtype=out_dtype, device=x.device)
     ffi.call("castforge_hip_gemv_gguf", p.ggml_type, _ptr(x), x.shape[0], p.n, p.k, _ptr(p.codes),
              _ptr(p.scales), _ptr(y), _out_dtype(out_dtype), _stream(x))

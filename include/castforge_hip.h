@@ -347,6 +347,12 @@ int32_t castforge_hip_gguf_repack(int32_t ggml_type, const void *raw, int64_t ro
 /* Planes back to the block payload (the inverse of castforge_hip_gguf_repack). */
 int32_t castforge_hip_gguf_unpack(int32_t ggml_type, const void *codes, const uint16_t *scales_f16, int64_t rows,
                                   int64_t k, void *raw_out, void *stream, char **out_error);
+/* Q4_0 planes to the INT4g layout (group 32, every zero point 8): int4_codes u32 [rows, k/8],
+ * zeros u32 [rows, ceil(k/32 / 8)] = 0x88888888; the planes' scales_f16 serve unchanged as
+ * INT4g scales.  (q - 8) * d is the INT4g dequant of the same block, so castforge_hip_gemv_w4a16
+ * (prefill MFMA kernel at M > 16) then computes the Q4_0 matmul. */
+int32_t castforge_hip_gguf_q4_0_to_int4g(const void *codes, int64_t rows, int64_t k, uint32_t *int4_codes,
+                                         uint32_t *zeros, void *stream, char **out_error);
 /* Planes to f32 [rows, k]: the values decode_ggml_tensor gives for the same blocks. */
 int32_t castforge_hip_dequantize_gguf(int32_t ggml_type, const void *codes, const uint16_t *scales_f16,
                                       int64_t rows, int64_t k, float *out, void *stream, char **out_error);

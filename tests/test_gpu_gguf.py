@@ -193,6 +193,21 @@ def test_gemv_matches_oracle(cuda, ty, m, n, k, out):
     _close(y, ref)
 
 
+@pytest.mark.parametrize("m,n,k", [(64, 96, 1024), (300, 256, 4096), (17, 48, 256)])
+def test_q4_0_prefill_through_int4g(cuda, m, n, k):
+    """Q4_0 at M > 16: the INT4g form of the planes dequantizes to the same values bit for bit,
+    and the prefill MFMA kernel over it matches the oracle's decode-then-matmul."""
+    raw = _blocks(Q4_0, n * k // 32, 700 + m)
+    p = ops.gguf_repack(Q4_0, _dev_u8(raw, cuda), n, k)
+    i4 = ops.gguf_q4_0_to_int4g(p)
+    _same(ops.dequantize_int4g(i4).cpu().numpy().reshape(-1), O.gguf_decode(Q4_0, raw, n * k))
+    xb, x = _x(701, m, k, cuda)
+    y = ops.gemm_gguf(x, p, torch.float32)
+    torch.cuda.synchronize()
+    w = O.gguf_decode(Q4_0, raw, n * k).reshape(n, k)
+    _close(y, O.matmul_2d(O.bf16_bits_to_f32(xb.reshape(m, k)), w, packed_rhs=True))
+
+
 @pytest.mark.parametrize("ty", [Q4_0, Q8_0])
 def test_gemv_batched_block_matches_single_and_torch(cuda, ty):
     """The seven LLaMA-7B block projections in one launch: equal to one call per matrix, and
