@@ -44,7 +44,8 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
-enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2 };
+// FMT_Q8G: GGUF Q8_0 planes (int8 codes, one f16 d per 32; same number as the GEMV's FMT_Q8_0)
+enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2, FMT_Q8G = 4 };
 
 constexpr int kThreads = 256;
 constexpr int BK = 32;     // K elements per slice: one 64-byte f16 row per tile row
@@ -86,7 +87,7 @@ __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 3); }
 template <int FMT>
 __device__ __forceinline__ int perm_src(int i) {
     if constexpr (FMT == FMT_INT4) return (i >> 1) + ((i & 1) << 2);
-    else if constexpr (FMT == FMT_INT8) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
+    else if constexpr (FMT == FMT_INT8 || FMT == FMT_Q8G) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
     else return i;
 }
 
@@ -143,7 +144,7 @@ void prefill_qgemm_kernel(PfArgs a) {
     constexpr int kXPieces = BM * 4 / kThreads;  // 16-byte x pieces per thread
     constexpr int kWRowsPerThread = BN >= kThreads ? BN / kThreads : 1;
     constexpr int kWThreadsPerRow = BN >= kThreads ? 1 : kThreads / BN;  // split a row's bytes
-    constexpr int kWBytesRow = FMT == FMT_INT8 ? 32 : 16;
+    constexpr int kWBytesRow = FMT == FMT_INT8 || FMT == FMT_Q8G ? 32 : 16;
     constexpr int kWBytesThread = kWBytesRow / kWThreadsPerRow;  // 16, 8 or 4 (per row)
     static_assert(kXPieces >= 1 && kWRowsPerThread == 1, "tile / thread mapping");
     static_assert(kWBytesThread >= 4, "W bytes per thread");
@@ -177,15 +178,17 @@ void prefill_qgemm_kernel(PfArgs a) {
     // ---- global sources (descriptors over the tile's rows: rows past M / N read zero) ----
     const int m_valid = min(BM, M - m0), n_valid = min(BN, N - n0);
     const rsrc_t rx = make_rsrc(a.x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(m_valid) * K * 2);
-    const int64_t w_row_bytes = FMT == FMT_INT8 ? K : K / 2;
+    const int64_t w_row_bytes = FMT == FMT_INT8 || FMT == FMT_Q8G ? K : K / 2;
     const rsrc_t rw = make_rsrc(static_cast<const uint8_t *>(a.codes) + n0 * w_row_bytes,
                                 static_cast<uint32_t>(n_valid * w_row_bytes));
     const int G = (K + a.group - 1) / a.group;     // INT4 groups / NF4 blocks per row
     const int ZW = (G + 7) / 8, GP = ZW * 8;
     rsrc_t rs = make_rsrc(a.codes, 0), rz = rs;  // empty ranges unless the format has metadata
-    if constexpr (FMT == FMT_INT4) {
+    if constexpr (FMT == FMT_INT4 || FMT == FMT_Q8G) {
         rs = make_rsrc(static_cast<const uint16_t *>(a.scales) + static_cast<int64_t>(n0) * GP,
                        static_cast<uint32_t>(n_valid) * GP * 2);
+    }
+    if constexpr (FMT == FMT_INT4) {
         rz = make_rsrc(a.zeros + static_cast<int64_t>(n0) * ZW, static_cast<uint32_t>(n_valid) * ZW * 4);
     } else if constexpr (FMT == FMT_NF4) {
         rs = make_rsrc(static_cast<const float *>(a.scales) + static_cast<int64_t>(n0) * G,
@@ -212,7 +215,18 @@ void prefill_qgemm_kernel(PfArgs a) {
                                                    rx, static_cast<uint32_t>(row * K + k0 + ch * 8) * 2, 0, 0));
         }
         const uint32_t wo = static_cast<uint32_t>(wr * w_row_bytes + (FMT == FMT_INT8 ? k0 : k0 / 2) + wb);
-        if constexpr (kWBytesThread >= 16) {
+        if constexpr (FMT == FMT_Q8G) {
+            // the slice is one block; its 8-byte piece p (elements 8p..8p+7) sits at byte
+            // 16 p + 8 (block & 1) of the block's 64-byte chunk
+            const uint32_t cb = static_cast<uint32_t>(wr * w_row_bytes + (k0 >> 6) * 64 + 8 * ((k0 >> 5) & 1));
+#pragma unroll
+            for (int h = 0; h < kWBytesThread / 8; ++h) {
+                const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                              rw, cb + 16 * (wb / 8 + h), 0, 0));
+                r.w[2 * h] = v.x;
+                r.w[2 * h + 1] = v.y;
+            }
+        } else if constexpr (kWBytesThread >= 16) {
 #pragma unroll
             for (int h = 0; h < kWBytesThread / 16; ++h) {
                 const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 16 * h, 0, 0));
@@ -226,8 +240,9 @@ void prefill_qgemm_kernel(PfArgs a) {
         }
         // raw metadata words only: decoding them here would wait for the loads
         const int g = k0 / a.group;
-        if constexpr (FMT == FMT_INT4) {
+        if constexpr (FMT == FMT_INT4 || FMT == FMT_Q8G)
             r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<uint32_t>(wr * GP + (g & ~1)) * 2, 0, 0);
+        if constexpr (FMT == FMT_INT4) {
             r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, static_cast<uint32_t>(wr * ZW + (g >> 3)) * 4, 0, 0);
         } else if constexpr (FMT == FMT_NF4) {
             r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<uint32_t>(wr * G + g) * 4, 0, 0);
@@ -285,6 +300,27 @@ void prefill_qgemm_kernel(PfArgs a) {
                 for (int q = 0; q < 4; ++q) {
                     const uint2 e = lut[(r.w[t] >> (8 * q)) & 255u];
                     split_pair(__uint_as_float(e.x) * am, __uint_as_float(e.y) * am, hi[q], lo[q]);
+                }
+                const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
+                *reinterpret_cast<uint4 *>(wplane + off) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+                *reinterpret_cast<uint4 *>(wplane + kWPlane + off) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            }
+        } else if constexpr (FMT == FMT_Q8G) {
+            // exact q f16 pairs times the block's f16 d, split into hi = f16(q d) and the exact
+            // remainder lo (a product of at most 19 significant bits)
+            const int g = kt * BK / a.group;
+            const uint32_t s2 = ((g & 1) ? (r.s >> 16) : (r.s & 0xFFFFu)) * 0x00010001u;
+#pragma unroll
+            for (int t = 0; t < kWBytesThread / 8; ++t) {
+                const int ch = wb / 8 + t;
+                uint32_t qv[4], hi[4], lo[4];
+                int8_word_q(r.w[2 * t], qv);
+                int8_word_q(r.w[2 * t + 1], qv + 2);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const half2_t h = as_h2(qv[q]) * as_h2(s2);
+                    hi[q] = as_u(h);
+                    lo[q] = as_u(__builtin_elementwise_fma(as_h2(qv[q]), as_h2(s2), -h));
                 }
                 const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
                 *reinterpret_cast<uint4 *>(wplane + off) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -519,6 +555,7 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
     if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
     else if (fmt == FMT_NF4) launch_fmt<FMT_NF4>(a, st);
+    else if (fmt == FMT_Q8G) launch_fmt<FMT_Q8G>(a, st);
     else launch_fmt<FMT_INT8>(a, st);
     return true;
 }

@@ -208,6 +208,22 @@ def test_q4_0_prefill_through_int4g(cuda, m, n, k):
     _close(y, O.matmul_2d(O.bf16_bits_to_f32(xb.reshape(m, k)), w, packed_rhs=True))
 
 
+@pytest.mark.parametrize("m,n,k", [(64, 96, 1024), (300, 256, 4096), (17, 48, 256), (130, 1000, 2048)])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_q8_0_prefill_reads_planes(cuda, m, n, k, out):
+    """Q8_0 at M > 16: the prefill MFMA kernel reads the planes directly (one block per
+    32-element slice) and matches the oracle's decode-then-matmul."""
+    raw = _blocks(Q8_0, n * k // 32, 800 + m)
+    p = ops.gguf_repack(Q8_0, _dev_u8(raw, cuda), n, k)
+    xb, x = _x(801, m, k, cuda)
+    y = ops.gemm_gguf(x, p, out)
+    torch.cuda.synchronize()
+    ref = O.matmul_2d(O.bf16_bits_to_f32(xb.reshape(m, k)), O.gguf_decode(Q8_0, raw, n * k).reshape(n, k), True)
+    if out == torch.bfloat16:
+        ref = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref))
+    _close(y, ref)
+
+
 @pytest.mark.parametrize("ty", [Q4_0, Q8_0])
 def test_gemv_batched_block_matches_single_and_torch(cuda, ty):
     """The seven LLaMA-7B block projections in one launch: equal to one call per matrix, and
