@@ -44,8 +44,9 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
-// FMT_Q8G: GGUF Q8_0 planes (int8 codes, one f16 d per 32; same number as the GEMV's FMT_Q8_0)
-enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2, FMT_Q8G = 4 };
+// FMT_Q4G / FMT_Q8G: GGUF Q4_0 / Q8_0 planes (codes, one f16 d per 32; the same numbers as the
+// GEMV's FMT_Q4_0 / FMT_Q8_0)
+enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2, FMT_Q4G = 3, FMT_Q8G = 4 };
 
 constexpr int kThreads = 256;
 constexpr int BK = 32;     // K elements per slice: one 64-byte f16 row per tile row
@@ -86,7 +87,7 @@ __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 3); }
 // Index, within an 8-element k-run, of the element the code extraction puts in f16 slot i.
 template <int FMT>
 __device__ __forceinline__ int perm_src(int i) {
-    if constexpr (FMT == FMT_INT4) return (i >> 1) + ((i & 1) << 2);
+    if constexpr (FMT == FMT_INT4 || FMT == FMT_Q4G) return (i >> 1) + ((i & 1) << 2);
     else if constexpr (FMT == FMT_INT8 || FMT == FMT_Q8G) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
     else return i;
 }
@@ -184,7 +185,7 @@ void prefill_qgemm_kernel(PfArgs a) {
     const int G = (K + a.group - 1) / a.group;     // INT4 groups / NF4 blocks per row
     const int ZW = (G + 7) / 8, GP = ZW * 8;
     rsrc_t rs = make_rsrc(a.codes, 0), rz = rs;  // empty ranges unless the format has metadata
-    if constexpr (FMT == FMT_INT4 || FMT == FMT_Q8G) {
+    if constexpr (FMT == FMT_INT4 || FMT == FMT_Q4G || FMT == FMT_Q8G) {
         rs = make_rsrc(static_cast<const uint16_t *>(a.scales) + static_cast<int64_t>(n0) * GP,
                        static_cast<uint32_t>(n_valid) * GP * 2);
     }
@@ -215,7 +216,14 @@ void prefill_qgemm_kernel(PfArgs a) {
                                                    rx, static_cast<uint32_t>(row * K + k0 + ch * 8) * 2, 0, 0));
         }
         const uint32_t wo = static_cast<uint32_t>(wr * w_row_bytes + (FMT == FMT_INT8 ? k0 : k0 / 2) + wb);
-        if constexpr (FMT == FMT_Q8G) {
+        if constexpr (FMT == FMT_Q4G) {
+            // the slice is one block; its 4-byte piece p (elements 8p..8p+7) sits at byte
+            // 16 p + 4 (block & 3) of the block's 64-byte chunk
+            const uint32_t cb = static_cast<uint32_t>(wr * w_row_bytes + (k0 >> 7) * 64 + 4 * ((k0 >> 5) & 3));
+#pragma unroll
+            for (int h = 0; h < kWBytesThread / 4; ++h)
+                r.w[h] = __builtin_amdgcn_raw_buffer_load_b32(rw, cb + 16 * (wb / 4 + h), 0, 0);
+        } else if constexpr (FMT == FMT_Q8G) {
             // the slice is one block; its 8-byte piece p (elements 8p..8p+7) sits at byte
             // 16 p + 8 (block & 1) of the block's 64-byte chunk
             const uint32_t cb = static_cast<uint32_t>(wr * w_row_bytes + (k0 >> 6) * 64 + 8 * ((k0 >> 5) & 1));
@@ -240,7 +248,7 @@ void prefill_qgemm_kernel(PfArgs a) {
         }
         // raw metadata words only: decoding them here would wait for the loads
         const int g = k0 / a.group;
-        if constexpr (FMT == FMT_INT4 || FMT == FMT_Q8G)
+        if constexpr (FMT == FMT_INT4 || FMT == FMT_Q4G || FMT == FMT_Q8G)
             r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<uint32_t>(wr * GP + (g & ~1)) * 2, 0, 0);
         if constexpr (FMT == FMT_INT4) {
             r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, static_cast<uint32_t>(wr * ZW + (g >> 3)) * 4, 0, 0);
@@ -270,11 +278,11 @@ void prefill_qgemm_kernel(PfArgs a) {
             *reinterpret_cast<uint4 *>(xplane + row * C::kRowBytes + swz(row, ch) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
         }
         // W: this thread's bytes cover chunks [c0, c0 + nch) of row wr
-        if constexpr (FMT == FMT_INT4) {
-            // one code word = 8 k = one 16-byte chunk of each plane
+        if constexpr (FMT == FMT_INT4 || FMT == FMT_Q4G) {
+            // one code word = 8 k = one 16-byte chunk of each plane (Q4_0: zero point 8)
             const int g = kt * BK / a.group;
             const uint32_t s2 = ((g & 1) ? (r.s >> 16) : (r.s & 0xFFFFu)) * 0x00010001u;
-            const uint32_t z = (r.z >> (4 * (g & 7))) & 15u;
+            const uint32_t z = FMT == FMT_Q4G ? 8u : (r.z >> (4 * (g & 7))) & 15u;
 #pragma unroll
             for (int t = 0; t < kWBytesThread / 4; ++t) {
                 const int ch = wb / 4 + t;
@@ -555,6 +563,7 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
     if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
     else if (fmt == FMT_NF4) launch_fmt<FMT_NF4>(a, st);
+    else if (fmt == FMT_Q4G) launch_fmt<FMT_Q4G>(a, st);
     else if (fmt == FMT_Q8G) launch_fmt<FMT_Q8G>(a, st);
     else launch_fmt<FMT_INT8>(a, st);
     return true;

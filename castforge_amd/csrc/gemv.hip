@@ -1229,8 +1229,8 @@ int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m,
             }
             return;
         }
-        // Q8_0 at M > 16: the prefill MFMA kernel reads the planes directly
-        if (fmt == FMT_Q8_0 && prefill_try(FMT_Q8_0, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st)) return;
+        // M > 16: the prefill MFMA kernel reads the planes directly
+        if (prefill_try(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st)) return;
         gemv_generic(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st);
     });
 }

@@ -475,12 +475,9 @@ def gguf_q4_0_to_int4g(p: GgufPacked) -> Int4Packed:
 
 
 def gemm_gguf(x: torch.Tensor, p: GgufPacked, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """y [M, n] = x [M, k] (bf16) times decode(W)^T over GGUF planes.  Q4_0 at M > 16 runs the
-    INT4g prefill MFMA kernel on a transient INT4g form of the planes (one pass over 0.56 B
-    per weight, small next to the GEMM)."""
+    """y [M, n] = x [M, k] (bf16) times decode(W)^T over GGUF planes (split-K GEMV up to
+    M = 16, the prefill MFMA kernel beyond)."""
     x = _check_x(x, p.k)
-    if x.shape[0] > 16 and p.ggml_type == ffi.GGML_Q4_0:
-        return gemm_w4a16(x, gguf_q4_0_to_int4g(p), out_dtype)
     y = torch.empty((x.shape[0], p.n), dtype=out_dtype, device=x.device)
     ffi.call("castforge_hip_gemv_gguf", p.ggml_type, _ptr(x), x.shape[0], p.n, p.k, _ptr(p.codes),
              _ptr(p.scales), _ptr(y), _out_dtype(out_dtype), _stream(x))

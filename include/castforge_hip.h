@@ -362,9 +362,9 @@ int32_t castforge_hip_dequantize_gguf(int32_t ggml_type, const void *codes, cons
  * dequant-GEMV of a GGUF weight: the reference decodes it to f32 (gguf.rs:513-550) and
  * evaluates the matmul (codegen/eval.rs:1465-1507).  x bf16 [m, k] 16-byte aligned; y f32 or
  * bf16.  M <= 16 runs the split-K MFMA kernel (one MFMA per block, scaled in f32 by its d),
- * each activation row as one problem of a batched launch; Q8_0 at M > 16 the prefill MFMA
- * kernel (exact hi / lo f16 planes of q * d, |q * d| < 65504); Q4_0 at M > 16 a generic
- * kernel (castforge_hip_gguf_q4_0_to_int4g + castforge_hip_gemv_w4a16 is the MFMA route). */
+ * each activation row as one problem of a batched launch; M > 16 the prefill MFMA kernel
+ * reading the planes directly (exact hi / lo f16 planes of the block values, which must lie
+ * within f16 range); shapes neither fits take a generic kernel. */
 int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m, int64_t n, int64_t k,
                                 const void *codes, const uint16_t *scales_f16, void *y, int32_t y_dtype,
                                 void *stream, char **out_error);

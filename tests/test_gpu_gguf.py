@@ -194,9 +194,10 @@ def test_gemv_matches_oracle(cuda, ty, m, n, k, out):
 
 
 @pytest.mark.parametrize("m,n,k", [(64, 96, 1024), (300, 256, 4096), (17, 48, 256)])
-def test_q4_0_prefill_through_int4g(cuda, m, n, k):
-    """Q4_0 at M > 16: the INT4g form of the planes dequantizes to the same values bit for bit,
-    and the prefill MFMA kernel over it matches the oracle's decode-then-matmul."""
+def test_q4_0_prefill_and_int4g_form(cuda, m, n, k):
+    """Q4_0 at M > 16: the prefill MFMA kernel reading the planes matches the oracle's
+    decode-then-matmul, and the INT4g form of the planes dequantizes to the same values bit
+    for bit."""
     raw = _blocks(Q4_0, n * k // 32, 700 + m)
     p = ops.gguf_repack(Q4_0, _dev_u8(raw, cuda), n, k)
     i4 = ops.gguf_q4_0_to_int4g(p)
