@@ -169,9 +169,9 @@ __device__ __forceinline__ rsrc_t make_rsrc_u(const void *base, uint32_t bytes) 
 }
 
 // Loads one unit issues: per row tile NB code loads, plus one scale and one zero-point load
-// (INT4) or one absmax load per chunk (NF4).
+// (INT4), one absmax load per chunk (NF4) or one scale load per chunk (GGUF Q4_0 / Q8_0).
 template <int FMT, int NB, int R>
-constexpr int kVmcntAfterUnit() { return vmcnt_imm(R * (NB + (FMT == 0 ? 2 : FMT == 2 ? NB : 0))); }
+constexpr int kVmcntAfterUnit() { return vmcnt_imm(R * (NB + (FMT == 0 ? 2 : (FMT == 2 || FMT == 3 || FMT == 4) ? NB : 0))); }
 
 template <int LW>
 __device__ __forceinline__ void load_words(rsrc_t r, uint32_t off, uint32_t *w) {
@@ -219,8 +219,11 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const int64_t grp = FMT == FMT_INT8 ? CK : P.group;  // INT8 has no groups (group 0)
     const uint32_t G = static_cast<uint32_t>((K + grp - 1) / grp);
     const uint32_t ZW = (G + 7) / 8, GP = ZW * 8;  // INT4 scale rows are padded to GP groups
-    const int gshift = __builtin_ctz(static_cast<uint32_t>(grp / CK));  // chunks per group = 2^gshift
+    const int gshift = is_gguf(FMT) ? 0 : __builtin_ctz(static_cast<uint32_t>(grp / CK));  // chunks per group = 2^gshift
     rsrc_t rs, rz;
+    if constexpr (is_gguf(FMT)) {
+        rs = make_rsrc(static_cast<const uint16_t *>(P.scales) + n0 * GP, static_cast<uint32_t>(rows_here) * GP * 2);
+    }
     if constexpr (FMT == FMT_INT4) {
         rs = make_rsrc(static_cast<const uint16_t *>(P.scales) + n0 * GP, static_cast<uint32_t>(rows_here) * GP * 2);
         rz = make_rsrc(P.zeros + n0 * ZW, static_cast<uint32_t>(rows_here) * ZW * 4);
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     for (int r = 0; r < R; ++r) {
         const uint32_t row = 16 * r + lr;
         code_off[r] = row * row_bytes + part * LW;
-        sc_off[r] = row * (FMT == FMT_INT4 ? GP : G);
+        sc_off[r] = row * ((FMT == FMT_INT4 || is_gguf(FMT)) ? GP : G);
         z_off[r] = row * ZW;
     }
 
@@ -243,7 +246,9 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     // zero points one word, instead of two scattered loads per chunk.
     struct Unit {
         uint32_t wq[NB][R][WPL];
-        uint32_t sv[R][NB];  // INT4: f16 scale pairs in [0, NB/2); NF4: f32 absmax bits per chunk
+        // INT4: f16 scale pairs in [0, NB/2); NF4: f32 absmax bits per chunk; GGUF: the chunk's
+        // block scales as f16 pairs (Q4_0: 2 words per chunk, Q8_0: 1)
+        uint32_t sv[R][FMT == FMT_Q4_0 ? 2 * NB : NB];
         uint32_t zv[R];      // INT4: the zero-point word of the unit's 8-group block
     };
     Unit ua, ub;
@@ -262,6 +267,15 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 load_words<LW>(rc, in ? code_off[r] + static_cast<uint32_t>(c) * (CK / CPB) : kOob, u.wq[j][r]);
+                if constexpr (FMT == FMT_Q4_0) {
+                    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                  rs, in ? (sc_off[r] + static_cast<uint32_t>(c) * 4u) * 2u : kOob, 0, 0));
+                    u.sv[r][2 * j] = v.x;
+                    u.sv[r][2 * j + 1] = v.y;
+                } else if constexpr (FMT == FMT_Q8_0) {
+                    u.sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(
+                        rs, in ? (sc_off[r] + static_cast<uint32_t>(c) * 2u) * 2u : kOob, 0, 0);
+                }
                 if constexpr (FMT == FMT_NF4)
                     u.sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(
                         rs, in ? (sc_off[r] + (static_cast<uint32_t>(c) >> gshift)) * 4 : kOob, 0, 0);
@@ -396,6 +410,33 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
                     const float sc = f16_to_f32(static_cast<uint16_t>(u.sv[r][j >> 1] >> (16 * (j & 1))));
                     if constexpr (ONE) acc[r][0] += pacc[r][0] * sc;
                     else acc[r] += pacc[r] * sc;
+                }
+            } else if constexpr (is_gguf(FMT)) {
+                // one MFMA per block (the four parts of a row hold elements 8p..8p+7 of each
+                // block of the chunk), scaled in f32 by the block's d
+                constexpr int BPC = gguf_bpc(FMT);
+                const _Float16 *xg = xs + xr * ((ce - cs) * CK) + (c - cs) * CK + 8 * part;
+#pragma unroll
+                for (int q = 0; q < BPC; ++q) {
+                    const half8_t aop = *reinterpret_cast<const half8_t *>(xg + 32 * q);
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        floatx4 pb = floatx4{0.f, 0.f, 0.f, 0.f};
+                        if constexpr (FMT == FMT_Q4_0) {
+                            uint32_t hb[4];
+                            int4_word_to_h(u.wq[j][r][q], as_h2(0xE408E408u), as_h2(0xD480D480u), i4k, hb);  // -1032, -72
+                            pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(hb[0], hb[1], hb[2], hb[3]), pb, 0, 0, 0);
+                        } else {
+                            uint32_t h0[2], h1[2];
+                            int8_word_to_h(u.wq[j][r][2 * q], h0);
+                            int8_word_to_h(u.wq[j][r][2 * q + 1], h1);
+                            pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]), pb, 0, 0, 0);
+                        }
+                        const uint32_t sw = FMT == FMT_Q4_0 ? u.sv[r][2 * j + (q >> 1)] : u.sv[r][j];
+                        const float d = f16_to_f32(static_cast<uint16_t>(sw >> (16 * (q & 1))));
+                        if constexpr (ONE) acc[r][0] += pb[0] * d;
+                        else acc[r] += pb * d;
+                    }
                 }
             } else if constexpr (FMT == FMT_NF4) {
                 floatx4 pacc[R];
@@ -965,11 +1006,8 @@ int64_t split_region(int fmt, int lw, Problem &p) {
 
 bool skinny_ok(int fmt, const Problem &p, int64_t m) {
     if (is_gguf(fmt)) {
-        // the GGUF planes have a kernel for M = 1 only, and only while a wave's LDS region fits
-        if (m != 1 || !CFH_GEMV_SPLIT || p.group != 32) return false;
-        Problem q = p;
+        if (m < 1 || m > 16 || p.group != 32) return false;
         if (p.k % chunk_k(fmt, 16) != 0 || p.k >= (int64_t{1} << 24)) return false;
-        if (split_region(fmt, 16, q) * kWaves > kLdsBytesSplit) return false;
         return aligned(p.x, 16) && aligned(p.codes, 16) && aligned(p.scales, 16);
     }
     if (m < 1 || m > 16) return false;
@@ -1004,7 +1042,7 @@ void launch_one(const Batch &b, int64_t tiles, int64_t lds, hipStream_t st) {
 template <int FMT, int R>
 void launch_lw(int lw, const Batch &b, int64_t tiles, int64_t lds, hipStream_t st) {
     if (lw == 16) launch_one<FMT, 16, R>(b, tiles, lds, st);
-    else if constexpr (FMT != FMT_INT8) {
+    else if constexpr (FMT != FMT_INT8 && !is_gguf(FMT)) {
         if (lw == 8) launch_one<FMT, 8, R>(b, tiles, lds, st);
         else launch_one<FMT, 4, R>(b, tiles, lds, st);
     }
@@ -1058,7 +1096,6 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
             return;
         }
     }
-    require(!is_gguf(fmt), "GGUF planes have no MFMA kernel for this shape");
     // 16-row tiles up to M = 4, 32 rows up to M = 8, 64 rows beyond (x is shared by more rows)
     const int R = m <= 4 ? CFH_GEMV_R_SMALL : m <= 8 ? 2 : 4;
     // longest K first: its workgroups run longest, so they start first
@@ -1087,6 +1124,14 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
         if (R == CFH_GEMV_R_SMALL) launch_lw<FMT_NF4, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
         else if (R == 2) launch_lw<FMT_NF4, 2>(lw, b, tiles, max_lds, st);
         else launch_lw<FMT_NF4, 4>(lw, b, tiles, max_lds, st);
+    } else if (fmt == FMT_Q4_0) {
+        if (R == CFH_GEMV_R_SMALL) launch_lw<FMT_Q4_0, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        else if (R == 2) launch_lw<FMT_Q4_0, 2>(lw, b, tiles, max_lds, st);
+        else launch_lw<FMT_Q4_0, 4>(lw, b, tiles, max_lds, st);
+    } else if (fmt == FMT_Q8_0) {
+        if (R == CFH_GEMV_R_SMALL) launch_lw<FMT_Q8_0, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
+        else if (R == 2) launch_lw<FMT_Q8_0, 2>(lw, b, tiles, max_lds, st);
+        else launch_lw<FMT_Q8_0, 4>(lw, b, tiles, max_lds, st);
     } else {
         if (R == CFH_GEMV_R_SMALL) launch_lw<FMT_INT8, CFH_GEMV_R_SMALL>(lw, b, tiles, max_lds, st);
         else if (R == 2) launch_lw<FMT_INT8, 2>(lw, b, tiles, max_lds, st);
@@ -1213,22 +1258,18 @@ int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m,
         hipStream_t st = static_cast<hipStream_t>(stream);
         const int yb = y_dtype == CFH_DTYPE_BF16;
         Problem p{x, codes, scales_f16, nullptr, y, n, k, 32, 1, 0, 0};
-        if (m <= 16 && skinny_ok(fmt, p, 1)) {
-            // each activation row is one M = 1 problem of the split-K kernel, up to 8 per launch;
-            // the rows re-read the same planes, which the MALL holds between them
+        if (m == 2 && skinny_ok(fmt, p, 1)) {
+            // two rows as two M = 1 problems of one split-K launch (measured faster than the
+            // skinny kernel at M = 2; the second row re-reads the planes from the MALL)
             const int esz = yb ? 2 : 4;
-            Problem ps[kMaxProblems];
-            for (int64_t r0 = 0; r0 < m; r0 += kMaxProblems) {
-                const int cnt = static_cast<int>(std::min<int64_t>(m - r0, kMaxProblems));
-                for (int i = 0; i < cnt; ++i) {
-                    ps[i] = p;
-                    ps[i].x = x + (r0 + i) * k;
-                    ps[i].y = static_cast<uint8_t *>(y) + (r0 + i) * n * esz;
-                }
-                launch_skinny(fmt, ps, cnt, 1, yb, st);
-            }
+            Problem ps[2] = {p, p};
+            ps[1].x = x + k;
+            ps[1].y = static_cast<uint8_t *>(y) + n * esz;
+            launch_skinny(fmt, ps, 2, 1, yb, st);
             return;
         }
+        // M <= 16: split-K kernel at M = 1, the skinny kernel (x of all rows staged once) beyond
+        if (gemv_try_skinny(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st)) return;
         // M > 16: the prefill MFMA kernel reads the planes directly
         if (prefill_try(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st)) return;
         gemv_generic(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st);

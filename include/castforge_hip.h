@@ -361,8 +361,9 @@ int32_t castforge_hip_dequantize_gguf(int32_t ggml_type, const void *codes, cons
  * (contraction along the blocked dimension, as GGUF producers store linear weights).  The
  * dequant-GEMV of a GGUF weight: the reference decodes it to f32 (gguf.rs:513-550) and
  * evaluates the matmul (codegen/eval.rs:1465-1507).  x bf16 [m, k] 16-byte aligned; y f32 or
- * bf16.  M <= 16 runs the split-K MFMA kernel (one MFMA per block, scaled in f32 by its d),
- * each activation row as one problem of a batched launch; M > 16 the prefill MFMA kernel
+ * bf16.  M = 1 and 2 run the split-K MFMA kernel (one MFMA per block, scaled in f32 by its d;
+ * M = 2 as two problems of one launch), M = 3..16 the skinny MFMA kernel (the same per-block
+ * MFMA, x of all rows staged once in LDS); M > 16 the prefill MFMA kernel
  * reading the planes directly (exact hi / lo f16 planes of the block values, which must lie
  * within f16 range); shapes neither fits take a generic kernel. */
 int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m, int64_t n, int64_t k,

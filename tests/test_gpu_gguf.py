@@ -177,7 +177,7 @@ def test_planes_reject_bad_shapes(cuda):
 
 # -------------------------------------------------------------------------------- GEMV ----
 @pytest.mark.parametrize("ty", [Q4_0, Q8_0])
-@pytest.mark.parametrize("m", [1, 3, 9, 17])
+@pytest.mark.parametrize("m", [1, 2, 3, 9, 16, 17])
 @pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (64, 11008), (4096, 4096)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
 def test_gemv_matches_oracle(cuda, ty, m, n, k, out):
