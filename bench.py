@@ -145,8 +145,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the quantized "
-              "GEMV/GEMM shards by output rows with no collective; see DESIGN.md). "
-              "Run with --gpus 1.", file=sys.stderr)
+              "GEMV/GEMM would shard by output rows, each GPU holding its rows' codes and "
+              "scales, with no collective at M = 1). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
