@@ -1277,10 +1277,11 @@ int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m,
 }
 
 int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_problem_t *problems, int32_t count,
-                                        int32_t y_dtype, void *stream, char **out_error) {
+                                        int64_t m, int32_t y_dtype, void *stream, char **out_error) {
     return guarded(out_error, [&] {
         require(ggml_type == CFH_GGML_Q4_0 || ggml_type == CFH_GGML_Q8_0,
                 "ggml_type must be CFH_GGML_Q4_0 or CFH_GGML_Q8_0");
+        require(m >= 1 && m <= 16, "batched GEMV requires 1 <= m <= 16");
         require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
         require(count == 0 || problems != nullptr, "problems must not be NULL");
         require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
@@ -1289,16 +1290,16 @@ int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_proble
         int used = 0;
         for (int i = 0; i < count; ++i) {
             const cfh_gguf_problem_t &q = problems[i];
-            common_checks(q.x, 1, q.n, q.k, q.codes, q.y, y_dtype);
+            common_checks(q.x, m, q.n, q.k, q.codes, q.y, y_dtype);
             if (q.n == 0) continue;
             require(q.k > 0 && q.scales_f16, "problem buffers must not be NULL");
             Problem p{q.x, q.codes, q.scales_f16, nullptr, q.y, q.n, q.k, 32, 1, 0, 0};
-            require(skinny_ok(fmt, p, 1),
-                    "batched GGUF GEMV needs k % 128 == 0 (Q4_0) or k % 64 == 0 (Q8_0), k below the "
-                    "split kernel's LDS bound and 16-byte aligned x / codes / scales");
+            require(skinny_ok(fmt, p, m),
+                    "batched GGUF GEMV needs k % 128 == 0 (Q4_0) or k % 64 == 0 (Q8_0), k below 2^24 "
+                    "and 16-byte aligned x / codes / scales");
             ps[used++] = p;
         }
-        if (used) launch_skinny(fmt, ps, used, 1, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
+        if (used) launch_skinny(fmt, ps, used, m, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
     });
 }
 

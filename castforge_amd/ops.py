@@ -485,19 +485,21 @@ def gemm_gguf(x: torch.Tensor, p: GgufPacked, out_dtype: torch.dtype = torch.bfl
 
 
 def gemv_gguf_batched(xs: list[torch.Tensor], ps: list[GgufPacked], ys: list[torch.Tensor]) -> None:
-    """One M = 1 launch for up to 8 GGUF matrices of one type; outputs preallocated."""
+    """One launch for up to 8 GGUF matrices of one type with the same M (1..16); outputs
+    preallocated."""
     if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
         raise ValueError("xs, ps, ys must have the same length <= 8")
     if not ps:
         return
     t = ps[0].ggml_type
+    m = xs[0].shape[0]
     arr = (ffi.GgufProblem * len(ps))()
     for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
         _check_x(x, p.k)
-        if p.ggml_type != t or x.shape[0] != 1 or y.shape != (1, p.n):
-            raise ValueError("problems must share the GGML type, with x [1, k] and y [1, n]")
+        if p.ggml_type != t or x.shape[0] != m or y.shape != (m, p.n):
+            raise ValueError("problems must share the GGML type and M, with x [M, k] and y [M, n]")
         arr[i] = ffi.GgufProblem(_ptr(x), _ptr(p.codes), _ptr(p.scales), _ptr(y), p.n, p.k)
-    ffi.call("castforge_hip_gemv_gguf_batched", t, arr, len(ps), _out_dtype(ys[0].dtype), _stream(xs[0]))
+    ffi.call("castforge_hip_gemv_gguf_batched", t, arr, len(ps), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
 
 
 # ------------------------------------------------------------- static W8A8 (calibrate) ----

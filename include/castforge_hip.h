@@ -303,7 +303,7 @@ int32_t castforge_hip_smoothquant(const float *w, int64_t n, float smooth_scale,
 /* GgmlType ids of the reference's GGUF reader / writer (gguf.rs:16-37). */
 enum { CFH_GGML_F32 = 0, CFH_GGML_F16 = 1, CFH_GGML_Q4_0 = 2, CFH_GGML_Q8_0 = 8, CFH_GGML_BF16 = 30 };
 
-/* One matrix of castforge_hip_gemv_gguf_batched: x bf16 [1, k], GGUF planes of W [n, k], y [1, n]. */
+/* One matrix of castforge_hip_gemv_gguf_batched: x bf16 [m, k], GGUF planes of W [n, k], y [m, n]. */
 typedef struct {
     const uint16_t *x;
     const void *codes;
@@ -369,9 +369,9 @@ int32_t castforge_hip_dequantize_gguf(int32_t ggml_type, const void *codes, cons
 int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m, int64_t n, int64_t k,
                                 const void *codes, const uint16_t *scales_f16, void *y, int32_t y_dtype,
                                 void *stream, char **out_error);
-/* Up to CFH_MAX_BATCH matrices of one type at M = 1 in one launch. */
+/* Up to CFH_MAX_BATCH matrices of one type with the same M (1..16) in one launch. */
 int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_problem_t *problems, int32_t count,
-                                        int32_t y_dtype, void *stream, char **out_error);
+                                        int64_t m, int32_t y_dtype, void *stream, char **out_error);
 
 /* *out = max |src[i]| over the non-NaN elements (0 for n == 0), written on the device: the
  * constant ranges of calibrate-quantize's calibrate_value_ranges (formats.rs:135-150). */

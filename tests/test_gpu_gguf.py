@@ -245,6 +245,21 @@ def test_gemv_batched_block_matches_single_and_torch(cuda, ty):
         assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"max err {err.max().item():.3e}"
 
 
+@pytest.mark.parametrize("m", [4, 16])
+def test_gemv_batched_block_m_gt_1(cuda, m):
+    """The seven block projections at M > 1 in one launch equal one call per matrix."""
+    ps, xs, ys = [], [], []
+    for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK):
+        raw = torch.randint(0, 256, (n * k // 32 * 18,), dtype=torch.uint8, device=cuda)
+        raw.view(-1, 18)[:, 0:2] = (torch.randn(n * k // 32, device=cuda) * 0.003).half().view(torch.uint8).view(-1, 2)
+        ps.append(ops.gguf_repack(Q4_0, raw, n, k))
+        xs.append(_x(900 + tid, m, k, cuda)[1])
+        ys.append(torch.empty((m, n), dtype=torch.float32, device=cuda))
+    ops.gemv_gguf_batched(xs, ps, ys)
+    for x, p, y in zip(xs, ps, ys):
+        assert torch.equal(ops.gemm_gguf(x, p, torch.float32), y)
+
+
 def test_gemv_batched_rejects_mixed_types(cuda):
     raw = _dev_u8(_blocks(Q4_0, 16, 2), cuda)
     p4 = ops.gguf_repack(Q4_0, raw, 4, 128)
