@@ -165,12 +165,14 @@ def main():
     def ev():
         return torch.cuda.Event(enable_timing=True)
 
-    def time_steps(fn, steps, warmup):
+    def time_steps(fn, steps, warmup, min_ms=0.0, replays=1, stream=None):
         """Milliseconds per step.  `warmup` eager calls of fn(i), then `steps` calls captured
         into one HIP graph (fn enqueues on torch's current stream, which is the capture stream
-        during capture), replayed once untimed (graph upload) and once between two events on
-        the capture stream.  The graph keeps Python/ctypes launch cost off the clock, so the
-        time is the GPU's: kernel durations plus the gaps between back-to-back launches."""
+        during capture), replayed once untimed (graph upload), then replayed at least
+        `replays` times and for at least `min_ms` in total, each replay between two events
+        on the capture stream; the median replay gives the time per step.  The graph keeps
+        Python/ctypes launch cost off the clock, so the time is the GPU's: kernel durations
+        plus the gaps between back-to-back launches."""
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
@@ -180,15 +182,22 @@ def main():
                 fn(i)
         g.replay()
         torch.cuda.synchronize()
-        s, e = ev(), ev()
-        s.record()
-        g.replay()
-        e.record()
-        e.synchronize()
+        times, total = [], 0.0
+        while len(times) < replays or total < min_ms:
+            s, e = ev(), ev()
+            s.record()
+            g.replay()
+            e.record()
+            e.synchronize()
+            t = s.elapsed_time(e)
+            times.append(t)
+            total += t
         torch.cuda.synchronize()
-        ms = s.elapsed_time(e) / steps
         del g
-        return ms
+        times.sort()
+        time_steps.last = {"replays": len(times), "timed_ms": round(total, 2),
+                           "min_us": round(times[0] / steps * 1e3, 2), "max_us": round(times[-1] / steps * 1e3, 2)}
+        return times[len(times) // 2] / steps
 
     # ---------------------------------------------------------------- block weights ----
     t0 = time.time()
@@ -211,23 +220,46 @@ def main():
             tot += n * k // 2 + n * ((g + 7) // 8 * 8) * 2 + n * ((g + 7) // 8) * 4 + 2 * m * k + 2 * m * n
         return tot
 
+    def planes_bytes():
+        """Compulsory bytes of one M = 1 step over GEMV planes: codes, one f16 scale and one u4
+        zero point per row and group, x and y (bf16)."""
+        return sum(n * k // 2 + n * (k // 128) * 2 + n * (k // 128) // 2 + 2 * k + 2 * n
+                   for (_, n, k) in synth.LLAMA7B_BLOCK)
+
     copies = [packed0] + [[ops.Int4Packed(p.codes.clone(), p.scales.clone(), p.zeros.clone(),
                                           p.n, p.k, p.group) for p in packed0]
                           for _ in range(args.copies - 1)]
+    # the GEMV planes of every copy, built once as a loader would
+    planes = [[ops.int4g_to_planes(p) for p in c] for c in copies]
+    torch.cuda.synchronize()
 
     def gemv_case(m):
         xs = [x_for(m, k, tid) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)]
         ys = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
         return lambda i: ops.gemv_w4a16_batched(xs, copies[i % len(copies)], ys)
 
+    def planes_case():
+        # a decoder's activations: q/k/v share one x, gate/up another
+        xk = {tid: x_for(1, k, tid) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)}
+        xs = [xk[0], xk[0], xk[0], xk[3], xk[4], xk[4], xk[6]]
+        ys = [torch.empty((1, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
+        return lambda i: ops.gemv_w4a16_planes_batched(xs, planes[i % len(planes)], ys)
+
     components = {}
-    ms_step = time_steps(gemv_case(1), args.steps, args.warmup)
-    bytes_m1 = w4_bytes(1)
+    ms_step = time_steps(planes_case(), args.steps, args.warmup, min_ms=50.0, replays=5)
+    timing = dict(time_steps.last)
+    bytes_m1 = planes_bytes()
     value = bytes_m1 / (ms_step * 1e-3) / 1e9
     # one step is one launch, so the average launch duration over the timed region (kernel
     # plus the inter-launch gap) is ms_step and roofline.achieved equals value
     achieved = value
-    log(f"[bench] W4A16 GEMV M=1: {ms_step * 1e3:.2f} us/step (one launch), {value:.0f} GB/s")
+    log(f"[bench] W4A16 GEMV M=1 (planes): {ms_step * 1e3:.2f} us/step (one launch), {value:.0f} GB/s; "
+        f"median of {timing['replays']} replays ({timing['timed_ms']} ms), "
+        f"{timing['min_us']}..{timing['max_us']} us")
+    st = time_steps(gemv_case(1), args.steps, 5, min_ms=20.0, replays=3)
+    components["w4a16_gemv_m1_canonical_GBps"] = round(w4_bytes(1) / (st * 1e-3) / 1e9, 1)
+    log(f"[bench] W4A16 GEMV M=1 (canonical layout): {st * 1e3:.2f} us/step, "
+        f"{components['w4a16_gemv_m1_canonical_GBps']} GB/s")
 
     if args.copy_calibration:
         # a copy of known size: 2^28 f32 read + 2^28 f32 written per launch
@@ -389,15 +421,23 @@ def main():
                 O.gemm_w4a16(x, c, s, z, n, k, 128)
             t_cpu += time.perf_counter() - t1
             passes += 1
-        cpu = {"value": round(bytes_m1 * passes / t_cpu / 1e9, 3), "unit": "GB/s", "cores": 1,
-               "kind": "port",
+        cpu_model = "unknown"
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+        cpu = {"value": round(w4_bytes(1) * passes / t_cpu / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "port", "cpu_model": cpu_model, "host_cpus": os.cpu_count(),
                "sample": f"{passes} pass(es) of the full block W4A16 GEMV at M=1 with the oracle's "
                          f"evaluator semantics (dequantize to f32, then the m,n,k f32 loop of "
                          f"eval.rs:1465-1507), single thread, {t_cpu:.1f} s"}
         log(f"[bench] cpu baseline {cpu['value']} GB/s over {passes} passes ({t_cpu:.1f}s)")
 
     traffic = None
-    tfile = ROOT / "profiles" / "traffic_w4a16_gemv_m1.json"
+    tfile = ROOT / "profiles" / "traffic_w4a16_planes_gemv_m1.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
 
@@ -416,11 +456,12 @@ def main():
         "data": "synthetic (N(0,0.02) weights, bf16 N(0,1) activations with 1% x20 channels)",
         "config": {"workload": "llama7b_block_int4g128_w4a16_gemv_m1", "m": 1, "group": 128,
                    "matrices": 7, "rotating_copies": len(copies),
+                   "layout": "GEMV planes (built once at load)", "x_shared": "q/k/v and gate/up",
                    "value_is": "W4A16 GEMV GB/s at M=1 (algorithmic bytes / whole-job time per step)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "skinny_m1_split_kernel<FMT_INT4, 16>", "bytes_per_launch": bytes_m1,
-                     "us_per_launch": round(ms_step * 1e3, 2)},
+                     "kernel": "planes_m1_kernel<16, 3>", "bytes_per_launch": bytes_m1,
+                     "us_per_launch": round(ms_step * 1e3, 2), "timing": timing},
         "cpu_baseline": cpu,
         "components": components,
     }

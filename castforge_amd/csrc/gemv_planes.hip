@@ -1,0 +1,564 @@
+// W4A16 decode GEMV (M = 1) over INT4 g128 weights in the GEMV planes layout, gfx950.
+//
+// Replaces the evaluation of `castforge.fused_qmatmul` at decode (eval.rs:1145-1179 with
+// eval_matmul_2d, eval.rs:1465-1507; packed_rhs [N, K] weights, fold.rs:549-554) for the
+// asymmetric INT4 group-128 format: y[n] = sum_k x[k] * (q[n, k] - z[n, g]) * s[n, g].
+//
+// GEMV planes.  The canonical INT4g arrays (codes u32 [N, K/8], f16 scales [N, GP], u4 zero
+// points [N, ceil(G/8)]) are rewritten once, at load time, so that one wave-wide 16-byte load
+// reads one contiguous kilobyte: the 64-byte group slice of 16 consecutive rows.
+//   codes : T x G chunks of 1024 B (T = ceil(N/16) row tiles, G = K/128 groups); chunk (t, g)
+//           holds, at byte 16 * (16 p + r), canonical words 16 g + 4 p .. 16 g + 4 p + 3 of
+//           row 16 t + r (p = 0..3: the four 32-code parts of the group);
+//   scales: f16 [T][G][16], the scale of row 16 t + r and group g at [t][g][r];
+//   zeros : u8 [T][G][8], byte j = zero point of row 16 t + 2 j (low nibble) and 2 j + 1.
+// Rows past N are zero.  castforge_hip_int4g_from_planes restores the canonical arrays bit for
+// bit.
+//
+// Kernel.  One workgroup of 16 waves per CU (its LDS request keeps a second one off the CU)
+// runs for the whole launch: launch overhead and x staging are paid once per CU instead of
+// once per 16-row tile.
+//   * Work split: each problem gets a number of workgroups in proportion to its code bytes, and
+//     spreads its rows over them in units of 8 rows, so every CU streams about the same number
+//     of bytes of one matrix.  A workgroup's chunk sequence is, tile after tile, each tile's G
+//     chunks; wave i processes positions i, i + 16, i + 32, ... (balanced to one chunk), with
+//     a D-deep ring of loads that runs across tile boundaries.
+//   * x (bf16) is copied into LDS once and converted to f16 in the order the nibble decode
+//     produces, with a per-chunk power of two that brings the chunk's largest |x| into
+//     [2^14, 2^15): every finite bf16 x is then exact in f16 (down to 2^-38 of the chunk's
+//     largest value), and the scale is undone on the chunk's f32 partial.
+//   * Decode: (w & 0x000F000F) | 0x64006400 is the f16 pair (1024 + q, 1024 + q'), the 0x00F0
+//     nibbles give 1024 + 16 q; one packed f16 add of -(1024 + z) (or fma by 1/16 and add of
+//     -(64 + z)) leaves the exact integers q - z, so every product x (q - z) is exact and the
+//     MFMA's f32 sums carry the only rounding, as the reference's f32 loop does.
+//   * Each wave keeps one f32 partial per row of its current tile (lanes 0..15 of the MFMA
+//     result) and stores it into its own LDS slot of that tile when it moves to another tile;
+//     no barrier inside the loop.  After the loop one barrier, then the workgroup sums each
+//     row's partials in wave order (the same bits on every run) and stores its rows.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "../../include/castforge_hip.h"
+#include "cfh_common.hpp"
+
+namespace cfh {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+constexpr int kGroup = 128;
+constexpr uint32_t kOob = 0x80000000u;  // past every descriptor's range: reads 0, no traffic
+constexpr int kMaxP = CFH_MAX_BATCH;
+
+#ifndef CFH_PLANES_WAVES
+#define CFH_PLANES_WAVES 16
+#endif
+#ifndef CFH_PLANES_DEPTH
+#define CFH_PLANES_DEPTH 3
+#endif
+constexpr int kWaves = CFH_PLANES_WAVES;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kDepth = CFH_PLANES_DEPTH;
+// workgroups per CU (their LDS request keeps any more off a CU) and the cache policy of the
+// streamed loads (2 = non-temporal: each byte is read once)
+#ifndef CFH_PLANES_WG_PER_CU
+#define CFH_PLANES_WG_PER_CU 1
+#endif
+#ifndef CFH_PLANES_CPOL
+#define CFH_PLANES_CPOL 2
+#endif
+constexpr int kWgPerCu = CFH_PLANES_WG_PER_CU;
+constexpr int kLdsMax = 160 * 1024;
+constexpr int kLdsFloor = kLdsMax / (kWgPerCu + 1) + 2048;
+
+struct PProblem {
+    const uint8_t *codes;
+    const uint16_t *scales;
+    const uint8_t *zeros;
+    const uint16_t *x;  // bf16 [K]
+    void *y;
+    int32_t n, G;       // rows, groups (K / 128)
+    int32_t units;      // ceil(n / 8)
+    int32_t wg0, wgs;   // this problem's workgroups [wg0, wg0 + wgs)
+    int32_t pad;
+};
+
+struct PBatch {
+    PProblem p[kMaxP];
+    int32_t count, y_bf16;
+};
+
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+    uint32_t v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "i"(c));
+    return v;
+}
+
+__device__ __forceinline__ half8_t pack8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(half8_t, make_uint4(a, b, c, d));
+}
+
+// Workgroup barrier for LDS data: this wave's LDS operations done (lgkmcnt(0)) and at most VM
+// vector-memory loads still in flight, then s_barrier.  Unlike __syncthreads() it does not
+// wait for the loads in flight (its release fence would); the single-thread fences only keep
+// the compiler from moving memory accesses across it.
+template <int VM>
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(VM) & ~(15 << 8));
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+struct Stage {
+    uint32_t w[4];
+    uint32_t sc, zb;
+};
+
+// LDS: [x as f16, G * 256 B][per chunk 2^sh, G * 4 B (16-byte padded)][partials: tiles x NW x 16 f32]
+template <int NW, int D>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW * kWgPerCu / 4)))
+void planes_m1_kernel(PBatch b) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = uni(tid >> 6);
+    const int w = blockIdx.x;
+    const int r16 = lane & 15, part = lane >> 4;
+
+    // this workgroup's problem and rows [rlo, rhi): units of 8 rows spread over the problem's
+    // workgroups (host-checked: wgs * units < 2^31)
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxP; ++i)
+        if (i < b.count && w >= b.p[i].wg0) pi = i;
+    const PProblem &P = b.p[pi];
+    const int G = P.G, local = w - P.wg0;
+    const int u0 = static_cast<int>(static_cast<uint32_t>(local * P.units) / static_cast<uint32_t>(P.wgs));
+    const int u1 = static_cast<int>(static_cast<uint32_t>((local + 1) * P.units) / static_cast<uint32_t>(P.wgs));
+    const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
+    const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
+    const int ntiles = t1 - t0, npos = ntiles * G;
+    const uint32_t xbytes = static_cast<uint32_t>(G) * (kGroup * 2);
+    const uint32_t soff = xbytes, aoff = xbytes + ((static_cast<uint32_t>(G) * 4 + 15) & ~15u);
+    float *const accs = reinterpret_cast<float *>(lds + aoff);
+
+    // partials to zero, before any copy into LDS is in flight (an LDS write after an LDS-bound
+    // copy is made to wait for every load in flight)
+    for (int i = tid; i < ntiles * NW * 16; i += 64 * NW) accs[i] = 0.0f;
+
+    // x (bf16) straight into LDS, 1 KB per wave-wide copy
+    for (int blk = wave; blk * 1024u < xbytes; blk += NW) {
+        const uint32_t e = blk * 1024u + lane * 16u;
+        if (e < xbytes)
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void *>(P.x + (e >> 1)),
+                reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds) + blk * 1024),
+                16, 0, 0);
+    }
+
+    // the first D positions of this wave: positions wave, wave + NW, ... of the sequence of
+    // the workgroup's tiles (t0 + t) and their chunks g
+    const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
+    const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
+    const rsrc_t rscale = make_rsrc(P.scales, chunks * 32u);
+    const rsrc_t rzero = make_rsrc(P.zeros, chunks * 8u);
+    int lt = 0, lg = wave;  // load cursor (tile relative to t0, chunk)
+    while (lg >= G) {
+        lg -= G;
+        ++lt;
+    }
+    int pt = lt, pg = lg;  // process cursor
+    // per-lane offsets within a chunk, pushed out of range (OR kOob) for rows outside
+    // [rlo, rhi) and for positions past the workgroup's tiles: recomputed when the tile changes.
+    // Every lane needs its row's zero point (its codes are decoded as exact q - z); the scale
+    // multiplies the MFMA result, which lanes 0..15 hold.
+    uint32_t vcode, vscale, vzero;
+    auto lane_offsets = [&]() __attribute__((always_inline)) {
+        const int row = (t0 + lt) * 16 + r16;
+        const bool ok = lt < ntiles && row >= rlo && row < rhi;
+        const uint32_t m = ok ? 0u : kOob;
+        vcode = (static_cast<uint32_t>(lane) * 16u) | m;
+        vscale = (static_cast<uint32_t>(r16) * 2u) | (lane < 16 ? m : kOob);
+        vzero = static_cast<uint32_t>(r16 >> 1) | m;
+    };
+    lane_offsets();
+    auto load = [&](Stage &st) __attribute__((always_inline)) {
+        const uint32_t chunk = static_cast<uint32_t>((t0 + lt) * G + lg);
+        const uint4 v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, vcode + chunk * 1024u, 0, CFH_PLANES_CPOL));
+        st.w[0] = v.x;
+        st.w[1] = v.y;
+        st.w[2] = v.z;
+        st.w[3] = v.w;
+        st.sc = __builtin_amdgcn_raw_buffer_load_b16(rscale, vscale + chunk * 32u, 0, 0);
+        st.zb = __builtin_amdgcn_raw_buffer_load_b8(rzero, vzero + chunk * 8u, 0, 0);
+        lg += NW;
+        if (lg >= G) {
+            do {
+                lg -= G;
+                ++lt;
+            } while (lg >= G);
+            lane_offsets();
+        }
+    };
+    Stage st[D];
+    static_for<D>([&](auto i) __attribute__((always_inline)) {
+        load(st[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    // this wave's copies of x have landed (the D positions issued after them may still be in
+    // flight) and its LDS writes are done
+    lds_barrier<3 * D>();
+
+    // x to f16 in the decode's order: per 8 values the pairs (0, 4), (1, 5), (2, 6), (3, 7) of
+    // one code word.  Eight lanes (16 values each) hold one chunk of 128 values: they agree on
+    // the power of two 2^-sh that brings its largest |x| into [2^14, 2^15) (every finite bf16
+    // is then exact in f16 down to 2^-38 of that value); 2^sh is kept per chunk.
+    {
+        constexpr int kPerm[16] = {0, 4, 1, 5, 2, 6, 3, 7, 8, 12, 9, 13, 10, 14, 11, 15};
+        const int total = G * 8;
+        for (int base = 0; base < total; base += 64 * NW) {  // uniform trip count
+            const int i = base + tid;
+            const bool act = i < total;
+            const int j = act ? i : 0;
+            uint16_t *px = reinterpret_cast<uint16_t *>(lds) + j * 16;
+            const uint4 r0 = *reinterpret_cast<const uint4 *>(px);
+            const uint4 r1 = *reinterpret_cast<const uint4 *>(px + 8);
+            const uint32_t wv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+            uint32_t emax = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                emax = max(emax, (wv[q] >> 7) & 0xFFu);
+                emax = max(emax, (wv[q] >> 23) & 0xFFu);
+            }
+            {  // over the chunk's 8 lanes (DPP: xor 1, xor 2, half-row mirror)
+                int e = static_cast<int>(emax);
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0xB1, 0xF, 0xF, false));
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x4E, 0xF, 0xF, false));
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x141, 0xF, 0xF, false));
+                emax = static_cast<uint32_t>(e);
+            }
+            // largest |x| < 2^(emax - 126): scale by 2^-sh so that it lands in [2^14, 2^15)
+            int sh = static_cast<int>(emax) - 127 - 14;
+            sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
+            const float pre = __uint_as_float(static_cast<uint32_t>(127 - sh) << 23);
+            const float post = __uint_as_float(static_cast<uint32_t>(127 + sh) << 23);
+            uint32_t o[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int s0 = kPerm[2 * q], s1 = kPerm[2 * q + 1];
+                const float f0 = bf16_to_f32(static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)))) * pre;
+                const float f1 = bf16_to_f32(static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)))) * pre;
+                o[q] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f0))) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f1))) << 16);
+            }
+            if (act) {
+                *reinterpret_cast<uint4 *>(px) = make_uint4(o[0], o[1], o[2], o[3]);
+                *reinterpret_cast<uint4 *>(px + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+                if ((i & 7) == 0) reinterpret_cast<float *>(lds + soff)[j >> 3] = post;
+            }
+        }
+    }
+    lds_barrier<63>();
+
+    const uint32_t LO = vgpr_const(0x000F000Fu), HI = vgpr_const(0x00F000F0u), MG = vgpr_const(0x64006400u);
+    float acc = 0.0f;
+    const int steps = npos > wave ? (npos - wave + NW - 1) / NW : 0;
+    // the oldest stage is consumed, then refilled with the position D steps ahead (keeping
+    // about 48 KB in flight per CU: deeper rings measured slower); every step of the loop runs
+    // (steps past the wave's last position read zero codes and add nothing), so the number of
+    // loads in flight is the same on every path
+    for (int k = 0; k < steps; k += D) {
+        static_for<D>([&](auto ii) __attribute__((always_inline)) {
+            constexpr int i = decltype(ii)::value;
+            const bool live = pt < ntiles;
+            const Stage &s = st[i];
+            const int g = live ? pg : 0;  // a step past the end reads chunk 0 (in range)
+            const uint8_t *xa = lds + g * (kGroup * 2) + part * 64;
+            const half8_t a0 = *reinterpret_cast<const half8_t *>(xa);
+            const half8_t a1 = *reinterpret_cast<const half8_t *>(xa + 16);
+            const half8_t a2 = *reinterpret_cast<const half8_t *>(xa + 32);
+            const half8_t a3 = *reinterpret_cast<const half8_t *>(xa + 48);
+            const float post = reinterpret_cast<const float *>(lds + soff)[g];
+            const uint32_t w0 = s.w[0], w1 = s.w[1], w2 = s.w[2], w3 = s.w[3];
+            const uint32_t w08 = w0 >> 8, w18 = w1 >> 8, w28 = w2 >> 8, w38 = w3 >> 8;
+            const uint32_t zi = (s.zb >> (4 * (r16 & 1))) & 15u;
+            const float sc = f16_to_f32(static_cast<uint16_t>(s.sc));
+            float part_sum;
+            {
+                // (1024 + q) - (1024 + z) and (1024 + 16 q) / 16 - (64 + z): exact small integers
+                const half2_t zc1024 = as_h2((0xE400u + zi) * 0x00010001u);
+                const half2_t zc64 = as_h2((0xD400u + (zi << 4)) * 0x00010001u);
+                const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+                auto dec = [&](uint32_t ww, uint32_t w8) __attribute__((always_inline)) {
+                    return pack8(as_u(as_h2((ww & LO) | MG) + zc1024), as_u(as_h2((ww & HI) | MG) * sixteenth + zc64),
+                                 as_u(as_h2((w8 & LO) | MG) + zc1024), as_u(as_h2((w8 & HI) | MG) * sixteenth + zc64));
+                };
+                // two accumulation chains halve the MFMA dependency latency
+                floatx4 pa = floatx4{0.f, 0.f, 0.f, 0.f}, pb = pa;
+                pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, dec(w0, w08), pa, 0, 0, 0);
+                pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, dec(w1, w18), pb, 0, 0, 0);
+                pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, dec(w2, w28), pa, 0, 0, 0);
+                pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, dec(w3, w38), pb, 0, 0, 0);
+                // a separate multiply and add (no contraction): chunk results that cancel
+                // exactly sum to exactly zero
+                part_sum = __fmul_rn(pa[0] + pb[0], sc * post);
+            }
+            acc = __fadd_rn(acc, live ? part_sum : 0.0f);
+            // next position; a wave's positions in one tile are consecutive steps, so one store
+            // of its partials per tile
+            const int tile = pt;
+            pg += NW;
+            while (pg >= G) {
+                pg -= G;
+                ++pt;
+            }
+            if (live && pt != tile) {
+                if (lane < 16) accs[(tile * NW + wave) * 16 + lane] = acc;
+                acc = 0.0f;
+            }
+            load(st[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    lds_barrier<63>();  // every wave's partials are in LDS
+
+    // rows of this workgroup: the waves' partials in wave order (the same bits on every run)
+    for (int i = tid; i < ntiles * 16; i += 64 * NW) {
+        const int row = (t0 + (i >> 4)) * 16 + (i & 15);
+        if (row >= rlo && row < rhi) {
+            const float *pa = accs + (i >> 4) * NW * 16 + (i & 15);
+            float v = 0.0f;
+#pragma unroll
+            for (int q = 0; q < NW; ++q) v += pa[q * 16];
+            if (b.y_bf16) static_cast<uint16_t *>(P.y)[row] = f32_to_bf16_rne(v);
+            else static_cast<float *>(P.y)[row] = v;
+        }
+    }
+}
+
+// ---- canonical <-> planes ------------------------------------------------------------------
+// One thread per 16-byte unit of the codes planes / per (tile, group, row) of the metadata.
+__global__ void to_planes_kernel(const uint32_t *codes, const uint16_t *scales, const uint32_t *zeros, int64_t n,
+                                 int64_t k, uint8_t *pc, uint16_t *ps, uint8_t *pz) {
+    const int64_t G = k / kGroup, GP = (G + 7) / 8 * 8, ZW = (G + 7) / 8, T = (n + 15) / 16;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (u >= T * G * 64) return;
+    const int64_t chunk = u >> 6, l = u & 63;
+    const int64_t t = chunk / G, g = chunk % G, p = l >> 4, r = l & 15, row = t * 16 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < n) v = *reinterpret_cast<const uint4 *>(codes + row * (k / 8) + 16 * g + 4 * p);
+    *reinterpret_cast<uint4 *>(pc + u * 16) = v;
+    if (p == 0) {
+        ps[chunk * 16 + r] = row < n ? scales[row * GP + g] : 0;
+        if ((r & 1) == 0) {
+            uint32_t z0 = row < n ? (zeros[row * ZW + g / 8] >> (4 * (g & 7))) & 15u : 0u;
+            uint32_t z1 = row + 1 < n ? (zeros[(row + 1) * ZW + g / 8] >> (4 * (g & 7))) & 15u : 0u;
+            pz[chunk * 8 + (r >> 1)] = static_cast<uint8_t>(z0 | (z1 << 4));
+        }
+    }
+}
+
+// One thread per 16-byte unit of the canonical codes; the thread holding a row's first unit
+// of a group-of-8 also writes that row's scale slots (pad slots 0) and zero word.
+__global__ void from_planes_kernel(const uint8_t *pc, const uint16_t *ps, const uint8_t *pz, int64_t n, int64_t k,
+                                   uint32_t *codes, uint16_t *scales, uint32_t *zeros) {
+    const int64_t G = k / kGroup, GP = (G + 7) / 8 * 8, ZW = (G + 7) / 8;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // over n * (k / 32)
+    const int64_t units = k / 32;
+    if (u >= n * units) return;
+    const int64_t row = u / units, c = u % units, g = c / 4, p = c % 4, t = row / 16, r = row % 16;
+    const int64_t chunk = t * G + g;
+    *reinterpret_cast<uint4 *>(codes + row * (k / 8) + 4 * c) =
+        *reinterpret_cast<const uint4 *>(pc + (chunk * 64 + p * 16 + r) * 16);
+    if (p == 0 && (g & 7) == 0) {
+        uint32_t zw = 0;
+        for (int64_t j = 0; j < 8; ++j) {
+            const int64_t gg = g + j;
+            uint16_t sv = 0;
+            if (gg < G) {
+                const int64_t ch = t * G + gg;
+                sv = ps[ch * 16 + r];
+                zw |= ((static_cast<uint32_t>(pz[ch * 8 + (r >> 1)]) >> (4 * (r & 1))) & 15u) << (4 * j);
+            }
+            scales[row * GP + gg] = sv;
+        }
+        zeros[row * ZW + g / 8] = zw;
+    }
+}
+
+// ---- host ----------------------------------------------------------------------------------
+int cu_count() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    cache[dev] = cus;
+    return cus;
+}
+
+// Workgroups per problem in proportion to its code bytes (largest remainders; at least one per
+// problem, at most one per 8-row unit): every CU then streams about the same number of bytes.
+std::vector<int> workgroups_per_problem(const std::vector<int64_t> &bytes, const std::vector<int64_t> &units,
+                                        int W) {
+    const size_t n = bytes.size();
+    std::vector<int> wgs(n, 1);
+    int64_t total = 0;
+    for (int64_t v : bytes) total += v;
+    int used = 0;
+    std::vector<std::pair<double, size_t>> rem;
+    for (size_t i = 0; i < n; ++i) {
+        const double share = static_cast<double>(W) * static_cast<double>(bytes[i]) / static_cast<double>(total);
+        wgs[i] = std::max(1, static_cast<int>(share));
+        wgs[i] = static_cast<int>(std::min<int64_t>(wgs[i], units[i]));
+        used += wgs[i];
+        rem.push_back({share - static_cast<double>(wgs[i]), i});
+    }
+    std::sort(rem.begin(), rem.end(), [](const auto &a, const auto &c) { return a.first > c.first; });
+    for (size_t j = 0; used < W && j < rem.size(); ++j) {
+        const size_t i = rem[j].second;
+        if (wgs[i] < units[i]) {
+            ++wgs[i];
+            ++used;
+        }
+    }
+    return wgs;
+}
+
+void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
+                    hipStream_t st) {
+    require(count >= 1 && count <= kMaxP, "count must be in 1..8");
+    require(problems != nullptr, "problems must not be NULL");
+    require(m == 1, "the GEMV planes kernel takes M = 1");
+    require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+    const int W = cu_count() * kWgPerCu;
+    PBatch b{};
+    std::vector<int64_t> bytes, units;
+    for (int i = 0; i < count; ++i) {
+        const cfh_w4a16_problem_t &q = problems[i];
+        require(q.group == kGroup, "GEMV planes hold INT4 groups of 128");
+        require(q.n >= 1 && q.k >= kGroup && q.k % kGroup == 0, "GEMV planes need n >= 1 and k % 128 == 0");
+        require(q.x && q.codes && q.scales_f16 && q.zeros && q.y, "x, planes and y must not be NULL");
+        require(aligned(q.x, 16) && aligned(q.codes, 16) && aligned(q.scales_f16, 4) && aligned(q.y, 4),
+                "x and codes planes must be 16-byte aligned, scales and y 4-byte aligned");
+        const int64_t T = (q.n + 15) / 16, G = q.k / kGroup;
+        require(T * G * 1024 < (int64_t(1) << 31), "GEMV planes of one matrix must stay below 2 GiB");
+        bytes.push_back(T * G * 1024);
+        units.push_back((q.n + 7) / 8);
+    }
+    const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+    int64_t lds_max = 0, grid = 0;
+    for (int i = 0; i < count; ++i) {
+        const cfh_w4a16_problem_t &q = problems[i];
+        PProblem &P = b.p[i];
+        P.codes = reinterpret_cast<const uint8_t *>(q.codes);
+        P.scales = q.scales_f16;
+        P.zeros = reinterpret_cast<const uint8_t *>(q.zeros);
+        P.x = q.x;
+        P.y = q.y;
+        P.n = static_cast<int32_t>(q.n);
+        P.G = static_cast<int32_t>(q.k / kGroup);
+        P.units = static_cast<int32_t>(units[static_cast<size_t>(i)]);
+        P.wg0 = static_cast<int32_t>(grid);
+        P.wgs = wgs[static_cast<size_t>(i)];
+        require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
+        grid += P.wgs;
+        // a workgroup's units span at most ceil(units / wgs) / 2 + 2 tiles
+        const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
+        lds_max = std::max<int64_t>(lds_max, static_cast<int64_t>(P.G) * 256 + (P.G * 4 + 15) / 16 * 16 + tiles * kWaves * 64);
+    }
+    b.count = count;
+    b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
+    require(lds_max <= kLdsMax / kWgPerCu, "a problem of the batch exceeds the GEMV planes kernel's LDS (k too large or too "
+                                "many rows per workgroup)");
+    const int64_t req = std::max<int64_t>(lds_max, kLdsFloor);
+    static bool attr_set = false;
+    if (!attr_set) {
+        check_hip(hipFuncSetAttribute(
+                      reinterpret_cast<const void *>(&planes_m1_kernel<kWaves, kDepth>),
+                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
+                  "hipFuncSetAttribute");
+        attr_set = true;
+    }
+    planes_m1_kernel<kWaves, kDepth>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), static_cast<size_t>(req), st>>>(b);
+    check_launch("planes_m1_kernel");
+}
+
+void planes_checks(const void *codes, const void *scales, const void *zeros, int64_t rows, int64_t k,
+                   int64_t group, const void *pc, const void *ps, const void *pz) {
+    require(group == kGroup, "GEMV planes hold INT4 groups of 128");
+    require(rows >= 0 && k >= 0 && k % kGroup == 0, "rows >= 0 and k % 128 == 0 are required");
+    if (rows > 0 && k > 0) {
+        require(codes && scales && zeros && pc && ps && pz, "buffers must not be NULL");
+        require(aligned(codes, 16) && aligned(pc, 16), "codes and codes planes must be 16-byte aligned");
+        require(aligned(scales, 2) && aligned(ps, 2) && aligned(zeros, 4), "scales and zeros must be aligned");
+        require(((rows + 15) / 16) * (k / kGroup) * 1024 < (int64_t(1) << 31), "planes must stay below 2 GiB");
+    }
+}
+
+}  // namespace
+}  // namespace cfh
+
+using namespace cfh;
+
+extern "C" {
+
+int32_t castforge_hip_int4g_to_planes(const uint32_t *codes, const uint16_t *scales_f16, const uint32_t *zeros,
+                                      int64_t rows, int64_t k, int64_t group, void *planes_codes,
+                                      uint16_t *planes_scales, uint8_t *planes_zeros, void *stream,
+                                      char **out_error) {
+    return guarded(out_error, [&] {
+        planes_checks(codes, scales_f16, zeros, rows, k, group, planes_codes, planes_scales, planes_zeros);
+        const int64_t units = ((rows + 15) / 16) * (k / kGroup) * 64;
+        if (units == 0) return;
+        to_planes_kernel<<<dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream)>>>(codes, scales_f16, zeros, rows, k,
+                                                               static_cast<uint8_t *>(planes_codes), planes_scales,
+                                                               planes_zeros);
+        check_launch("to_planes_kernel");
+    });
+}
+
+int32_t castforge_hip_int4g_from_planes(const void *planes_codes, const uint16_t *planes_scales,
+                                        const uint8_t *planes_zeros, int64_t rows, int64_t k, int64_t group,
+                                        uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros, void *stream,
+                                        char **out_error) {
+    return guarded(out_error, [&] {
+        planes_checks(codes, scales_f16, zeros, rows, k, group, planes_codes, planes_scales, planes_zeros);
+        const int64_t units = rows * (k / 32);
+        if (units == 0) return;
+        from_planes_kernel<<<dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0,
+                             static_cast<hipStream_t>(stream)>>>(static_cast<const uint8_t *>(planes_codes),
+                                                                 planes_scales, planes_zeros, rows, k, codes,
+                                                                 scales_f16, zeros);
+        check_launch("from_planes_kernel");
+    });
+}
+
+int32_t castforge_hip_gemv_w4a16_planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m,
+                                                int32_t y_dtype, void *stream, char **out_error) {
+    return guarded(out_error, [&] { planes_batched(problems, count, m, y_dtype, static_cast<hipStream_t>(stream)); });
+}
+
+}  // extern "C"

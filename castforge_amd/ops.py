@@ -225,6 +225,23 @@ def _check_x(x: torch.Tensor, k: int) -> torch.Tensor:
     return x
 
 
+def _check_batch(xs: list[torch.Tensor], ys: list[torch.Tensor], m: int, ns: list[int], ks: list[int]) -> int:
+    """Validates the activations and preallocated outputs of a batched launch: every x bf16
+    [m, k] and every y contiguous [m, n] on x's device, all y of ONE dtype (f32 or bf16, the
+    C ABI takes a single y_dtype for the batch).  Returns that dtype's ABI code."""
+    dev = xs[0].device
+    for x, y, n, k in zip(xs, ys, ns, ks):
+        _check_x(x, k)
+        _dev(y)
+        if x.device != dev or y.device != dev:
+            raise ValueError("every x and y of a batch must be on the same device")
+        if x.shape[0] != m or tuple(y.shape) != (m, n):
+            raise ValueError("all problems must share M and y must be [M, n]")
+        if y.dtype != ys[0].dtype:
+            raise ValueError(f"every y of a batch must have one dtype: {ys[0].dtype} and {y.dtype}")
+    return _out_dtype(ys[0].dtype)
+
+
 def gemm_w4a16(x: torch.Tensor, p: Int4Packed, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     x = _check_x(x, p.k)
     y = torch.empty((x.shape[0], p.n), dtype=out_dtype, device=x.device)
@@ -270,16 +287,74 @@ def gemv_w4a16_batched(xs: list[torch.Tensor], ps: list[Int4Packed], ys: list[to
     """One launch for several W4A16 problems with the same M (1..16); outputs preallocated."""
     if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
         raise ValueError("xs, ps, ys must have the same length <= 8")
+    if not ps:
+        return
     m = xs[0].shape[0]
-    arr = (ffi.W4A16Problem * max(1, len(ps)))()
+    yd = _check_batch(xs, ys, m, [p.n for p in ps], [p.k for p in ps])
+    arr = (ffi.W4A16Problem * len(ps))()
     for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
-        _check_x(x, p.k)
-        if x.shape[0] != m or y.shape != (m, p.n):
-            raise ValueError("all problems must share M and y must be [M, n]")
         arr[i] = ffi.W4A16Problem(_ptr(x), _ptr(p.codes), _ptr(p.scales), _ptr(p.zeros), _ptr(y),
                                   p.n, p.k, p.group)
-    yd = _out_dtype(ys[0].dtype)
     ffi.call("castforge_hip_gemv_w4a16_batched", arr, len(ps), m, yd, _stream(xs[0]))
+
+
+@dataclass
+class Int4Planes:
+    """INT4 g128 weights in the GEMV planes layout (castforge_hip_int4g_to_planes): codes u8
+    [T * G * 1024], scales f16 [T, G, 16], zeros u8 [T, G, 8] with T = ceil(N/16), G = K/128."""
+    codes: torch.Tensor
+    scales: torch.Tensor
+    zeros: torch.Tensor
+    n: int
+    k: int
+    group: int = 128
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.codes, self.scales, self.zeros))
+
+
+def int4g_to_planes(p: Int4Packed) -> Int4Planes:
+    """The GEMV planes of canonical INT4 g128 weights (built once, at load time)."""
+    if p.group != 128 or p.k % 128:
+        raise ValueError("GEMV planes hold INT4 weights with group 128 and k % 128 == 0")
+    t, g = (p.n + 15) // 16, p.k // 128
+    dev = p.codes.device
+    pl = Int4Planes(torch.empty(t * g * 1024, dtype=torch.uint8, device=dev),
+                    torch.empty((t, g, 16), dtype=torch.float16, device=dev),
+                    torch.empty((t, g, 8), dtype=torch.uint8, device=dev), p.n, p.k, 128)
+    ffi.call("castforge_hip_int4g_to_planes", _ptr(_dev(p.codes)), _ptr(_dev(p.scales)), _ptr(_dev(p.zeros)),
+             p.n, p.k, 128, _ptr(pl.codes), _ptr(pl.scales), _ptr(pl.zeros), _stream(p.codes))
+    return pl
+
+
+def int4g_from_planes(pl: Int4Planes) -> Int4Packed:
+    """Canonical INT4 g128 arrays back from GEMV planes (bit for bit)."""
+    n, k = pl.n, pl.k
+    g = k // 128
+    dev = pl.codes.device
+    p = Int4Packed(torch.empty((n, k // 8), dtype=torch.int32, device=dev),
+                   torch.empty((n, (g + 7) // 8 * 8), dtype=torch.float16, device=dev),
+                   torch.empty((n, (g + 7) // 8), dtype=torch.int32, device=dev), n, k, 128)
+    ffi.call("castforge_hip_int4g_from_planes", _ptr(_dev(pl.codes)), _ptr(_dev(pl.scales)), _ptr(_dev(pl.zeros)),
+             n, k, 128, _ptr(p.codes), _ptr(p.scales), _ptr(p.zeros), _stream(pl.codes))
+    return p
+
+
+def gemv_w4a16_planes_batched(xs: list[torch.Tensor], ps: list[Int4Planes], ys: list[torch.Tensor]) -> None:
+    """M = 1 decode over GEMV planes, all problems in one launch (one workgroup per CU)."""
+    if not (len(xs) == len(ps) == len(ys)) or not 1 <= len(ps) <= ffi.MAX_BATCH:
+        raise ValueError("xs, ps, ys must have the same length in 1..8")
+    yd = _check_batch(xs, ys, 1, [p.n for p in ps], [p.k for p in ps])
+    arr = (ffi.W4A16Problem * len(ps))()
+    for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
+        arr[i] = ffi.W4A16Problem(_ptr(x), _ptr(p.codes), _ptr(p.scales), _ptr(p.zeros), _ptr(y), p.n, p.k, 128)
+    ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, len(ps), 1, yd, _stream(xs[0]))
+
+
+def gemv_w4a16_planes(x: torch.Tensor, p: Int4Planes, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    y = torch.empty((1, p.n), dtype=out_dtype, device=x.device)
+    gemv_w4a16_planes_batched([x], [p], [y])
+    return y
 
 
 def gemv_w8a16_batched(xs: list[torch.Tensor], qs: list[tuple[torch.Tensor, torch.Tensor]],
@@ -287,31 +362,29 @@ def gemv_w8a16_batched(xs: list[torch.Tensor], qs: list[tuple[torch.Tensor, torc
     """One launch for several W8A16 problems (codes i8 [n, k], scales f32) with the same M."""
     if not (len(xs) == len(qs) == len(ys)) or len(qs) > ffi.MAX_BATCH:
         raise ValueError("xs, qs, ys must have the same length <= 8")
-    m = xs[0].shape[0] if xs else 1
-    arr = (ffi.W8A16Problem * max(1, len(qs)))()
+    if not qs:
+        return
+    m = xs[0].shape[0]
+    yd = _check_batch(xs, ys, m, [q.shape[0] for q, _ in qs], [q.shape[1] for q, _ in qs])
+    arr = (ffi.W8A16Problem * len(qs))()
     for i, (x, (q, s), y) in enumerate(zip(xs, qs, ys)):
         n, k = q.shape
-        _check_x(x, k)
-        if x.shape[0] != m or y.shape != (m, n):
-            raise ValueError("all problems must share M and y must be [M, n]")
-        arr[i] = ffi.W8A16Problem(_ptr(x), _ptr(q), _ptr(_dev(s)), _ptr(y), n, k, _GRAN[granularity])
-    if qs:
-        ffi.call("castforge_hip_gemv_w8a16_batched", arr, len(qs), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
+        arr[i] = ffi.W8A16Problem(_ptr(x), _ptr(_dev(q)), _ptr(_dev(s)), _ptr(y), n, k, _GRAN[granularity])
+    ffi.call("castforge_hip_gemv_w8a16_batched", arr, len(qs), m, yd, _stream(xs[0]))
 
 
 def gemv_nf4_batched(xs: list[torch.Tensor], ps: list["Nf4Packed"], ys: list[torch.Tensor]) -> None:
     """One launch for several NF4 problems with the same M and block size."""
     if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
         raise ValueError("xs, ps, ys must have the same length <= 8")
-    m = xs[0].shape[0] if xs else 1
-    arr = (ffi.Nf4Problem * max(1, len(ps)))()
+    if not ps:
+        return
+    m = xs[0].shape[0]
+    yd = _check_batch(xs, ys, m, [p.n for p in ps], [p.k for p in ps])
+    arr = (ffi.Nf4Problem * len(ps))()
     for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
-        _check_x(x, p.k)
-        if x.shape[0] != m or y.shape != (m, p.n):
-            raise ValueError("all problems must share M and y must be [M, n]")
         arr[i] = ffi.Nf4Problem(_ptr(x), _ptr(p.codes), _ptr(p.absmax), _ptr(y), p.n, p.k, p.block)
-    if ps:
-        ffi.call("castforge_hip_gemv_nf4_batched", arr, len(ps), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
+    ffi.call("castforge_hip_gemv_nf4_batched", arr, len(ps), m, yd, _stream(xs[0]))
 
 
 # -------------------------------------------------------------- outlier suppression ----
@@ -493,13 +566,13 @@ def gemv_gguf_batched(xs: list[torch.Tensor], ps: list[GgufPacked], ys: list[tor
         return
     t = ps[0].ggml_type
     m = xs[0].shape[0]
+    if any(p.ggml_type != t for p in ps):
+        raise ValueError("problems must share the GGML type and M, with x [M, k] and y [M, n]")
+    yd = _check_batch(xs, ys, m, [p.n for p in ps], [p.k for p in ps])
     arr = (ffi.GgufProblem * len(ps))()
     for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
-        _check_x(x, p.k)
-        if p.ggml_type != t or x.shape[0] != m or y.shape != (m, p.n):
-            raise ValueError("problems must share the GGML type and M, with x [M, k] and y [M, n]")
         arr[i] = ffi.GgufProblem(_ptr(x), _ptr(p.codes), _ptr(p.scales), _ptr(y), p.n, p.k)
-    ffi.call("castforge_hip_gemv_gguf_batched", t, arr, len(ps), m, _out_dtype(ys[0].dtype), _stream(xs[0]))
+    ffi.call("castforge_hip_gemv_gguf_batched", t, arr, len(ps), m, yd, _stream(xs[0]))
 
 
 # ------------------------------------------------------------- static W8A8 (calibrate) ----

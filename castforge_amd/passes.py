@@ -699,8 +699,13 @@ class QuantizePass(Pass):
         self.__dict__.update(locals())
         del self.__dict__["self"]
 
+    _UNSUPPORTED = ("fp4", "mxfp4", "nvfp4", "e2m1", "qat", "qat_ste", "ste")
+
     def run(self, module: Module) -> PassResult:
         s = self.scheme.lower()
+        # rejected before any step (e.g. hadamard=true's rotation) touches the module
+        if s in self._UNSUPPORTED:
+            raise ValueError(f"quantize: scheme `{s}` is not part of the HIP quantized-weight path")
         if s in ("f16", "bf16", "mixed_precision", "amp"):
             tgt = "bf16" if s == "bf16" or self.format.lower() == "bf16" else "f16"
             return LowerMixedPrecisionPass(tgt).run(module).with_name(self.name)
@@ -735,8 +740,6 @@ class QuantizePass(Pass):
             r = CalibrateQuantizePass(self.bits, self.samples).run(module)
         elif s in ("smoothquant", "smooth"):
             r = SmoothQuantizePass(self.bits, self.alpha, self.samples).run(module)
-        elif s in ("fp4", "mxfp4", "nvfp4", "e2m1", "qat", "qat_ste", "ste"):
-            raise ValueError(f"quantize: scheme `{s}` is not part of the HIP quantized-weight path")
         elif self.granularity in ("channel", "per_channel"):
             r = QuantizePackedPass("int8_channel", 0, self.round or "half_even", self.min_elements).run(module)
         else:

@@ -20,9 +20,10 @@ import struct
 from dataclasses import dataclass
 from typing import Any
 
+import numpy as np
 import torch
 
-from .ir import Dense, QuantPacked, QuantUniform, TensorRef, TensorType, format_scale
+from .ir import Dense, QuantPacked, QuantUniform, TensorRef, TensorType
 
 
 @dataclass
@@ -35,6 +36,13 @@ class QuantizedI8:
     data: Any  # device int8 tensor
     scale: float
     zero_point: int
+
+
+@dataclass
+class InMemory:
+    """Raw bytes of a tensor whose dtype the loader does not decode (tensor_store.rs:22, kept
+    as DType::U8 by load_safetensors, tensor_store.rs:736-744)."""
+    data: Any  # uint8 tensor
 
 
 @dataclass
@@ -144,7 +152,15 @@ class TensorStore:
             b = e.backing
             shape = tuple(e.ty.shape)
             if isinstance(b, F32Data):
-                put(name, "F32", shape, b.data.detach().contiguous().cpu().numpy().tobytes())
+                vals = b.data.detach().contiguous().cpu().numpy().astype(np.float32, copy=False).ravel()
+                if e.ty.dtype == "f16":  # tensor_store.rs:446-451: truncating f32_to_f16_bits
+                    put(name, "F16", shape, f32_to_f16_bits_trunc(vals).tobytes())
+                elif e.ty.dtype == "bf16":  # tensor_store.rs:452-457: bits >> 16
+                    put(name, "BF16", shape, (vals.view(np.uint32) >> 16).astype(np.uint16).tobytes())
+                else:
+                    put(name, "F32", shape, vals.tobytes())
+            elif isinstance(b, InMemory):
+                put(name, "U8", shape, b.data.detach().contiguous().cpu().numpy().tobytes())
             elif isinstance(b, QuantizedI8):
                 put(name, "I8", shape, b.data.detach().contiguous().cpu().numpy().tobytes(),
                     {"scale": float(b.scale), "zero_point": int(b.zero_point)})
@@ -166,33 +182,50 @@ class TensorStore:
         return struct.pack("<Q", len(hb)) + hb + b"".join(blobs)
 
     def load_safetensors_bytes(self, raw: bytes, device) -> int:
-        import numpy as np
-
+        """tensor_store.rs:656-752: F32; F16 / BF16 decoded exactly to f32 values that keep
+        their dtype; I8 with the `scale` / `zero_point` keys as QuantizedI8 (the type's scale
+        string `{:.6}` with trailing zeros and dot trimmed); every other dtype kept as raw U8
+        bytes.  Packed formats of this library come back from their component tensors."""
         (hlen,) = struct.unpack("<Q", raw[:8])
         header = json.loads(raw[8:8 + hlen].decode())
         base = 8 + hlen
         meta = json.loads(header.pop("__metadata__", {}).get("castforge_packed", "{}"))
-        npd = {"F32": np.float32, "F16": np.float16, "I8": np.int8, "I32": np.int32, "U8": np.uint8}
+        npd = {"F32": np.float32, "F16": np.uint16, "BF16": np.uint16, "I8": np.int8, "I32": np.int32,
+               "U8": np.uint8}
+        width = {"F32": 4, "F16": 2, "BF16": 2}
         parts: dict[str, Any] = {}
         loaded = 0
         for name, h in header.items():
             a, b = h["data_offsets"]
-            arr = np.frombuffer(raw[base + a:base + b], dtype=npd[h["dtype"]]).reshape(h["shape"]).copy()
-            t = torch.from_numpy(arr).to(device)
+            blob = raw[base + a:base + b]
+            shape = tuple(h["shape"])
             stem, _, part = name.rpartition(".")
             if stem in meta and part in ("codes", "scales", "zeros"):
-                parts.setdefault(stem, {})[part] = t
+                dt = np.float16 if h["dtype"] == "F16" else npd[h["dtype"]]
+                parts.setdefault(stem, {})[part] = torch.from_numpy(
+                    np.frombuffer(blob, dtype=dt).reshape(shape).copy()).to(device)
                 continue
-            shape = tuple(h["shape"])
-            if h["dtype"] == "I8":
-                scale = float(h.get("scale", 1.0))
-                zp = int(h.get("zero_point", 0))
-                dt = QuantUniform("i8", "f32", format_scale(scale), zp) if "scale" in h else "i8"
+            dtype = h["dtype"]
+            if dtype in width and len(blob) % width[dtype]:
+                raise ValueError(f"{dtype} tensor `{name}` byte length {len(blob)} is not a multiple of "
+                                 f"{width[dtype]}")
+            if dtype == "F32":
+                vals = np.frombuffer(blob, np.float32).copy()
+                self.insert(TensorEntry(name, TensorType(shape, "f32"), F32Data(torch.from_numpy(vals).to(device))))
+            elif dtype in ("F16", "BF16"):
+                bits = np.frombuffer(blob, np.uint16)
+                vals = f16_bits_to_f32(bits) if dtype == "F16" else (bits.astype(np.uint32) << 16).view(np.float32)
+                self.insert(TensorEntry(name, TensorType(shape, dtype.lower()),
+                                        F32Data(torch.from_numpy(vals.copy()).to(device))))
+            elif dtype == "I8":
+                t = torch.from_numpy(np.frombuffer(blob, np.int8).reshape(shape).copy()).to(device)
+                scale = float(np.float32(h["scale"])) if h.get("scale") is not None else 1.0
+                zp = int(h["zero_point"]) if h.get("zero_point") is not None else 0
+                dt = QuantUniform("i8", "f32", loader_scale_string(scale), zp) if h.get("scale") is not None else "i8"
                 self.insert(TensorEntry(name, TensorType(shape, dt), QuantizedI8(t, scale, zp)))
-            elif h["dtype"] in ("F32", "F16"):
-                self.insert(TensorEntry(name, TensorType(shape, "f32"), F32Data(t.float())))
             else:
-                continue
+                t = torch.from_numpy(np.frombuffer(blob, np.uint8).copy()).to(device)
+                self.insert(TensorEntry(name, TensorType(shape, "u8"), InMemory(t)))
             loaded += 1
         for stem, m in meta.items():
             p = parts.get(stem, {})
@@ -201,6 +234,37 @@ class TensorStore:
                                                               p.get("zeros"), m["group"], tuple(m["shape"]))))
             loaded += 1
         return loaded
+
+
+def loader_scale_string(scale: float) -> str:
+    """The scale string load_safetensors gives an I8 tensor (tensor_store.rs:716-724):
+    `{:.6}` of the f32 scale with trailing zeros, then a trailing dot, trimmed ("1", "0.5")."""
+    return f"{float(np.float32(scale)):.6f}".rstrip("0").rstrip(".")
+
+
+def f16_bits_to_f32(bits):
+    """tensor_store.rs:59-82 on an array of f16 bit patterns: exact, subnormals included, a NaN
+    keeps its payload (mantissa << 13) without the quiet bit being forced."""
+    bits = np.asarray(bits, np.uint16)
+    out = bits.view(np.float16).astype(np.float32).view(np.uint32).copy()
+    u = bits.astype(np.uint32)
+    nan = ((u >> 10) & 0x1F == 0x1F) & (u & 0x3FF != 0)
+    out[nan] = ((u[nan] >> 15) << 31) | 0x7F800000 | ((u[nan] & 0x3FF) << 13)
+    return out.view(np.float32)
+
+
+def f32_to_f16_bits_trunc(vals):
+    """tensor_store.rs:84-102 on an f32 array: mantissa truncated, exponent overflow to +-inf,
+    new exponent <= 0 to signed zero (no subnormals), NaN -> 0x7e00 | sign."""
+    b = np.asarray(vals, np.float32).view(np.uint32)
+    sign = ((b >> 16) & 0x8000).astype(np.uint32)
+    exp = ((b >> 23) & 0xFF).astype(np.int64)
+    mant = b & 0x7FFFFF
+    new_exp = exp - 112
+    res = np.where(new_exp >= 31, sign | 0x7C00,
+                   np.where(new_exp <= 0, sign, sign | (np.clip(new_exp, 0, 31).astype(np.uint32) << 10) | (mant >> 13)))
+    res = np.where(exp == 255, sign | 0x7C00 | np.where(mant != 0, 0x200, 0), res)
+    return res.astype(np.uint16)
 
 
 def dequantize_packed(b: QuantizedPacked):

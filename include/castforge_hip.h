@@ -196,6 +196,36 @@ int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, in
                                          int64_t m, int32_t y_dtype, void *stream,
                                          char **out_error);
 
+/* GEMV planes: the layout of INT4 g128 weights that the M = 1 decode kernel below streams, built
+ * once at load time (no reference counterpart: the reference keeps one i8 per element,
+ * ir/tensor_store.rs:44-48).  For an [N, K] matrix (K % 128 == 0, group 128), T = ceil(N/16),
+ * G = K/128:
+ *   planes_codes : T x G chunks of 1024 bytes; chunk (t, g) holds, at byte 16 * (16 p + r),
+ *                  canonical code words 16 g + 4 p .. 16 g + 4 p + 3 of row 16 t + r
+ *                  (p = 0..3), so one wave-wide 16-byte load reads one contiguous kilobyte;
+ *   planes_scales: f16 [T][G][16], the scale of row 16 t + r, group g at [t][g][r];
+ *   planes_zeros : u8 [T][G][8], byte j = zero point of row 16 t + 2 j (low nibble), 2 j + 1.
+ * Rows past N are zero.  from_planes restores the canonical codes, scales (pad slots 0) and
+ * zeros (pad nibbles 0) bit for bit.  codes / planes_codes 16-byte aligned. */
+int32_t castforge_hip_int4g_to_planes(const uint32_t *codes, const uint16_t *scales_f16, const uint32_t *zeros,
+                                      int64_t rows, int64_t k, int64_t group, void *planes_codes,
+                                      uint16_t *planes_scales, uint8_t *planes_zeros, void *stream,
+                                      char **out_error);
+int32_t castforge_hip_int4g_from_planes(const void *planes_codes, const uint16_t *planes_scales,
+                                        const uint8_t *planes_zeros, int64_t rows, int64_t k, int64_t group,
+                                        uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros, void *stream,
+                                        char **out_error);
+
+/* castforge_hip_gemv_w4a16_batched at M = 1 over GEMV planes (codes / scales_f16 / zeros of each
+ * problem point at its planes; group 128, k % 128 == 0, x and codes 16-byte aligned): the decode
+ * GEMV of `castforge.fused_qmatmul` (codegen/eval.rs:1145-1179, eval_matmul_2d eval.rs:1465-1507)
+ * in one launch of one workgroup per CU.  Every finite bf16 x is handled exactly (a power-of-two
+ * pre-scale per 128 activations, undone on the f32 partial); a non-finite x gives NaN or inf in
+ * the rows it reaches.  Each problem's activations must fit the kernel's LDS (about 2.1 * k bytes
+ * plus 1 KB per 16 rows a workgroup takes: k up to about 65536 for the shapes of a decoder). */
+int32_t castforge_hip_gemv_w4a16_planes_batched(const cfh_w4a16_problem_t *problems, int32_t count,
+                                                int64_t m, int32_t y_dtype, void *stream, char **out_error);
+
 /* The same for INT8 (per-channel or per-tensor scales, k % 64 == 0) and NF4 weights (one block
  * size for the whole batch), e.g. the INT8 block of config 1 or the NF4 MLP of config 3. */
 typedef struct cfh_w8a16_problem_t {

@@ -154,3 +154,33 @@ def test_nf4_batched_rejects_mixed_blocks(cuda):
     ys = [torch.empty((1, 16), dtype=torch.float32, device=cuda) for _ in ps]
     with pytest.raises(Exception, match="block size"):
         ops.gemv_nf4_batched(xs, ps, ys)
+
+
+def test_batched_wrappers_reject_mixed_or_strided_outputs(cuda):
+    """Every batched wrapper validates each y (one dtype for the batch, contiguous, [M, n], on
+    x's device) before the launch: the C ABI takes a single y_dtype, so a bf16 y after an f32
+    one would be written 4 bytes per element."""
+    n, k = 32, 256
+    w = torch.from_numpy(synth.weight(5, 1, n, k)).to(cuda)
+    x = torch.zeros((1, k), dtype=torch.bfloat16, device=cuda)
+    p4 = ops.quantize_int4g(w, 128)
+    q8 = ops.quantize_int8(w, 8, "channel", "half_even")
+    nf = ops.quantize_nf4(w, 64)
+    f32y = lambda: torch.empty((1, n), dtype=torch.float32, device=cuda)  # noqa: E731
+    bad_sets = [
+        ([f32y(), torch.empty((1, n), dtype=torch.bfloat16, device=cuda)], "one dtype"),
+        ([f32y(), torch.empty((1, 2 * n), dtype=torch.float32, device=cuda)[:, ::2]], "contiguous"),
+        ([f32y(), torch.empty((1, n + 1), dtype=torch.float32, device=cuda)], r"\[M, n\]"),
+    ]
+    calls = [
+        lambda ys: ops.gemv_w4a16_batched([x, x], [p4, p4], ys),
+        lambda ys: ops.gemv_w8a16_batched([x, x], [q8, q8], ys, "channel"),
+        lambda ys: ops.gemv_nf4_batched([x, x], [nf, nf], ys),
+    ]
+    for call in calls:
+        for ys, msg in bad_sets:
+            with pytest.raises(ValueError, match=msg):
+                call(ys)
+        ys = [f32y(), f32y()]
+        call(ys)  # a valid batch still runs
+    torch.cuda.synchronize()

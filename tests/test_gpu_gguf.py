@@ -177,7 +177,7 @@ def test_planes_reject_bad_shapes(cuda):
 
 # -------------------------------------------------------------------------------- GEMV ----
 @pytest.mark.parametrize("ty", [Q4_0, Q8_0])
-@pytest.mark.parametrize("m", [1, 2, 3, 9, 16, 17])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 16, 17])
 @pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (64, 11008), (4096, 4096)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
 def test_gemv_matches_oracle(cuda, ty, m, n, k, out):
@@ -245,19 +245,41 @@ def test_gemv_batched_block_matches_single_and_torch(cuda, ty):
         assert bool((err <= ATOL + RTOL * ref.abs()).all()), f"max err {err.max().item():.3e}"
 
 
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0])
 @pytest.mark.parametrize("m", [4, 16])
-def test_gemv_batched_block_m_gt_1(cuda, m):
-    """The seven block projections at M > 1 in one launch equal one call per matrix."""
-    ps, xs, ys = [], [], []
+def test_gemv_batched_block_m_gt_1(cuda, ty, m):
+    """The seven block projections at M > 1 in one launch equal one call per matrix and the
+    oracle's decode-then-matmul (sampled rows of each matrix, to keep the CPU side short)."""
+    ps, xs, ys, raws = [], [], [], []
     for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK):
-        raw = torch.randint(0, 256, (n * k // 32 * 18,), dtype=torch.uint8, device=cuda)
-        raw.view(-1, 18)[:, 0:2] = (torch.randn(n * k // 32, device=cuda) * 0.003).half().view(torch.uint8).view(-1, 2)
-        ps.append(ops.gguf_repack(Q4_0, raw, n, k))
-        xs.append(_x(900 + tid, m, k, cuda)[1])
+        raw = _blocks(ty, n * k // 32, 900 + 10 * tid + ty)
+        raws.append(raw)
+        ps.append(ops.gguf_repack(ty, _dev_u8(raw, cuda), n, k))
+        xs.append(_x(900 + tid, m, k, cuda))
         ys.append(torch.empty((m, n), dtype=torch.float32, device=cuda))
-    ops.gemv_gguf_batched(xs, ps, ys)
-    for x, p, y in zip(xs, ps, ys):
+    ops.gemv_gguf_batched([x for _, x in xs], ps, ys)
+    rng = np.random.default_rng(ty + m)
+    for (xb, x), p, y, raw in zip(xs, ps, ys, raws):
         assert torch.equal(ops.gemm_gguf(x, p, torch.float32), y)
+        rows = np.sort(rng.choice(p.n, 24, replace=False))
+        sub = raw.reshape(p.n, -1)[rows].reshape(-1)  # whole rows of blocks (k % 32 == 0)
+        w = O.gguf_decode(ty, sub, 24 * p.k).reshape(24, p.k)
+        ref = O.matmul_2d(O.bf16_bits_to_f32(xb.reshape(m, p.k)), w, packed_rhs=True)
+        _close(y[:, torch.from_numpy(rows).to(y.device)], ref)
+
+
+@pytest.mark.parametrize("ty", [Q4_0, Q8_0])
+def test_gemv_m1_beyond_split_lds_limit(cuda, ty):
+    """K = 32768 needs more LDS per workgroup than the M = 1 split-K kernel takes, so M = 1
+    runs the skinny kernel's one-row path; checked against the oracle."""
+    n, k = 40, 32768
+    raw = _blocks(ty, n * k // 32, 950 + ty)
+    p = ops.gguf_repack(ty, _dev_u8(raw, cuda), n, k)
+    xb, x = _x(951, 1, k, cuda)
+    y = ops.gemm_gguf(x, p, torch.float32)
+    torch.cuda.synchronize()
+    ref = O.matmul_2d(O.bf16_bits_to_f32(xb.reshape(1, k)), O.gguf_decode(ty, raw, n * k).reshape(n, k), True)
+    _close(y, ref)
 
 
 def test_gemv_batched_rejects_mixed_types(cuda):

@@ -166,3 +166,98 @@ def test_fuse_dequant_rewrite_and_dce():
     assert op.operands == [x, c.results[0]]
     assert not any(o.is_op("stablehlo", "uniform_dequantize") for o in m.ops.values())
     m.verify()
+
+
+# ------------------------------------------------------------ safetensors dtypes (CPU) ----
+def _st_bytes(entries):
+    """A safetensors file from (name, dtype, shape, raw bytes, extra header keys)."""
+    import json as _json
+    import struct as _struct
+
+    header, blobs, off = {}, [], 0
+    for name, dt, shape, data, extra in entries:
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(data)], **extra}
+        blobs.append(data)
+        off += len(data)
+    hb = _json.dumps(header).encode()
+    return _struct.pack("<Q", len(hb)) + hb + b"".join(blobs)
+
+
+def test_safetensors_loader_dtypes_follow_the_reference():
+    """tensor_store.rs:656-752: F16 / BF16 load as f32 values that keep their dtype (exact
+    decode, f16 subnormals and NaN payloads included), I8 with an integral scale gets the
+    trimmed string "1" (no ".0"), and an unknown dtype is kept as raw U8 bytes."""
+    import numpy as np
+
+    from castforge_amd.tensor_store import F32Data, InMemory, QuantizedI8, TensorStore
+
+    f16 = np.array([1.0, -0.5, 6.1e-5, 3e-7, 65504.0, -np.inf], np.float16).view(np.uint16)
+    f16 = np.concatenate([f16, np.array([0x7C01, 0xFE00], np.uint16)])  # signalling / quiet NaN
+    bf = np.array([0x3F80, 0xC2F7, 0x0001, 0x7F80], np.uint16)
+    raw = _st_bytes([("h", "F16", (8,), f16.tobytes(), {}),
+                     ("b", "BF16", (2, 2), bf.tobytes(), {}),
+                     ("q", "I8", (3,), np.array([1, -2, 127], np.int8).tobytes(), {"scale": 1.0, "zero_point": 0}),
+                     ("q2", "I8", (1,), b"\x05", {"scale": 0.0059055118, "zero_point": 0}),
+                     ("i", "I64", (1,), np.array([7], np.int64).tobytes(), {})])
+    st = TensorStore()
+    assert st.load_safetensors_bytes(raw, "cpu") == 5
+    h = st.get("h")
+    assert h.ty.dtype == "f16" and isinstance(h.backing, F32Data)
+    got = h.backing.data.numpy().view(np.uint32)
+    want = np.array([0x3F800000, 0xBF000000, f2u(float(np.float16(6.1e-5))), f2u(float(np.float16(3e-7))),
+                     0x477FE000, 0xFF800000, 0x7F802000, 0xFFC00000], np.uint32)
+    assert got.tolist() == want.tolist()
+    b = st.get("b")
+    assert b.ty.dtype == "bf16" and tuple(b.ty.shape) == (2, 2)
+    assert b.backing.data.numpy().view(np.uint32).tolist() == [0x3F800000, 0xC2F70000, 0x00010000, 0x7F800000]
+    q = st.get("q")
+    assert isinstance(q.backing, QuantizedI8) and str(q.ty.dtype) == "!quant.uniform<i8:f32,1:0>"
+    assert str(st.get("q2").ty.dtype) == "!quant.uniform<i8:f32,0.005906:0>"
+    i = st.get("i")
+    assert isinstance(i.backing, InMemory) and i.ty.dtype == "u8"
+    assert i.backing.data.numpy().tobytes() == np.array([7], np.int64).tobytes()
+    # writing back: F16 / BF16 through the truncating converters, unknown bytes as U8
+    back = TensorStore()
+    assert back.load_safetensors_bytes(st.to_safetensors_bytes(), "cpu") == 5
+    # the writer's converter has no subnormals: the two f16 subnormals come back as +0
+    assert back.get("h").backing.data.numpy().view(np.uint32)[:6].tolist() == [0x3F800000, 0xBF000000, 0, 0,
+                                                                               0x477FE000, 0xFF800000]
+    assert back.get("b").backing.data.numpy().view(np.uint32).tolist() == [0x3F800000, 0xC2F70000, 0x00010000,
+                                                                            0x7F800000]
+    assert back.get("i").backing.data.numpy().tobytes() == np.array([7], np.int64).tobytes()
+    with pytest.raises(ValueError, match="not a multiple of 2"):
+        TensorStore().load_safetensors_bytes(_st_bytes([("x", "BF16", (1,), b"\x00\x00\x00", {})]), "cpu")
+
+
+def test_f16_truncating_writer_matches_reference_rules():
+    """f32_to_f16_bits (tensor_store.rs:84-102): truncation, not rounding; exponent overflow
+    to inf; no subnormals (flush to signed zero); the KAT translator.rs:295-296."""
+    import numpy as np
+
+    from castforge_amd.tensor_store import f32_to_f16_bits_trunc
+
+    v = np.array([-1e-10, 1.0 + 3 * 2 ** -12, 65520.0, 65536.0, 1e-5, -0.0, np.nan, -np.inf, 2.0 ** -14],
+                 np.float32)
+    # 65520 truncates to 65504 (0x7bff) where round-to-nearest-even would give inf
+    assert f32_to_f16_bits_trunc(v).tolist() == [0x8000, 0x3C00, 0x7BFF, 0x7C00, 0x0000, 0x8000, 0x7E00, 0xFC00,
+                                                 0x0400]
+
+
+def f2u(x: float) -> int:
+    import struct as _struct
+
+    return _struct.unpack("<I", _struct.pack("<f", x))[0]
+
+
+@pytest.mark.parametrize("scheme", ["fp4", "nvfp4", "qat"])
+def test_quantize_unsupported_scheme_leaves_module_unchanged(scheme):
+    """quantize(scheme=fp4|..., hadamard=true) raises before the rotation step runs, so the
+    caller's module is not left half transformed (the reference runs QuantizeFp4Pass /
+    InsertQatStePass there, schemes.rs:128-145; this path does not build them)."""
+    m = Module()
+    w = torch.arange(16, dtype=torch.float32).reshape(4, 4)
+    m.constant("w", w.clone())
+    before = m.tensor_store.get("w").backing.data.clone()
+    with pytest.raises(ValueError, match="not part of the HIP"):
+        QuantizePass(scheme=scheme, hadamard=True, block_size=4).run(m)
+    assert torch.equal(m.tensor_store.get("w").backing.data, before)
