@@ -27,6 +27,8 @@ namespace {
 
 typedef int int32x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
 #ifndef CFH_FP8_BK
 #define CFH_FP8_BK 64
@@ -128,34 +130,73 @@ __device__ __forceinline__ void fp8_read_frags(const uint8_t *__restrict__ cur, 
     }
 }
 
+// Eight E4M3 codes (bytes 8 c .. 8 c + 7 of a lane's 32-byte fragment) -> eight exact f16
+// (every E4M3 value, subnormals included, is an f16 normal; scale 1.0 leaves it unchanged).
+__device__ __forceinline__ half8_t e4m3x8_to_f16(const int32x8 &v, int c) {
+    const uint32_t lo = static_cast<uint32_t>(v[2 * c]), hi = static_cast<uint32_t>(v[2 * c + 1]);
+    const half2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
+    const half2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true);
+    const half2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false);
+    const half2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true);
+    return half8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// MFMAs of one slice on W sub-tiles [I0, I1).
+//   kExact false: v_mfma_scale_f32_32x32x64_f8f6f4 on the E4M3 codes.  The fp8 MFMAs sum
+//     their products in a fixed-point adder aligned to the largest product of a block of
+//     eight, keeping about 13 bits below it: 256 + 2^-6 returns 256, and a block holding one
+//     x30 outlier product truncates its small neighbours to ~2^-8 of a typical product.
+//   kExact true: the codes are widened to exact f16 and fed to v_mfma_f32_32x32x16_f16,
+//     whose products are exact and whose sum keeps f32-like precision (measured on gfx950:
+//     256 + 15 x 2^-6 returns 256.234375 exactly).  Twice the MFMA time of the fp8 form.
+//   A lane's 32-byte fragment holds K bytes [32 (lane / 32), + 32) of a 64-wide step; f16
+//   chunk c gives the lane K bytes 32 (lane / 32) + 8 c + 0..7 of both operands, so the
+//   16-wide f16 MFMA c sums a matching set of products and four of them cover the step.
+template <bool kExact, int I0, int I1>
+__device__ __forceinline__ void fp8_mma_range(const Fp8Frags &f, floatx16 (&acc)[4][JT]) {
+#pragma unroll
+    for (int kk = 0; kk < BK / 64; ++kk) {
+        if constexpr (kExact) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                half8_t wv[I1 - I0], av[JT];
+#pragma unroll
+                for (int i = I0; i < I1; ++i) wv[i - I0] = e4m3x8_to_f16(f.w[kk][i], c);
+#pragma unroll
+                for (int j = 0; j < JT; ++j) av[j] = e4m3x8_to_f16(f.a[kk][j], c);
+#pragma unroll
+                for (int i = I0; i < I1; ++i)
+#pragma unroll
+                    for (int j = 0; j < JT; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wv[i - I0], av[j], acc[i][j], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = I0; i < I1; ++i)
+#pragma unroll
+                for (int j = 0; j < JT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[kk][i], f.a[kk][j], acc[i][j],
+                                                                                0, 0, 0, 0, 0, 0);
+        }
+    }
+}
+
+template <bool kExact>
 __device__ __forceinline__ void fp8_mma(const Fp8Frags &f, floatx16 (&acc)[4][JT]) {
-#pragma unroll
-    for (int kk = 0; kk < BK / 64; ++kk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < JT; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[kk][i], f.a[kk][j], acc[i][j],
-                                                                            0, 0, 0, 0, 0, 0);
+    fp8_mma_range<kExact, 0, 4>(f, acc);
 }
 
 // MFMAs of W sub-tiles [2 H, 2 H + 2) (half of a slice's work).
-template <int H>
+template <bool kExact, int H>
 __device__ __forceinline__ void fp8_mma_half(const Fp8Frags &f, floatx16 (&acc)[4][JT]) {
-#pragma unroll
-    for (int kk = 0; kk < BK / 64; ++kk)
-#pragma unroll
-        for (int i = 2 * H; i < 2 * H + 2; ++i)
-#pragma unroll
-            for (int j = 0; j < JT; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.w[kk][i], f.a[kk][j], acc[i][j],
-                                                                            0, 0, 0, 0, 0, 0);
+    fp8_mma_range<kExact, 2 * H, 2 * H + 2>(f, acc);
 }
 
 // One pipeline step: refill ring slot `nxt` with a later slice (LDS-DMA), read the fragments
 // of the following slice from `cur` into `fn`, and run the MFMAs of the fragments already in
 // `f`.  The pointers are restrict-qualified: the compiler then knows that the fragment reads
 // do not depend on the LDS-DMA writes into `nxt` and need not wait for them.
+template <bool kExact>
 __device__ __forceinline__ void fp8_step(const uint8_t *__restrict__ cur, uint8_t *__restrict__ nxt,
                                          bool refill, bool read_next, __amdgpu_buffer_rsrc_t rsrc,
                                          int first_block, int lvoff, int K, int k_next, int wn, int wm,
@@ -163,7 +204,19 @@ __device__ __forceinline__ void fp8_step(const uint8_t *__restrict__ cur, uint8_
                                          floatx16 (&acc)[4][JT]) {
     if (refill) fp8_issue(rsrc, nxt, first_block, lvoff, K, k_next);
     if (read_next) fp8_read_frags(cur, wn, wm, fr, fc, fn);
-    fp8_mma(f, acc);
+    fp8_mma<kExact>(f, acc);
+    if constexpr (kExact) {
+        // 64 f16 MFMAs and 128 conversions per slice: spread the 16 LDS reads and the loads
+        // over the first MFMAs, each behind its share of conversions
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // 8 VALU (conversions)
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // 4 MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+            if (q < kLoadsPerWave) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 VMEM load
+        }
+        return;
+    }
 #if CFH_FP8_INTERLEAVE
     // one wave per SIMD feeds the MFMA pipe: start the MFMAs at once and slot the LDS reads
     // and the LDS-DMA loads between them instead of issuing every read first
@@ -181,6 +234,7 @@ __device__ __forceinline__ void fp8_step(const uint8_t *__restrict__ cur, uint8_
 #endif
 }
 
+template <bool kExact>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4)))
 void fp8_gemm_kernel(const uint8_t *__restrict__ A, const float *__restrict__ sa,
                      const uint8_t *__restrict__ W, const float *__restrict__ sw,
@@ -273,7 +327,7 @@ void fp8_gemm_kernel(const uint8_t *__restrict__ A, const float *__restrict__ sa
         constexpr bool kSteady = decltype(steady)::value;
         // no explicit vmcnt wait: the LDS writes below consume the staging registers, so the
         // compiler waits for exactly the loads they need
-        fp8_mma_half<0>(f, acc);
+        fp8_mma_half<kExact, 0>(f, acc);
         if (kSteady || t + 1 < KT) lwrite(sn, (t + 1) & 1);
         if (kSteady || t + 3 < KT) gload(sn, t + 3);
 #if CFH_FP8_INTERLEAVE
@@ -289,7 +343,7 @@ void fp8_gemm_kernel(const uint8_t *__restrict__ A, const float *__restrict__ sa
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));
         __builtin_amdgcn_s_barrier();
         if (kSteady || t + 1 < KT) fp8_read_frags(lds + ((t + 1) & 1) * kStageBytes, wn, wm, fr, fc, fn);
-        fp8_mma_half<1>(f, acc);
+        fp8_mma_half<kExact, 1>(f, acc);
 #if CFH_FP8_INTERLEAVE
         if (kSteady) {
 #pragma unroll
@@ -337,7 +391,7 @@ void fp8_gemm_kernel(const uint8_t *__restrict__ A, const float *__restrict__ sa
         __builtin_amdgcn_s_barrier();
         const int nk = t + NSTAGE;
         // steady steps are branch-free, so the scheduler can interleave loads, reads and MFMAs
-        fp8_step(lds + ((t + 1) % NSTAGE) * kStageBytes, lds + (t % NSTAGE) * kStageBytes + tile_off,
+        fp8_step<kExact>(lds + ((t + 1) % NSTAGE) * kStageBytes, lds + (t % NSTAGE) * kStageBytes + tile_off,
                  kSteady || nk < KT, kSteady || t + 1 < KT, rsrc, first_block, lvoff, K, nk * BK, wn, wm,
                  fr, fc, f, fn, acc);
     };
@@ -464,17 +518,12 @@ __global__ void fp8_gemm_generic_kernel(const uint8_t *__restrict__ A, const flo
     else static_cast<float *>(Y)[idx] = v;
 }
 
-// devices (bit = device ordinal < 64) on which the kernel's dynamic-LDS limit has been raised
-std::atomic<uint64_t> lds_attr_devices{0};
+// devices (bit = device ordinal < 64) on which each variant's dynamic-LDS limit has been raised
+std::atomic<uint64_t> lds_attr_devices[2];
 
-}  // namespace
-}  // namespace cfh
-
-using namespace cfh;
-
-extern "C" int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m,
-                                          const uint8_t *qw, const float *sw, int64_t n, int64_t k,
-                                          void *y, int32_t y_dtype, void *stream, char **out_error) {
+int32_t gemm_fp8(const uint8_t *qa, const float *sa, int64_t m, const uint8_t *qw, const float *sw,
+                 int64_t n, int64_t k, void *y, int32_t y_dtype, void *stream, char **out_error,
+                 bool exact) {
     return guarded(out_error, [&] {
         require(m >= 0 && n >= 0 && k >= 0, "m, n, k must be non-negative");
         if (m == 0 || n == 0) return;
@@ -489,19 +538,21 @@ extern "C" int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, in
             int dev = 0;
             check_hip(hipGetDevice(&dev), "hipGetDevice");
             const uint64_t bit = dev < 64 ? (uint64_t{1} << dev) : 0;
-            if (bit == 0 || !(lds_attr_devices.load(std::memory_order_acquire) & bit)) {
-                check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(fp8_gemm_kernel),
+            const auto kern = exact ? fp8_gemm_kernel<true> : fp8_gemm_kernel<false>;
+            std::atomic<uint64_t> &done = lds_attr_devices[exact ? 1 : 0];
+            if (bit == 0 || !(done.load(std::memory_order_acquire) & bit)) {
+                check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes),
                           "hipFuncSetAttribute(fp8_gemm_kernel)");
-                lds_attr_devices.fetch_or(bit, std::memory_order_acq_rel);
+                done.fetch_or(bit, std::memory_order_acq_rel);
             }
             const int tiles_m = static_cast<int>((m + BM - 1) / BM), tiles_n = static_cast<int>((n + BN - 1) / BN);
-            fp8_gemm_kernel<<<dim3(tiles_m * tiles_n), dim3(kThreads), kLdsBytes, st>>>(
+            kern<<<dim3(tiles_m * tiles_n), dim3(kThreads), kLdsBytes, st>>>(
                 qa, sa, qw, sw, y, yb,
                 (yb && n % 8 == 0 && aligned(y, 16)) ? 2 : (n % 4 == 0 && aligned(y, 16)) ? 1 : 0,
                 (n % 4 == 0 && aligned(sw, 16)) ? 1 : 0, static_cast<int>(m),
                 static_cast<int>(n), static_cast<int>(k), tiles_m, tiles_n);
-            check_launch("fp8_gemm");
+            check_launch(exact ? "fp8_gemm_exact" : "fp8_gemm");
         } else {
             const int64_t tot = m * n;
             require((tot + 255) / 256 <= 0x7fffffff, "shape too large for the generic FP8 kernel");
@@ -510,4 +561,19 @@ extern "C" int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, in
             check_launch("fp8_gemm_generic");
         }
     });
+}
+
+}  // namespace
+}  // namespace cfh
+
+extern "C" int32_t castforge_hip_gemm_fp8(const uint8_t *qa, const float *sa, int64_t m,
+                                          const uint8_t *qw, const float *sw, int64_t n, int64_t k,
+                                          void *y, int32_t y_dtype, void *stream, char **out_error) {
+    return cfh::gemm_fp8(qa, sa, m, qw, sw, n, k, y, y_dtype, stream, out_error, false);
+}
+
+extern "C" int32_t castforge_hip_gemm_fp8_exact(const uint8_t *qa, const float *sa, int64_t m,
+                                                const uint8_t *qw, const float *sw, int64_t n, int64_t k,
+                                                void *y, int32_t y_dtype, void *stream, char **out_error) {
+    return cfh::gemm_fp8(qa, sa, m, qw, sw, n, k, y, y_dtype, stream, out_error, true);
 }

@@ -119,7 +119,8 @@ class _Evaluator:
                 return ops.gemm_w8a16(x, b.codes, b.scales, "channel", torch.float32)
             if b.format == "fp8_row":
                 qa, sa = ops.quantize_fp8(x)  # per-token dynamic E4M3 activations (W8A8)
-                return ops.gemm_fp8(qa, sa, b.codes, b.scales, out_dtype=torch.float32)
+                # f16-MFMA form: stays within the f32 evaluator's tolerance on any input
+                return ops.gemm_fp8(qa, sa, b.codes, b.scales, out_dtype=torch.float32, exact=True)
             if b.format in ("gguf_q4_0", "gguf_q8_0"):
                 ty = ops.GGML_TYPES["Q4_0" if b.format == "gguf_q4_0" else "Q8_0"]
                 return ops.gemm_gguf(x, ops.GgufPacked(ty, b.codes, b.scales, n, k), torch.float32)
