@@ -12,6 +12,7 @@
 // pattern orders exactly as total_cmp does (NaN above +inf), so four byte-wise radix passes
 // (histogram, then a one-wave bin search) find the threshold's bit pattern without sorting.
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
@@ -178,17 +179,37 @@ __global__ __launch_bounds__(kBlock) void fp8_grid_kernel(const float *__restric
     }
 }
 
-}  // namespace
-}  // namespace cfh
+// Scratch of castforge_hip_quantize_groupwise_noalloc: one threshold-search state per device,
+// held until the process ends.  Host code never passes `scratch` itself to a kernel (in host
+// code the name is a stand-in, not a device address): device_scratch() resolves this device's
+// copy once with hipGetSymbolAddress and every use goes through that pointer.
+static __device__ __align__(256) uint8_t scratch[CFH_GROUPWISE_WORKSPACE_BYTES];
+static_assert(sizeof(SelectWs) <= sizeof(scratch), "selection state fits the scratch array");
 
-using namespace cfh;
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void *scratch_ptr[kMaxDevices] = {};
 
-extern "C" {
+// This device's address of `scratch`, resolved on the first call made on the device (the
+// device current at that call).
+void *device_scratch() {
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < kMaxDevices, "device ordinal beyond the scratch table (64 devices)");
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void *p = nullptr;
+        check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        require(p != nullptr, "hipGetSymbolAddress(scratch) returned NULL");
+        scratch_ptr[dev] = p;
+    }
+    return scratch_ptr[dev];
+}
 
-int32_t castforge_hip_quantize_groupwise(const float *src, int64_t n, int32_t bits, int64_t group_size,
-                                         int32_t awq_salient, float salient_ratio, int32_t round_mode,
-                                         float *deq, float *scales, void *workspace,
-                                         int64_t *salient_count_out, void *stream, char **out_error) {
+// Both groupwise entry points: `workspace` is the caller's buffer or this device's scratch.
+int32_t groupwise(const float *src, int64_t n, int32_t bits, int64_t group_size, int32_t awq_salient,
+                  float salient_ratio, int32_t round_mode, float *deq, float *scales, void *workspace,
+                  bool use_scratch, int64_t *salient_count_out, void *stream, char **out_error) {
     if (salient_count_out) *salient_count_out = 0;
     return guarded(out_error, [&] {
         require(n >= 0, "n must be non-negative");
@@ -208,6 +229,7 @@ int32_t castforge_hip_quantize_groupwise(const float *src, int64_t n, int32_t bi
         if (salient_count_out) *salient_count_out = n > 0 ? cnt : 1;
         if (n == 0) return;
         require(src && deq, "src and deq must not be NULL");
+        if (use_scratch && awq_salient) workspace = device_scratch();
         require(!awq_salient || workspace, "workspace must not be NULL when awq_salient is set");
         hipStream_t st = static_cast<hipStream_t>(stream);
         const float qmin = bits == 4 ? -8.0f : -128.0f, qmax = bits == 4 ? 7.0f : 127.0f;
@@ -230,6 +252,30 @@ int32_t castforge_hip_quantize_groupwise(const float *src, int64_t n, int32_t bi
                                                                       round_mode, ws, deq, scales);
         check_launch("groupwise");
     });
+}
+
+}  // namespace
+}  // namespace cfh
+
+using namespace cfh;
+
+extern "C" {
+
+int32_t castforge_hip_quantize_groupwise(const float *src, int64_t n, int32_t bits, int64_t group_size,
+                                         int32_t awq_salient, float salient_ratio, int32_t round_mode,
+                                         float *deq, float *scales, void *workspace,
+                                         int64_t *salient_count_out, void *stream, char **out_error) {
+    return groupwise(src, n, bits, group_size, awq_salient, salient_ratio, round_mode, deq, scales, workspace,
+                     false, salient_count_out, stream, out_error);
+}
+
+int32_t castforge_hip_quantize_groupwise_noalloc(const float *src, int64_t n, int32_t bits,
+                                                 int64_t group_size, int32_t awq_salient,
+                                                 float salient_ratio, int32_t round_mode, float *deq,
+                                                 float *scales, int64_t *salient_count_out, void *stream,
+                                                 char **out_error) {
+    return groupwise(src, n, bits, group_size, awq_salient, salient_ratio, round_mode, deq, scales, nullptr,
+                     true, salient_count_out, stream, out_error);
 }
 
 int32_t castforge_hip_quantize_fp8_grid(const float *src, int64_t n, int32_t e5m2, int32_t mxfp8,

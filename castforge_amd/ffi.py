@@ -125,6 +125,8 @@ SIGNATURES = {
     "castforge_hip_gemm_fp8_exact": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, c_int32, _P, _E]),
     "castforge_hip_quantize_groupwise": (c_int32, [_P, c_int64, c_int32, c_int64, c_int32, ctypes.c_float, c_int32,
                                                    _P, _P, _P, POINTER(c_int64), _P, _E]),
+    "castforge_hip_quantize_groupwise_noalloc": (c_int32, [_P, c_int64, c_int32, c_int64, c_int32, ctypes.c_float,
+                                                           c_int32, _P, _P, POINTER(c_int64), _P, _E]),
     "castforge_hip_quantize_fp8_grid": (c_int32, [_P, c_int64, c_int32, c_int32, c_int64, _P, _P, _E]),
     "castforge_hip_qmatmul_epilogue": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, c_int32, _P, _E]),
     "castforge_hip_static_quantize": (c_int32, [_P, c_int64, ctypes.c_float, c_int32, _P, _P, _E]),

@@ -12,7 +12,8 @@
  *     hipStream_t (NULL = the null stream); work is enqueued asynchronously on it;
  *   - shapes are int64 element counts; weights are row-major [N, K] with K contiguous, the
  *     `packed_rhs` layout of the reference (passes/weights/fold.rs:549-554);
- *   - calls on different streams are independent; no global mutable state.
+ *   - calls on different streams are independent; no global mutable state, except the
+ *     per-device scratch array of castforge_hip_quantize_groupwise_noalloc.
  *
  * Packed formats (new in this library; the reference stores one i8 per element):
  *   INT8  : codes i8 [N, K]; scales f32 [N] (per channel) or [1] (per tensor).
@@ -130,6 +131,20 @@ int32_t castforge_hip_quantize_groupwise(const float *src, int64_t n, int32_t bi
                                          int32_t awq_salient, float salient_ratio, int32_t round_mode,
                                          float *deq, float *scales, void *workspace,
                                          int64_t *salient_count_out, void *stream, char **out_error);
+
+/* No counterpart in the reference.  castforge_hip_quantize_groupwise for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the AWQ threshold search runs in a static per-device scratch array of
+ * CFH_GROUPWISE_WORKSPACE_BYTES (held until the process ends) instead of a caller workspace,
+ * and the call allocates nothing.  Same arguments and results otherwise; n < 2^32 (the limit
+ * of the search's 32-bit counters), larger tensors are rejected with rc 1.  Every call on one
+ * GPU shares that GPU's array and re-initialises it on its stream: calls that overlap on one
+ * GPU (different streams or host threads) race and must be serialised by the caller. */
+int32_t castforge_hip_quantize_groupwise_noalloc(const float *src, int64_t n, int32_t bits,
+                                                 int64_t group_size, int32_t awq_salient,
+                                                 float salient_ratio, int32_t round_mode, float *deq,
+                                                 float *scales, int64_t *salient_count_out, void *stream,
+                                                 char **out_error);
 
 /* FP8 / MXFP8 uniform-grid write-back quantizer.  Replaces QuantizeFp8Pass::run
  * (passes/quantize/schemes.rs:633-754): blocks of max(block_size, 4) consecutive elements;
