@@ -1,4 +1,4 @@
-// Prefill (M > 16) dequant-fused GEMM for packed INT4 / INT8 / NF4 weights on gfx950 MFMA.
+// Prefill (M > 16) dequant-fused GEMM for packed INT4 / INT8 / NF4 / GGUF weights on gfx950 MFMA.
 //
 // Y[m, n] = sum_k x[m, k] * dequant(W)[n, k]: x bf16 [M, K]; W packed [N, K] (the packed_rhs
 // layout, passes/weights/fold.rs:549-554).  This is the evaluation of `castforge.fused_qmatmul`
@@ -6,28 +6,30 @@
 // reference interpreter runs an M*N*K scalar f32 loop on one core.
 //
 // Exactness.  The product must stay within 1e-2 relative / 1e-3 absolute of the f32 evaluator
-// for any row, including near-zero outputs, so the dequantized weight is never rounded to
-// 16 bits.  Every weight w (an f32 value in the evaluator) is carried as an exact f16 pair
-// hi + lo and the tile runs two MFMAs, x * hi and x * lo:
-//   INT4  w = (q - z) * s with s an f16 scale: (q - z) is an exact f16, hi = f16(w) and
-//         lo = w - hi are exact (a 15-bit product split over two 11-bit halves);
-//   NF4   w = f32(T[q] * absmax) as the evaluator rounds it, hi = f16(w), lo = f16(w - hi)
-//         (relative error <= 2^-22);
-//   INT8  w = q * s with one scale per row (or tensor): q is an exact f16 and s multiplies
-//         the f32 accumulator in the epilogue, so one MFMA suffices.
-// Activations are converted bf16 -> f16 (exact for 2^-14 <= |x| < 65504).
+// for any finite input, including near-zero outputs and activations beyond f16's range, so
+// v_mfma_f32_32x32x16_bf16 is fed exact operands only: x as the bf16 it is, and every weight as
+// one or more bf16 terms that sum exactly to the f32 weight the evaluator uses.
+//   INT4  (q - z) * s and Q4_0 (q - 8) * d (15 significant bits): two terms, hi = bf16(w),
+//         lo = w - hi;
+//   INT8  one term, the integer q; the per-row (or tensor) scale multiplies the accumulator;
+//   Q8_0  q * d (19 bits) and NF4 f32(T[q] * absmax) (24 bits): three terms.
+//   A non-finite scale gives a non-finite weight (the remainder terms are 0) and so, as in the
+//   evaluator, non-finite outputs on its row.
+//   (A one-term INT4 form that applies the group scale to the accumulator -- multiplying it by
+//   s_prev / s_cur at every group start -- was measured: 1.15x faster at 128 x 128 tiles, but
+//   the rounding of the running sum at each group start put near-zero outputs of
+//   cancellation-heavy rows further from the exact value than the evaluator's own f32 sum, and
+//   VALU work on the accumulators keeps them out of the AGPRs, which spills the large tiles.)
 //
 // Design:
 //   * workgroup tile BN (n) x BM (m) with 4 waves; W is the MFMA row operand, so each lane
 //     ends with 4 consecutive n of one m;
-//   * per K slice of 32 the workgroup loads codes / metadata and x into registers, dequantizes
-//     once per workgroup (shared by all BM rows of x) and writes f16 planes to LDS: W hi
-//     [BN][32], W lo [BN][32] (INT4 / NF4) and x [BM][32]; 64-byte rows, 16-byte chunks
-//     XOR-swizzled by row so fragment reads hit distinct banks;
-//   * v_mfma_f32_32x32x16_f16; two LDS stages: while slice t's MFMAs run, slice t+1 is
-//     converted from registers into the other stage and slice t+2's global loads are issued;
-//   * the nibble / byte extraction places codes in a fixed order inside each 16-byte chunk;
-//     x is written to LDS in the same order, so the MFMA's k index matches on both operands;
+//   * per K slice of 32 the workgroup loads codes / metadata and x into registers, decodes the
+//     weights once per workgroup (shared by all BM rows of x) into bf16 planes in LDS and
+//     copies x as is: 64-byte rows, 16-byte chunks XOR-swizzled by row so fragment reads hit
+//     distinct banks; both operands in natural k order;
+//   * two LDS stages: while slice t's MFMAs run, slice t+1 is decoded from registers into the
+//     other stage and slice t+R's global loads are issued;
 //   * XCD-aware tile order (each XCD owns a contiguous range of tiles grouped by m).
 #include <cstdio>
 #include <cstdlib>
@@ -39,8 +41,7 @@
 namespace cfh {
 namespace {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
@@ -48,8 +49,13 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 // GEMV's FMT_Q4_0 / FMT_Q8_0)
 enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2, FMT_Q4G = 3, FMT_Q8G = 4 };
 
+// bf16 weight planes per format
+template <int FMT> constexpr int planes() {
+    return FMT == FMT_INT8 ? 1 : FMT == FMT_Q4G || FMT == FMT_INT4 ? 2 : 3;
+}
+
 constexpr int kThreads = 256;
-constexpr int BK = 32;     // K elements per slice: one 64-byte f16 row per tile row
+constexpr int BK = 32;     // K elements per slice: one 64-byte bf16 row per tile row
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
 
@@ -78,47 +84,38 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
                                              static_cast<int>(bytes), 0x00020000);
 }
 
-__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
-__device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+// f32 of the low / high bf16 of a packed pair
+__device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// Upper halves of two f32 holding bf16-exact values -> one bf16 pair (a low, b high).
+__device__ __forceinline__ uint32_t pack_hi16(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
 
 // Physical 16-byte chunk of logical chunk c in a 64-byte tile row r.
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 2) & 3); }
 
-// Index, within an 8-element k-run, of the element the code extraction puts in f16 slot i.
-template <int FMT>
-__device__ __forceinline__ int perm_src(int i) {
-    if constexpr (FMT == FMT_INT4 || FMT == FMT_Q4G) return (i >> 1) + ((i & 1) << 2);
-    else if constexpr (FMT == FMT_INT8 || FMT == FMT_Q8G) return ((i >> 2) << 2) + ((i >> 1) & 1) + ((i & 1) << 1);
-    else return i;
+// INT8 word (signed codes of k .. k + 3) -> 2 bf16 pairs of exact q in k order.
+__device__ __forceinline__ uint2 int8_word_bf16(uint32_t w) {
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = static_cast<float>(static_cast<int32_t>(w << (24 - 8 * j)) >> 24);
+    return make_uint2(pack_hi16(v[0], v[1]), pack_hi16(v[2], v[3]));
 }
 
-// INT4 word (8 codes) -> 4 f16 pairs of exact (q - z), slot order (n0,n4),(n1,n5),(n2,n6),(n3,n7).
-__device__ __forceinline__ void int4_word_qz(uint32_t w, uint32_t z, uint32_t out[4]) {
-    const uint32_t zc1024 = (0xE400u + z) * 0x00010001u;       // -(1024 + z) splatted
-    const uint32_t zc64 = (0xD400u + (z << 4)) * 0x00010001u;  // -(64 + z) splatted
-    const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-    const uint32_t w8 = w >> 8;
-    out[0] = as_u(as_h2((w & 0x000F000Fu) | 0x64006400u) + as_h2(zc1024));
-    out[1] = as_u(as_h2((w & 0x00F000F0u) | 0x64006400u) * sixteenth + as_h2(zc64));
-    out[2] = as_u(as_h2((w8 & 0x000F000Fu) | 0x64006400u) + as_h2(zc1024));
-    out[3] = as_u(as_h2((w8 & 0x00F000F0u) | 0x64006400u) * sixteenth + as_h2(zc64));
-}
-
-// INT8 word (4 signed codes) -> 2 f16 pairs of exact q, slot order (b0,b2),(b1,b3).
-__device__ __forceinline__ void int8_word_q(uint32_t w, uint32_t out[2]) {
-    const half2_t c1152 = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
-    const uint32_t u = w ^ 0x80808080u;
-    out[0] = as_u(as_h2((u & 0x00FF00FFu) | 0x64006400u) + c1152);
-    out[1] = as_u(as_h2(((u >> 8) & 0x00FF00FFu) | 0x64006400u) + c1152);
-}
-
-// f32 pair -> exact-as-possible f16 hi pair and f16 residual pair (hi + lo == w to 2^-22).
-__device__ __forceinline__ void split_pair(float w0, float w1, uint32_t &hi, uint32_t &lo) {
-    const _Float16 h0 = static_cast<_Float16>(w0), h1 = static_cast<_Float16>(w1);
-    const _Float16 l0 = static_cast<_Float16>(w0 - static_cast<float>(h0));
-    const _Float16 l1 = static_cast<_Float16>(w1 - static_cast<float>(h1));
-    hi = as_u(half2_t{h0, h1});
-    lo = as_u(half2_t{l0, l1});
+// f32 pair -> T bf16 pairs whose sum is the pair exactly (for values of up to 8 T significant
+// bits; T = 2 or 3).  Each term is the RNE bf16 of what the previous ones leave, and that
+// remainder is exact in f32.  A non-finite value gives a non-finite first term (and NaN
+// remainders), so its products stay non-finite.
+template <int T>
+__device__ __forceinline__ void split_bf16(float w0, float w1, uint32_t (&t)[3]) {
+#pragma unroll
+    for (int i = 0; i < T; ++i) {
+        t[i] = f32x2_to_bf16x2_rne(w0, w1);
+        w0 -= bf_lo(t[i]);
+        w1 -= bf_hi(t[i]);
+    }
 }
 
 template <int BM, int BN, int WN>
@@ -130,6 +127,10 @@ struct Cfg {
     static constexpr int kRowBytes = BK * 2;     // 64
 };
 
+// LDS bytes of one stage: P weight planes, then the x tile.
+template <int FMT, int BM, int BN>
+constexpr int stage_bytes() { return planes<FMT>() * BN * 64 + BM * 64; }
+
 // W rows handled per thread per slice: BN / 256 (BN = 256 -> 1 row, BN = 128 -> lanes pair up)
 // Large tiles keep one wave per SIMD (their accumulators fill the register file); tiles of
 // 128 x 128 and below leave room for a second workgroup per CU.
@@ -137,11 +138,10 @@ template <int FMT, int BM, int BN, int WN, int R>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM * BN > 128 * 128 ? 1 : 2, BM * BN > 128 * 128 ? 1 : 2)))
 void prefill_qgemm_kernel(PfArgs a) {
     using C = Cfg<BM, BN, WN>;
-    constexpr int P = FMT == FMT_INT8 ? 1 : 2;   // f16 planes of W (hi, lo)
+    constexpr int P = planes<FMT>();
     constexpr int kWPlane = BN * C::kRowBytes;
-    constexpr int kXPlane = BM * C::kRowBytes;
-    constexpr int kStage = P * kWPlane + kXPlane;
-    // x slice: BM rows x 4 chunks of 16 bytes; W slice: BN rows x (16 B INT4/NF4 | 32 B INT8)
+    constexpr int kStage = stage_bytes<FMT, BM, BN>();
+    // x slice: BM rows x 4 chunks of 16 bytes; W slice: BN rows x (16 B INT4/NF4/Q4_0 | 32 B INT8/Q8_0)
     constexpr int kXPieces = BM * 4 / kThreads;  // 16-byte x pieces per thread
     constexpr int kWRowsPerThread = BN >= kThreads ? BN / kThreads : 1;
     constexpr int kWThreadsPerRow = BN >= kThreads ? 1 : kThreads / BN;  // split a row's bytes
@@ -204,7 +204,7 @@ void prefill_qgemm_kernel(PfArgs a) {
     struct Regs {
         uint4 x[kXPieces];
         uint32_t w[kWBytesThread / 4];
-        uint32_t s, z;  // INT4: f16 scale bits, zero word; NF4: absmax bits
+        uint32_t s, z;  // INT4: f16 scale bits, zero word; NF4: absmax bits; GGUF: d bits
     };
     auto gload = [&](Regs &r, int kt) {
         const int k0 = kt * BK;
@@ -257,7 +257,7 @@ void prefill_qgemm_kernel(PfArgs a) {
         }
     };
 
-    // registers of slice kt -> f16 planes of LDS stage `st`
+    // registers of slice kt -> bf16 planes of LDS stage `st`
     auto lwrite = [&](const Regs &r, int kt, int st) {
         uint8_t *base = lds + st * kStage;
         uint8_t *wplane = base;
@@ -266,84 +266,64 @@ void prefill_qgemm_kernel(PfArgs a) {
         for (int p = 0; p < kXPieces; ++p) {
             const int piece = tid + p * kThreads;
             const int row = piece >> 2, ch = piece & 3;
-            const uint32_t v[4] = {r.x[p].x, r.x[p].y, r.x[p].z, r.x[p].w};
-            uint32_t o[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int s0 = perm_src<FMT>(2 * q), s1 = perm_src<FMT>(2 * q + 1);
-                const uint16_t b0 = static_cast<uint16_t>(v[s0 >> 1] >> (16 * (s0 & 1)));
-                const uint16_t b1 = static_cast<uint16_t>(v[s1 >> 1] >> (16 * (s1 & 1)));
-                o[q] = as_u(half2_t{static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))});
-            }
-            *reinterpret_cast<uint4 *>(xplane + row * C::kRowBytes + swz(row, ch) * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4 *>(xplane + row * C::kRowBytes + swz(row, ch) * 16) = r.x[p];
         }
         // W: this thread's bytes cover chunks [c0, c0 + nch) of row wr
-        if constexpr (FMT == FMT_INT4 || FMT == FMT_Q4G) {
-            // one code word = 8 k = one 16-byte chunk of each plane (Q4_0: zero point 8)
-            const int g = kt * BK / a.group;
-            const uint32_t s2 = ((g & 1) ? (r.s >> 16) : (r.s & 0xFFFFu)) * 0x00010001u;
-            const uint32_t z = FMT == FMT_Q4G ? 8u : (r.z >> (4 * (g & 7))) & 15u;
-#pragma unroll
-            for (int t = 0; t < kWBytesThread / 4; ++t) {
-                const int ch = wb / 4 + t;
-                uint32_t qz[4], hi[4], lo[4];
-                int4_word_qz(r.w[t], z, qz);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const half2_t h = as_h2(qz[q]) * as_h2(s2);
-                    hi[q] = as_u(h);
-                    lo[q] = as_u(__builtin_elementwise_fma(as_h2(qz[q]), as_h2(s2), -h));
-                }
-                const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
-                *reinterpret_cast<uint4 *>(wplane + off) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-                *reinterpret_cast<uint4 *>(wplane + kWPlane + off) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            }
-        } else if constexpr (FMT == FMT_NF4) {
-            const float am = __uint_as_float(r.s);
-#pragma unroll
-            for (int t = 0; t < kWBytesThread / 4; ++t) {
-                const int ch = wb / 4 + t;
-                uint32_t hi[4], lo[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint2 e = lut[(r.w[t] >> (8 * q)) & 255u];
-                    split_pair(__uint_as_float(e.x) * am, __uint_as_float(e.y) * am, hi[q], lo[q]);
-                }
-                const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
-                *reinterpret_cast<uint4 *>(wplane + off) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-                *reinterpret_cast<uint4 *>(wplane + kWPlane + off) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            }
-        } else if constexpr (FMT == FMT_Q8G) {
-            // exact q f16 pairs times the block's f16 d, split into hi = f16(q d) and the exact
-            // remainder lo (a product of at most 19 significant bits)
-            const int g = kt * BK / a.group;
-            const uint32_t s2 = ((g & 1) ? (r.s >> 16) : (r.s & 0xFFFFu)) * 0x00010001u;
+        if constexpr (FMT == FMT_INT8) {
+            // two code words = 8 k = one chunk
 #pragma unroll
             for (int t = 0; t < kWBytesThread / 8; ++t) {
                 const int ch = wb / 8 + t;
-                uint32_t qv[4], hi[4], lo[4];
-                int8_word_q(r.w[2 * t], qv);
-                int8_word_q(r.w[2 * t + 1], qv + 2);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const half2_t h = as_h2(qv[q]) * as_h2(s2);
-                    hi[q] = as_u(h);
-                    lo[q] = as_u(__builtin_elementwise_fma(as_h2(qv[q]), as_h2(s2), -h));
-                }
-                const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
-                *reinterpret_cast<uint4 *>(wplane + off) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-                *reinterpret_cast<uint4 *>(wplane + kWPlane + off) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+                const uint2 h0 = int8_word_bf16(r.w[2 * t]), h1 = int8_word_bf16(r.w[2 * t + 1]);
+                *reinterpret_cast<uint4 *>(wplane + wr * C::kRowBytes + swz(wr, ch) * 16) =
+                    make_uint4(h0.x, h0.y, h1.x, h1.y);
             }
         } else {
-            // INT8: two code words = 8 k = one chunk
+            // f32 weights as the evaluator forms them, split into P exact bf16 terms
+            float d = 0.0f;
+            float zf = 0.0f;
+            if constexpr (FMT == FMT_NF4) {
+                d = __uint_as_float(r.s);
+            } else {
+                if constexpr (FMT == FMT_INT4) zf = static_cast<float>((r.z >> (4 * ((kt * BK / a.group) & 7))) & 15u);
+                const int g = kt * BK / a.group;
+                d = f16_to_f32(static_cast<uint16_t>((g & 1) ? (r.s >> 16) : (r.s & 0xFFFFu)));
+            }
+            constexpr int kWordsPerChunk = FMT == FMT_Q8G ? 2 : 1;
 #pragma unroll
-            for (int t = 0; t < kWBytesThread / 8; ++t) {
-                const int ch = wb / 8 + t;
-                uint32_t h0[2], h1[2];
-                int8_word_q(r.w[2 * t], h0);
-                int8_word_q(r.w[2 * t + 1], h1);
-                *reinterpret_cast<uint4 *>(wplane + wr * C::kRowBytes + swz(wr, ch) * 16) =
-                    make_uint4(h0[0], h0[1], h1[0], h1[1]);
+            for (int t = 0; t < kWBytesThread / (4 * kWordsPerChunk); ++t) {
+                const int ch = wb / (4 * kWordsPerChunk) + t;
+                float v[8];
+                if constexpr (FMT == FMT_NF4) {
+                    const uint32_t w = r.w[t];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint2 e = lut[(w >> (8 * q)) & 255u];
+                        v[2 * q] = __uint_as_float(e.x) * d;
+                        v[2 * q + 1] = __uint_as_float(e.y) * d;
+                    }
+                } else if constexpr (FMT == FMT_Q4G || FMT == FMT_INT4) {
+                    // exact (q - z) times the f16 scale: 15 significant bits, exact in f32
+                    const uint32_t w = r.w[t];
+                    const float z = FMT == FMT_Q4G ? 8.0f : zf;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        v[q] = (static_cast<float>((w >> (4 * q)) & 15u) - z) * d;
+                } else {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            v[4 * h + q] = static_cast<float>(static_cast<int32_t>(r.w[2 * t + h] << (24 - 8 * q)) >> 24) * d;
+                }
+                uint32_t terms[4][3];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) split_bf16<P>(v[2 * q], v[2 * q + 1], terms[q]);
+                const int off = wr * C::kRowBytes + swz(wr, ch) * 16;
+#pragma unroll
+                for (int pl = 0; pl < P; ++pl)
+                    *reinterpret_cast<uint4 *>(wplane + pl * kWPlane + off) =
+                        make_uint4(terms[0][pl], terms[1][pl], terms[2][pl], terms[3][pl]);
             }
         }
     };
@@ -359,25 +339,25 @@ void prefill_qgemm_kernel(PfArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    auto mma_stage = [&](int st) {
-        const uint8_t *base = lds + st * kStage;
+    auto mma_stage = [&](int t) {
+        const uint8_t *base = lds + (t & 1) * kStage;
         const uint8_t *wplane = base;
         const uint8_t *xplane = base + P * kWPlane;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
             const int ch = 2 * kk + fh;
-            half8_t wf[P][C::I], xf[C::J];
+            bf16x8_t wf[P][C::I], xf[C::J];
 #pragma unroll
             for (int i = 0; i < C::I; ++i) {
                 const int r = wn + i * 32 + fr;
 #pragma unroll
                 for (int p = 0; p < P; ++p)
-                    wf[p][i] = *reinterpret_cast<const half8_t *>(wplane + p * kWPlane + r * C::kRowBytes + swz(r, ch) * 16);
+                    wf[p][i] = *reinterpret_cast<const bf16x8_t *>(wplane + p * kWPlane + r * C::kRowBytes + swz(r, ch) * 16);
             }
 #pragma unroll
             for (int j = 0; j < C::J; ++j) {
                 const int r = wm + j * 32 + fr;
-                xf[j] = *reinterpret_cast<const half8_t *>(xplane + r * C::kRowBytes + swz(r, ch) * 16);
+                xf[j] = *reinterpret_cast<const bf16x8_t *>(xplane + r * C::kRowBytes + swz(r, ch) * 16);
             }
 #pragma unroll
             for (int p = 0; p < P; ++p)
@@ -385,10 +365,7 @@ void prefill_qgemm_kernel(PfArgs a) {
                 for (int i = 0; i < C::I; ++i)
 #pragma unroll
                     for (int j = 0; j < C::J; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[p][i], xf[j], acc[i][j], 0, 0, 0);
-#ifdef CFH_PF_SB
-            __builtin_amdgcn_sched_barrier(0);
-#endif
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[p][i], xf[j], acc[i][j], 0, 0, 0);
         }
     };
 
@@ -413,7 +390,7 @@ void prefill_qgemm_kernel(PfArgs a) {
         constexpr bool kSteady = decltype(steady)::value;
         constexpr int si = decltype(SI)::value;
         if (kSteady || t + R < KT) gload(ring[si], t + R);
-        mma_stage(t & 1);
+        mma_stage(t);
         if (kSteady || t + 1 < KT) lwrite(ring[(si + 1) % R], t + 1, (t + 1) & 1);
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));
         __builtin_amdgcn_s_barrier();
@@ -480,8 +457,7 @@ void prefill_qgemm_kernel(PfArgs a) {
 
 template <int FMT, int BM, int BN, int WN, int R>
 void launch_cfg(PfArgs a, hipStream_t st) {
-    constexpr int P = FMT == FMT_INT8 ? 1 : 2;
-    constexpr int lds = 2 * (P * BN * 64 + BM * 64);
+    constexpr int lds = 2 * stage_bytes<FMT, BM, BN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;

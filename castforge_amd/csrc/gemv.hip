@@ -12,10 +12,12 @@
 //     group / NF4 block per row and its scale multiplies the fp32 MFMA result (no rounding of
 //     the scale into the f16 operand);
 //   * v_mfma_f32_16x16x32_f16 with dequantized W rows as B and the activation rows as A; x is
-//     converted from bf16 to f16 in LDS, in the permuted order the nibble extraction produces;
+//     converted from bf16 to f16 in LDS, in the permuted order the nibble extraction produces,
+//     each (row, chunk) scaled by an exact power of two that the chunk's f32 partial undoes, so
+//     any finite bf16 activation is accepted (x_scale_of);
 //   * M = 1 (skinny_m1_split_kernel): each wave owns a contiguous quarter of K, copies its
 //     groups' scales / zero points and its x slice into its own LDS region up front, and then
-//     streams codes only, with the INT4 zero point folded out of the per-code decode;
+//     streams codes only, decoded to exact (q - z) f16 operands;
 //   * M = 2..16 (skinny_qgemm_kernel): the waves interleave over K in units of NB chunks,
 //     double-buffered per wave, with exact (q - z) / q / NF4 hi+lo operands;
 //   * problems with the longest K are dispatched first so no long workgroup forms a tail.
@@ -77,7 +79,7 @@ struct Problem {
     int32_t tile_begin;     // first workgroup index of this problem
     int32_t kc;             // K elements staged per LDS pass (M = 1 split-K: LDS bytes per wave)
     int32_t soff, zoff;     // M = 1 split-K: scale and zero-point pieces within a wave's LDS bytes
-    int32_t xsoff;          // M = 1 split-K, INT4: per-chunk x sums within a wave's LDS bytes
+    int32_t xsoff;          // M = 1 split-K: per-chunk activation post factors within a wave's LDS bytes
 };
 
 struct Batch {
@@ -85,6 +87,7 @@ struct Batch {
     int32_t count;
     int32_t m;
     int32_t y_bf16;
+    int32_t kc_max;  // M > 1 kernel: the largest problem's kc (the activation post factors follow)
 };
 
 template <int FMT> constexpr int codes_per_byte() { return FMT == FMT_INT8 || FMT == FMT_Q8_0 ? 1 : 2; }
@@ -108,6 +111,50 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
     uint32_t v;
     asm("v_mov_b32 %0, %1" : "=v"(v) : "i"(c));
     return v;
+}
+
+// Activation range.  bf16 activations span 2^-133 .. 2^128, f16 operands 2^-24 .. 65504.  Each
+// chunk of x (one row, the K elements one chunk of weight codes spans) is multiplied by an
+// exact power of two pre = 2^-sh chosen from the chunk's largest bf16 exponent e:
+// sh = clamp(e - 141, -126, 126) puts the chunk's largest element in [2^14, 2^15), so every
+// element within 2^-28 of it converts to f16 exactly and smaller ones lose at most 2^-25 of
+// 2^-sh.  The chunk's f32 partial sum is multiplied by post = 2^sh, which undoes the scale
+// exactly: y(2^e x) = 2^e y(x) bit for bit while nothing overflows.  Inf / NaN stay non-finite.
+__device__ __forceinline__ uint32_t bf16x8_emax(const uint32_t wv[4]) {
+    uint32_t e = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        e = max(e, (wv[q] >> 7) & 0xFFu);
+        e = max(e, (wv[q] >> 23) & 0xFFu);
+    }
+    return e;
+}
+
+// Max over aligned groups of R lanes (R = 1, 2, 4, 8 or 16), every lane of a group receiving it.
+template <int R>
+__device__ __forceinline__ uint32_t lane_group_max(uint32_t v) {
+#pragma unroll
+    for (int o = 1; o < R; o <<= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o)));
+    return v;
+}
+
+__device__ __forceinline__ void x_scale_of(uint32_t emax, float &pre, float &post) {
+    int sh = static_cast<int>(emax) - 141;
+    sh = sh < -126 ? -126 : sh > 126 ? 126 : sh;
+    pre = __uint_as_float(static_cast<uint32_t>(127 - sh) << 23);
+    post = __uint_as_float(static_cast<uint32_t>(127 + sh) << 23);
+}
+
+// 8 bf16 (4 words) -> 4 f16 pairs of x * pre in the extraction order of FMT.
+__device__ __forceinline__ void bf16x8_to_f16_perm(int fmt, const uint32_t wv[4], float pre, uint32_t o[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int s0 = perm_src(fmt, 2 * q), s1 = perm_src(fmt, 2 * q + 1);
+        const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
+        const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
+        const half2_t h = {static_cast<_Float16>(bf16_to_f32(b0) * pre), static_cast<_Float16>(bf16_to_f32(b1) * pre)};
+        o[q] = __builtin_bit_cast(uint32_t, h);
+    }
 }
 
 struct Int4Consts {
@@ -303,6 +350,7 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     };
 
     const int KC = P.kc;
+    const int KCmax = b.kc_max;  // the largest problem's stage: xpost follows it
     const int nchunks = static_cast<int>(K / CK);
     const int cps = KC / CK;  // chunks per LDS stage
 
@@ -328,21 +376,24 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
             }
         }
     };
+    // Each (row m, chunk) is scaled by its own power of two (x_scale_of); its post factor goes
+    // to xpost[chunk][m], M4 = M rounded up to 4 slots per chunk.  The CK / 8 runs of a chunk
+    // are consecutive iterations, so aligned groups of CK / 8 lanes hold one chunk.
+    const int M4 = (M + 3) & ~3;
+    float *const xpost = reinterpret_cast<float *>(xs + M * KCmax);
     auto stage_convert = [&](int cs_, int ce_) {
-        const int runs = M * (ce_ - cs_) * CK / 8;
+        const int kc = (ce_ - cs_) * CK;
+        const int runs = M * kc / 8;
         for (int it = tid; it < runs; it += kThreads) {
             const uint4 raw = *reinterpret_cast<const uint4 *>(xs + it * 8);
             const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+            float pre, post;
+            x_scale_of(lane_group_max<CK / 8>(bf16x8_emax(wv)), pre, post);
             uint32_t o[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int s0 = perm_src(FMT, 2 * q), s1 = perm_src(FMT, 2 * q + 1);
-                const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
-                const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
-                half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
-                o[q] = as_u(h);
-            }
+            bf16x8_to_f16_perm(FMT, wv, pre, o);
             *reinterpret_cast<uint4 *>(xs + it * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+            const int e = it * 8, m = e / kc, c = (e - m * kc) / CK;
+            if ((it & (CK / 8 - 1)) == 0) xpost[c * M4 + m] = post;
         }
     };
 
@@ -375,12 +426,22 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     const int xr = lr < M ? lr : 0;
     const Int4Consts i4k = int4_consts();
 
+    // the post factors of this lane's output rows m = 4 part + q (rows >= M read row 0's)
+    const int mi = part * 4 < M ? part * 4 : 0;
+    auto post_of = [&](int c, int cs) -> floatx4 {
+        if constexpr (ONE) {
+            return floatx4{xpost[(c - cs) * M4], 0.f, 0.f, 0.f};
+        } else {
+            return *reinterpret_cast<const floatx4 *>(xpost + (c - cs) * M4 + mi);
+        }
+    };
     auto process = [&](const Unit &u, int cb, int cs, int ce) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const int c = cb + j;
             if (c >= ce) break;
             const _Float16 *xa = xs + xr * ((ce - cs) * CK) + (c - cs) * CK + part * (CK / 4);
+            const floatx4 post = post_of(c, cs);
             if constexpr (FMT == FMT_INT4) {
                 floatx4 pacc[R];
                 uint32_t zc1024[R], zc64[R];
@@ -408,14 +469,17 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
                 for (int r = 0; r < R; ++r)
                 {
                     const float sc = f16_to_f32(static_cast<uint16_t>(u.sv[r][j >> 1] >> (16 * (j & 1))));
-                    if constexpr (ONE) acc[r][0] += pacc[r][0] * sc;
-                    else acc[r] += pacc[r] * sc;
+                    if constexpr (ONE) acc[r][0] += (pacc[r][0] * sc) * post[0];
+                    else acc[r] += (pacc[r] * sc) * post;
                 }
             } else if constexpr (is_gguf(FMT)) {
                 // one MFMA per block (the four parts of a row hold elements 8p..8p+7 of each
                 // block of the chunk), scaled in f32 by the block's d
                 constexpr int BPC = gguf_bpc(FMT);
                 const _Float16 *xg = xs + xr * ((ce - cs) * CK) + (c - cs) * CK + 8 * part;
+                floatx4 cacc[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) cacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int q = 0; q < BPC; ++q) {
                     const half8_t aop = *reinterpret_cast<const half8_t *>(xg + 32 * q);
@@ -434,9 +498,14 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
                         }
                         const uint32_t sw = FMT == FMT_Q4_0 ? u.sv[r][2 * j + (q >> 1)] : u.sv[r][j];
                         const float d = f16_to_f32(static_cast<uint16_t>(sw >> (16 * (q & 1))));
-                        if constexpr (ONE) acc[r][0] += pb[0] * d;
-                        else acc[r] += pb * d;
+                        if constexpr (ONE) cacc[r][0] += pb[0] * d;
+                        else cacc[r] += pb * d;
                     }
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if constexpr (ONE) acc[r][0] += cacc[r][0] * post[0];
+                    else acc[r] += cacc[r] * post;
                 }
             } else if constexpr (FMT == FMT_NF4) {
                 floatx4 pacc[R];
@@ -456,10 +525,14 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
                 }
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    if constexpr (ONE) acc[r][0] += pacc[r][0] * __builtin_bit_cast(float, u.sv[r][j]);
-                    else acc[r] += pacc[r] * __builtin_bit_cast(float, u.sv[r][j]);
+                    const float am = __builtin_bit_cast(float, u.sv[r][j]);
+                    if constexpr (ONE) acc[r][0] += (pacc[r][0] * am) * post[0];
+                    else acc[r] += (pacc[r] * am) * post;
                 }
             } else {
+                floatx4 pacc[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) pacc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int t = 0; t < WPL / 2; ++t) {
                     const half8_t aop = *reinterpret_cast<const half8_t *>(xa + t * 8);
@@ -468,9 +541,14 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
                         uint32_t h0[2], h1[2];
                         int8_word_to_h(u.wq[j][r][2 * t], h0);
                         int8_word_to_h(u.wq[j][r][2 * t + 1], h1);
-                        acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]),
-                                                                       acc[r], 0, 0, 0);
+                        pacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]),
+                                                                        pacc[r], 0, 0, 0);
                     }
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    if constexpr (ONE) acc[r][0] += pacc[r][0] * post[0];
+                    else acc[r] += pacc[r] * post;
                 }
             }
         }
@@ -578,7 +656,9 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 template <int FMT, int LW>
 __global__ __launch_bounds__(kThreads)
 #if CFH_GEMV_SPLIT_WPE
-__attribute__((amdgpu_waves_per_eu(CFH_GEMV_SPLIT_WPE)))
+// (INT4 with 16-byte lanes decodes four words per chunk to exact (q - z): 4 waves per SIMD
+// give it the registers to do so without spilling)
+__attribute__((amdgpu_waves_per_eu(FMT == FMT_INT4 && LW == 16 ? 4 : CFH_GEMV_SPLIT_WPE)))
 #endif
 void skinny_m1_split_kernel(Batch b) {
     constexpr int WPL = LW / 4;
@@ -587,9 +667,6 @@ void skinny_m1_split_kernel(Batch b) {
     constexpr int NB = CFH_GEMV_NB_SPLIT;
     constexpr int D = kSplitDepth;
     constexpr uint32_t kOob = 0x80000000u;  // past every descriptor's range: reads zero, no traffic
-    // INT4 with at least two code words per lane and chunk: the zero point is folded out of
-    // the per-code decode (below); with one word (group 32) the exact per-code decode is used
-    constexpr bool kFold = FMT == FMT_INT4 && WPL >= 2;
     extern __shared__ __align__(16) uint8_t lds[];  // [kWaves][region]: x slice, scales, zero points
     __shared__ float red[kWaves][64];
     __shared__ uint2 lut[FMT == FMT_NF4 ? kWaves * 256 : 1];  // NF4: one table per wave
@@ -625,7 +702,7 @@ void skinny_m1_split_kernel(Batch b) {
     _Float16 *const xw = reinterpret_cast<_Float16 *>(reg);
     const uint8_t *const ms = reg + P.soff;  // scale (INT4) / absmax (NF4) pieces
     const uint8_t *const mz = reg + P.zoff;  // zero-point pieces (INT4)
-    float2 *const xsum = reinterpret_cast<float2 *>(reg + P.xsoff);  // INT4: per chunk (T, X), see below
+    float *const xpost = reinterpret_cast<float *>(reg + P.xsoff);  // per chunk of the slice
     uint2 *const wl = lut + (FMT == FMT_NF4 ? wave * 256 : 0);
 
     // NF4 decode table (hi, lo f16 pairs of two codes), written before any copy into LDS is
@@ -706,53 +783,19 @@ void skinny_m1_split_kernel(Batch b) {
         __builtin_amdgcn_sched_barrier(0);  // unit by unit, in the order they are consumed
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(D * NB));  // the copies into LDS have landed
-    if constexpr (kFold) {
-        // Groups of 16 x values (the codes of two words) become f16 in the order the INT4
-        // decode below produces: the low nibbles of each byte (codes 0, 4, 2, 6 of each word)
-        // of both words, then the high nibbles (1, 5, 3, 7).  Per chunk, X = sum of its x and
-        // T = 1024 * (sum over low-nibble positions) + 64 * (sum over high-nibble positions),
-        // in f32 of the f16 values; the lanes of a chunk (one per group) reduce them.
-        constexpr int kSrc[16] = {0, 4, 2, 6, 8, 12, 10, 14, 1, 5, 3, 7, 9, 13, 11, 15};
-        constexpr int GPC = CK / 16;  // groups per chunk
-        const int groups = (c_hi > c_lo ? c_hi - c_lo : 0) * CK / 16;
-        for (int it = lane; it < groups; it += 64) {
-            const uint4 r0 = *reinterpret_cast<const uint4 *>(xw + it * 16);
-            const uint4 r1 = *reinterpret_cast<const uint4 *>(xw + it * 16 + 8);
-            const uint32_t wv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-            uint32_t o[8];
-            float slo = 0.0f, shi = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int s0 = kSrc[2 * q], s1 = kSrc[2 * q + 1];
-                const _Float16 h0 = static_cast<_Float16>(bf16_to_f32(static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)))));
-                const _Float16 h1 = static_cast<_Float16>(bf16_to_f32(static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)))));
-                const float f = static_cast<float>(h0) + static_cast<float>(h1);
-                if (q < 4) slo += f;
-                else shi += f;
-                half2_t h = {h0, h1};
-                o[q] = as_u(h);
-            }
-            *reinterpret_cast<uint4 *>(xw + it * 16) = make_uint4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<uint4 *>(xw + it * 16 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-            slo = lane_group_sum<GPC>(slo);
-            shi = lane_group_sum<GPC>(shi);
-            if (it % GPC == 0) xsum[it / GPC] = make_float2(1024.0f * slo + 64.0f * shi, slo + shi);
-        }
-    } else {
+    {
+        // x slice -> f16 in the extraction order, each chunk scaled by its own power of two
+        // (x_scale_of); the CK / 8 runs of a chunk sit on CK / 8 consecutive lanes
         const int runs = (c_hi > c_lo ? c_hi - c_lo : 0) * CK / 8;
         for (int it = lane; it < runs; it += 64) {
             const uint4 raw = *reinterpret_cast<const uint4 *>(xw + it * 8);
             const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+            float pre, post;
+            x_scale_of(lane_group_max<CK / 8>(bf16x8_emax(wv)), pre, post);
             uint32_t o[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int s0 = perm_src(FMT, 2 * q), s1 = perm_src(FMT, 2 * q + 1);
-                const uint16_t b0 = static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)));
-                const uint16_t b1 = static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)));
-                half2_t h = {static_cast<_Float16>(bf16_to_f32(b0)), static_cast<_Float16>(bf16_to_f32(b1))};
-                o[q] = as_u(h);
-            }
+            bf16x8_to_f16_perm(FMT, wv, pre, o);
             *reinterpret_cast<uint4 *>(xw + it * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+            if ((it & (CK / 8 - 1)) == 0) xpost[it / (CK / 8)] = post;
         }
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));  // this wave's LDS writes are done
@@ -760,8 +803,8 @@ void skinny_m1_split_kernel(Batch b) {
     const Int4Consts i4k = int4_consts();
     float acc = 0.0f;  // slot 0 of the 16x16 MFMA tile: row lr of this tile (lanes with part 0)
     // A chunk past K (the last unit may be partial) or of a unit past the wave's range reads
-    // zero codes, takes its x and metadata from the wave's first chunk (finite) and is scaled
-    // by 0: no branch, so no path leaves a unit's registers unread.
+    // zero codes and takes its x and metadata from the wave's first chunk; its sum is dropped
+    // by a select (no branch, so no path leaves a unit's registers unread).
     auto process = [&](const Unit &u, int k) {
         const int cb = (u0 + k) * NB;
 #pragma unroll
@@ -769,34 +812,9 @@ void skinny_m1_split_kernel(Batch b) {
             const bool live = k < U && cb + j < nchunks;
             const int c = live ? cb + j : c_lo;
             const _Float16 *xa = xw + (c - c_lo) * CK + part * (CK / 4);
+            const float post = xpost[c - c_lo];
             floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (kFold) {
-                // Codes decode to 1024 + q (low nibbles) and 1024 + 16 q (high nibbles) by one
-                // AND-OR each; the two MFMA chains give sum x (1024 + q) and sum x (1024 + 16 q),
-                // and sum x (q - z) = lo + hi / 16 - T - z X with the chunk's x sums.
-                const uint32_t zw = *reinterpret_cast<const uint32_t *>(
-                    mz + meta_lds_off(static_cast<uint32_t>(c >> 3) * 4u - z_lo, lr));
-                const float z = static_cast<float>((zw >> (4 * (static_cast<uint32_t>(c) & 7u))) & 15u);
-                floatx4 plo = floatx4{0.f, 0.f, 0.f, 0.f}, phi = plo;
-#pragma unroll
-                for (int q = 0; q < WPL / 2; ++q) {
-                    const uint32_t wa = u.wq[j][2 * q], wb = u.wq[j][2 * q + 1];
-                    const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
-                    // masks and magic in VGPRs: each AND-OR is then one v_and_or_b32
-                    const uint32_t LO = i4k.lo_mask, HI = i4k.hi_mask, MG = i4k.magic;
-                    const half8_t alo = *reinterpret_cast<const half8_t *>(xa + q * 16);
-                    const half8_t ahi = *reinterpret_cast<const half8_t *>(xa + q * 16 + 8);
-                    plo = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        alo, pack8((wa & LO) | MG, (wa8 & LO) | MG, (wb & LO) | MG, (wb8 & LO) | MG), plo, 0, 0, 0);
-                    phi = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        ahi, pack8((wa & HI) | MG, (wa8 & HI) | MG, (wb & HI) | MG, (wb8 & HI) | MG), phi, 0, 0, 0);
-                }
-                const float2 tx = xsum[c - c_lo];
-                const float r = fmaf(phi[0], 0.0625f, plo[0]) - fmaf(z, tx.y, tx.x);
-                const float sc = f16_to_f32(*reinterpret_cast<const uint16_t *>(
-                    ms + meta_lds_off(static_cast<uint32_t>(c) * 2u - s_lo, lr)));
-                acc += r * (live ? sc : 0.0f);
-            } else if constexpr (FMT == FMT_INT4) {  // one word per lane: exact (q - z) codes
+            if constexpr (FMT == FMT_INT4) {  // exact (q - z) codes
                 const uint32_t zw = *reinterpret_cast<const uint32_t *>(
                     mz + meta_lds_off(static_cast<uint32_t>(c >> 3) * 4u - z_lo, lr));
                 const uint32_t z = (zw >> (4 * (static_cast<uint32_t>(c) & 7u))) & 15u;
@@ -810,7 +828,8 @@ void skinny_m1_split_kernel(Batch b) {
                 }
                 const float sc = f16_to_f32(*reinterpret_cast<const uint16_t *>(
                     ms + meta_lds_off(static_cast<uint32_t>(c) * 2u - s_lo, lr)));
-                acc += pacc[0] * (live ? sc : 0.0f);
+                const float v = (pacc[0] * sc) * post;
+                acc += live ? v : 0.0f;
             } else if constexpr (FMT == FMT_NF4) {
 #pragma unroll
                 for (int q = 0; q < WPL; ++q) {
@@ -823,7 +842,8 @@ void skinny_m1_split_kernel(Batch b) {
                 }
                 const float am = *reinterpret_cast<const float *>(
                     ms + meta_lds_off(static_cast<uint32_t>(c >> gshift) * 4u - s_lo, lr));
-                acc += pacc[0] * (live ? am : 0.0f);
+                const float v = (pacc[0] * am) * post;
+                acc += live ? v : 0.0f;
             } else if constexpr (is_gguf(FMT)) {
                 // One MFMA per 32-element block: the four parts of a row hold elements 8p..8p+7
                 // of each block of the chunk, so the MFMA's K sum is that block's exact-code dot
@@ -839,6 +859,7 @@ void skinny_m1_split_kernel(Batch b) {
                     sv[0] = *reinterpret_cast<const uint32_t *>(sp);
                 }
                 const _Float16 *xc = xw + (c - c_lo) * CK + 8 * part;
+                float cs = 0.0f;
 #pragma unroll
                 for (int q = 0; q < BPC; ++q) {
                     const half8_t aop = *reinterpret_cast<const half8_t *>(xc + 32 * q);
@@ -854,8 +875,10 @@ void skinny_m1_split_kernel(Batch b) {
                         pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]), pb, 0, 0, 0);
                     }
                     const float d = f16_to_f32(static_cast<uint16_t>(sv[q >> 1] >> (16 * (q & 1))));
-                    acc += pb[0] * (live ? d : 0.0f);
+                    cs += pb[0] * d;
                 }
+                const float v = cs * post;
+                acc += live ? v : 0.0f;
             } else {
 #pragma unroll
                 for (int q = 0; q < WPL / 2; ++q) {
@@ -865,7 +888,8 @@ void skinny_m1_split_kernel(Batch b) {
                     int8_word_to_h(u.wq[j][2 * q + 1], h1);
                     pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(aop, pack8(h0[0], h0[1], h1[0], h1[1]), pacc, 0, 0, 0);
                 }
-                acc += live ? pacc[0] : 0.0f;
+                const float v = pacc[0] * post;
+                acc += live ? v : 0.0f;
             }
         }
     };
@@ -986,7 +1010,7 @@ int64_t split_region(int fmt, int lw, Problem &p) {
     const int64_t nunits = (p.k / ck + CFH_GEMV_NB_SPLIT - 1) / CFH_GEMV_NB_SPLIT;
     const int64_t cw = (nunits + kWaves - 1) / kWaves * CFH_GEMV_NB_SPLIT;  // chunks per wave, at most
     const int64_t xbytes = (cw * ck * 2 + 255) / 256 * 256;
-    const int64_t tbytes = fmt == FMT_INT4 && lw >= 8 ? (cw * 8 + 255) / 256 * 256 : 0;  // x sums
+    const int64_t tbytes = (cw * 4 + 255) / 256 * 256;  // activation post factor per chunk
     int64_t sbytes = 0, zbytes = 0;
     if (fmt == FMT_INT4) {
         sbytes = 1024 * copies(2 * cw + 14);
@@ -1020,7 +1044,11 @@ bool skinny_ok(int fmt, const Problem &p, int64_t m) {
     return aligned(p.x, 16) && aligned(p.codes, 16);
 }
 
-// K elements staged per LDS pass: a whole number of units (unit = nb chunks of ck elements)
+// Bytes of the per-(chunk, row) activation post factors that follow a stage of kc elements.
+int64_t xpost_bytes(int64_t kc, int64_t m, int ck) { return kc / ck * ((m + 3) / 4 * 4) * 4; }
+
+// K elements staged per LDS pass: a whole number of units (unit = nb chunks of ck elements);
+// the stage (m rows of kc f16) fills kLdsBytesMax, its post factors come on top
 int32_t kc_for(int64_t k, int64_t m, int ck, int nb) {
     const int64_t unit = static_cast<int64_t>(ck) * nb;
     int64_t kc = (kLdsBytesMax / 2) / m;
@@ -1101,17 +1129,19 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
     // longest K first: its workgroups run longest, so they start first
     std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
     Batch b{};
-    int64_t tiles = 0, max_lds = 0;
+    int64_t tiles = 0, kc_max = 0;
     for (int i = 0; i < count; ++i) {
         require(lw_for(fmt, ps[i].group) == lw, "batched problems must share the group size class");
         b.p[i] = ps[i];
         b.p[i].tile_begin = static_cast<int32_t>(tiles);
         b.p[i].kc = kc_for(ps[i].k, m, ck, R == 4 ? 2 : CFH_GEMV_NB_SMALL);
         tiles += (ps[i].n + 16 * R - 1) / (16 * R);
-        const int64_t lds = m * b.p[i].kc * 2;
-        if (lds > max_lds) max_lds = lds;
+        kc_max = std::max<int64_t>(kc_max, b.p[i].kc);
     }
     require(tiles <= 0x7fffffff, "too many rows for one launch");
+    // the stage of the largest problem, then its post factors
+    const int64_t max_lds = m * kc_max * 2 + xpost_bytes(kc_max, m, ck);
+    b.kc_max = static_cast<int32_t>(kc_max);
     b.count = count;
     b.m = static_cast<int32_t>(m);
     b.y_bf16 = y_bf16;
