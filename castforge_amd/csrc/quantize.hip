@@ -877,8 +877,10 @@ void quantize_int8_rows(const float *src, int64_t rows, int64_t cols, SymEnc e, 
 // each group is quantized by as few launches as possible (at most kQSets matrices, and for
 // INT4 at most 65535 rows, per launch).  A matrix the batched kernels cannot take (alignment,
 // row length, group size) is quantized on its own by the single-matrix path.
-void quantize_batched(const cfh_quant_problem_t *ps, int32_t count, bool int4, int64_t group,
-                      SymEnc e, hipStream_t st) {
+// in_scales (INT4 only, may be NULL): per problem, the AWQ per-column pre-scale (device f32
+// [cols], 16-byte aligned) fused into the pass as in castforge_hip_quantize_int4g_awq.
+void quantize_batched(const cfh_quant_problem_t *ps, const float *const *in_scales, int32_t count,
+                      bool int4, int64_t group, SymEnc e, hipStream_t st) {
     require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
     require(count == 0 || ps != nullptr, "problems must not be NULL");
     if (int4) require(pow2_in(group, 8, 256), "group must be a power of two in [8, 256]");
@@ -889,6 +891,9 @@ void quantize_batched(const cfh_quant_problem_t *ps, int32_t count, bool int4, i
         if (int4) {
             require(q.cols % 8 == 0, "cols must be a multiple of 8 (8 codes per 32-bit word)");
             require(q.rows == 0 || q.cols == 0 || q.zeros, "zeros must not be NULL");
+            if (in_scales && q.rows > 0 && q.cols > 0)
+                require(in_scales[i] != nullptr && aligned(in_scales[i], 16),
+                        "in_scale must be a non-NULL 16-byte aligned device pointer");
         } else {
             require(q.rows == 0 || q.scales, "scales must not be NULL");
         }
@@ -915,8 +920,9 @@ void quantize_batched(const cfh_quant_problem_t *ps, int32_t count, bool int4, i
                 const bool ok = group >= 16 && CFH_INT4Q16 && q.rows <= 65535 && cols < (int64_t{1} << 31) &&
                                 aligned(q.src, 16) && aligned(q.codes, 4) && aligned(q.scales, 2) && aligned(q.zeros, 4);
                 if (!ok) {
-                    quantize_int4g_impl(q.src, nullptr, q.rows, cols, group, static_cast<uint32_t *>(q.codes),
-                                        static_cast<uint16_t *>(q.scales), q.zeros, st);
+                    quantize_int4g_impl(q.src, in_scales ? in_scales[j] : nullptr, q.rows, cols, group,
+                                        static_cast<uint32_t *>(q.codes), static_cast<uint16_t *>(q.scales),
+                                        q.zeros, st);
                     continue;
                 }
                 if (rows + q.rows > 65535) flush();
@@ -933,7 +939,7 @@ void quantize_batched(const cfh_quant_problem_t *ps, int32_t count, bool int4, i
             }
             if (sets.count == kQSets) flush();
             sets.src[sets.count] = q.src;
-            sets.in_scale[sets.count] = nullptr;
+            sets.in_scale[sets.count] = int4 && in_scales ? in_scales[j] : nullptr;
             sets.codes[sets.count] = q.codes;
             sets.scales[sets.count] = q.scales;
             sets.zeros[sets.count] = q.zeros;
@@ -1096,7 +1102,15 @@ extern "C" {
 int32_t castforge_hip_quantize_int4g_batched(const cfh_quant_problem_t *problems, int32_t count,
                                              int64_t group, void *stream, char **out_error) {
     return guarded(out_error, [&] {
-        quantize_batched(problems, count, true, group, SymEnc{}, static_cast<hipStream_t>(stream));
+        quantize_batched(problems, nullptr, count, true, group, SymEnc{}, static_cast<hipStream_t>(stream));
+    });
+}
+int32_t castforge_hip_quantize_int4g_awq_batched(const cfh_quant_problem_t *problems,
+                                                 const float *const *in_scales, int32_t count,
+                                                 int64_t group, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        require(count == 0 || in_scales != nullptr, "in_scales must not be NULL");
+        quantize_batched(problems, in_scales, count, true, group, SymEnc{}, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -1108,7 +1122,7 @@ int32_t castforge_hip_quantize_int8_batched(const cfh_quant_problem_t *problems,
                 "round_mode must be CFH_ROUND_HALF_AWAY or CFH_ROUND_HALF_EVEN");
         // formats.rs:654-660: bits == 4 -> [-8, 7], anything else -> [-128, 127]
         SymEnc e{bits == 4 ? -8.0f : -128.0f, bits == 4 ? 7.0f : 127.0f, round_mode};
-        quantize_batched(problems, count, false, 0, e, static_cast<hipStream_t>(stream));
+        quantize_batched(problems, nullptr, count, false, 0, e, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -120,6 +120,8 @@ SIGNATURES = {
     "castforge_hip_gemv_w4a16_planes_batched": (c_int32, [POINTER(W4A16Problem), c_int32, c_int64, c_int32, _P, _E]),
     "castforge_hip_gemv_nf4_batched": (c_int32, [POINTER(Nf4Problem), c_int32, c_int64, c_int32, _P, _E]),
     "castforge_hip_quantize_int4g_batched": (c_int32, [POINTER(QuantProblem), c_int32, c_int64, _P, _E]),
+    "castforge_hip_quantize_int4g_awq_batched": (c_int32, [POINTER(QuantProblem), POINTER(_P), c_int32, c_int64, _P,
+                                                           _E]),
     "castforge_hip_quantize_int8_batched": (c_int32, [POINTER(QuantProblem), c_int32, c_int32, c_int32, _P, _E]),
     "castforge_hip_gemm_fp8": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, c_int32, _P, _E]),
     "castforge_hip_gemm_fp8_exact": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, _P, c_int32, _P, _E]),

@@ -117,9 +117,20 @@ def _quant_batch(ws: list[torch.Tensor]) -> list[torch.Tensor]:
     return ws
 
 
-def quantize_int4g_batched(ws: list[torch.Tensor], group: int = 128) -> list[Int4Packed]:
-    """quantize_int4g over several matrices in one launch per column count (bit-identical)."""
+def quantize_int4g_batched(ws: list[torch.Tensor], group: int = 128,
+                           in_scales: list[torch.Tensor] | None = None) -> list[Int4Packed]:
+    """quantize_int4g over several matrices in one launch per column count (bit-identical);
+    with in_scales, the AWQ form (quantize_int4g(w, group, in_scale) per matrix)."""
     ws = _quant_batch(ws)
+    if in_scales is not None:
+        if len(in_scales) != len(ws):
+            raise ValueError("in_scales must hold one f32 [K] tensor per matrix")
+        in_scales = [_dev(s) for s in in_scales]
+        for s, w in zip(in_scales, ws):
+            if (s.dtype != torch.float32 or s.dim() != 1 or s.numel() != w.shape[1] or not s.is_contiguous()
+                    or s.device != w.device or s.data_ptr() % 16):
+                raise ValueError("each in_scale must be a contiguous 16-byte aligned float32 [K] on the "
+                                 "weight's device")
     out, arr = [], (ffi.QuantProblem * max(1, len(ws)))()
     for i, w in enumerate(ws):
         n, k = w.shape
@@ -129,7 +140,10 @@ def quantize_int4g_batched(ws: list[torch.Tensor], group: int = 128) -> list[Int
         zeros = torch.empty((n, (g + 7) // 8), dtype=torch.int32, device=w.device)
         arr[i] = ffi.QuantProblem(_ptr(w), n, k, _ptr(codes), _ptr(scales), _ptr(zeros))
         out.append(Int4Packed(codes, scales, zeros, n, k, group))
-    if ws:
+    if ws and in_scales is not None:
+        ptrs = (ctypes.c_void_p * len(ws))(*[s.data_ptr() for s in in_scales])
+        ffi.call("castforge_hip_quantize_int4g_awq_batched", arr, ptrs, len(ws), group, _stream(ws[0]))
+    elif ws:
         ffi.call("castforge_hip_quantize_int4g_batched", arr, len(ws), group, _stream(ws[0]))
     return out
 

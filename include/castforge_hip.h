@@ -173,6 +173,14 @@ typedef struct cfh_quant_problem_t {
 int32_t castforge_hip_quantize_int4g_batched(const cfh_quant_problem_t *problems, int32_t count,
                                              int64_t group, void *stream, char **out_error);
 
+/* castforge_hip_quantize_int4g_awq over up to CFH_MAX_BATCH matrices in as few launches as
+ * castforge_hip_quantize_int4g_batched: in_scales is a host array of `count` device pointers,
+ * in_scales[i] the f32 [cols] pre-scale of problem i (16-byte aligned).  New; no reference
+ * counterpart (BASELINE config 5's per-layer AWQ quantize). */
+int32_t castforge_hip_quantize_int4g_awq_batched(const cfh_quant_problem_t *problems,
+                                                 const float *const *in_scales, int32_t count,
+                                                 int64_t group, void *stream, char **out_error);
+
 int32_t castforge_hip_quantize_int8_batched(const cfh_quant_problem_t *problems, int32_t count,
                                             int32_t bits, int32_t round_mode, void *stream,
                                             char **out_error);

@@ -318,6 +318,26 @@ def test_int4g_batched_matches_single(cuda):
             assert np.array_equal(b.codes.cpu().numpy().view(np.uint32), codes)
 
 
+def test_int4g_awq_batched_matches_single_and_oracle(cuda):
+    """The batched AWQ form (one launch per column count) equals castforge_hip_quantize_int4g_awq
+    per matrix bit for bit, and the oracle's quantization of f32(W * s); misaligned members take
+    the single-matrix path inside the same call."""
+    ws = _batch_inputs(cuda)
+    ss = [torch.from_numpy(synth.awq_channel_scales(31, i, w.shape[1])).to(cuda) for i, w in enumerate(ws)]
+    batched = ops.quantize_int4g_batched(ws, 128, ss)
+    for w, sc, b in zip(ws, ss, batched):
+        one = ops.quantize_int4g(w, 128, sc)
+        assert torch.equal(one.codes, b.codes) and torch.equal(one.zeros, b.zeros)
+        assert torch.equal(one.scales.view(torch.int16), b.scales.view(torch.int16))
+        if w.numel():
+            c_ref, s_ref, z_ref = O.quantize_int4g_awq(w.cpu().numpy(), sc.cpu().numpy(), 128)
+            assert np.array_equal(b.codes.cpu().numpy().view(np.uint32), c_ref)
+            assert np.array_equal(b.scales.cpu().numpy().view(np.uint16), s_ref)
+            assert np.array_equal(b.zeros.cpu().numpy().view(np.uint32), z_ref)
+    with pytest.raises(ValueError, match="in_scale"):
+        ops.quantize_int4g_batched(ws[:1], 128, [ss[0][:-4]])
+
+
 @pytest.mark.parametrize("mode", ["half_away", "half_even"])
 def test_int8_batched_matches_single(cuda, mode):
     ws = _batch_inputs(cuda)
