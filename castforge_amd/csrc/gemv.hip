@@ -43,12 +43,26 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kLdsBytesMax = CFH_GEMV_LDS_MAX;  // activation stage per workgroup
 constexpr int kLdsBytesSplit = 65536;  // the M = 1 split-K kernel's x slices per workgroup
 constexpr int kMaxProblems = 8;
+constexpr uint32_t kOobGx = 0x80000000u;  // buffer offset past every range: reads 0, no traffic
 // rows-per-workgroup multiplier and chunks in flight per wave for M <= 4 (tuning knobs)
 #ifndef CFH_GEMV_R_SMALL
 #define CFH_GEMV_R_SMALL 1
 #endif
 #ifndef CFH_GEMV_NB_SMALL
 #define CFH_GEMV_NB_SMALL 4
+#endif
+// M = 2..16 (skinny_gx_kernel): rows per workgroup (16 R) by M, and chunks per unit
+#ifndef CFH_GX_R_SMALL
+#define CFH_GX_R_SMALL 2
+#endif
+#ifndef CFH_GX_R_MID
+#define CFH_GX_R_MID 2
+#endif
+#ifndef CFH_GX_R_BIG
+#define CFH_GX_R_BIG 4
+#endif
+#ifndef CFH_GX_NB
+#define CFH_GX_NB 2
 #endif
 // M = 1 decode uses the split-K kernel (0: the per-tile kernel, for comparison)
 #ifndef CFH_GEMV_SPLIT
@@ -607,6 +621,299 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     }
 }
 
+// ---- M = 2..16 with x from global memory --------------------------------------------------
+// Each wave reads the activation fragments of its own chunks straight from global memory
+// (L2: x is a few KB per row) into registers, next to the weight codes of the same unit, and
+// converts them to f16 there: per (row, chunk) the power of two of x_scale_of, agreed on by
+// the four lanes that hold the row's chunk (xor 16, 32), the post factor of each output row
+// fetched from the lane that owns it.  No LDS staging of x, so no pass boundaries and no
+// barrier before the final cross-wave sum.  The conversion is shared by the R row tiles of
+// the unit; the weight decode and the per-chunk scale handling are those of
+// skinny_qgemm_kernel.  Measured (7-matrix block, INT4 g128): M = 2 / 4 / 8 / 16 in 40 / 42 /
+// 46 / 52 us, against 57 / 76 us at M = 8 / 16 for the LDS-staged kernel; the limit is the
+// VALU work of the x conversion (probe builds without any x or metadata loads run as fast).
+// Two waves per SIMD: measured faster than one wave with spill-free registers at R = 4 (52 vs
+// 57 us per block at M = 16); the conversion of x is the VALU cost that the second wave hides.
+template <int FMT, int LW, int R, int NB>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void skinny_gx_kernel(Batch b) {
+    constexpr int WPL = LW / 4;
+    constexpr int CPB = codes_per_byte<FMT>();
+    constexpr int CK = 4 * LW * CPB;   // K elements per chunk
+    constexpr int XV = CK / 32;        // 16-byte x loads per lane per chunk
+    __shared__ floatx4 red[kWaves - 1][R][64];
+    __shared__ uint2 lut[FMT == FMT_NF4 ? 256 : 1];
+
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxProblems; ++i)
+        if (i < b.count && static_cast<int>(blockIdx.x) >= b.p[i].tile_begin) pi = i;
+    const Problem &P = b.p[pi];
+    const int M = b.m;
+    const int64_t N = P.n, K = P.k;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x - P.tile_begin) * 16 * R;
+    const int rows_here = static_cast<int>((N - n0) < 16 * R ? (N - n0) : 16 * R);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, part = lane >> 4;
+    const uint32_t row_bytes = static_cast<uint32_t>(K / CPB);
+    const rsrc_t rc = make_rsrc(static_cast<const uint8_t *>(P.codes) + n0 * row_bytes,
+                                static_cast<uint32_t>(rows_here) * row_bytes);
+    const int64_t grp = FMT == FMT_INT8 ? CK : P.group;
+    const uint32_t G = static_cast<uint32_t>((K + grp - 1) / grp);
+    const uint32_t ZW = (G + 7) / 8, GP = ZW * 8;
+    const int gshift = is_gguf(FMT) ? 0 : __builtin_ctz(static_cast<uint32_t>(grp / CK));
+    rsrc_t rs = make_rsrc(P.codes, 0), rz = rs;
+    if constexpr (FMT == FMT_INT4 || is_gguf(FMT))
+        rs = make_rsrc(static_cast<const uint16_t *>(P.scales) + n0 * GP, static_cast<uint32_t>(rows_here) * GP * 2);
+    if constexpr (FMT == FMT_INT4) {
+        rz = make_rsrc(P.zeros + n0 * ZW, static_cast<uint32_t>(rows_here) * ZW * 4);
+    } else if constexpr (FMT == FMT_NF4) {
+        rs = make_rsrc(static_cast<const float *>(P.scales) + n0 * G, static_cast<uint32_t>(rows_here) * G * 4);
+    }
+    // x [M, K] bf16: this lane's row lr (rows >= M read zero) and its part of each chunk
+    // (GGUF: elements 8 part .. + 7 of each 32-block; others: a contiguous quarter)
+    const rsrc_t rx = make_rsrc(P.x, static_cast<uint32_t>(M * K * 2));
+    const uint32_t x_off = lr < M ? static_cast<uint32_t>(lr * K + (is_gguf(FMT) ? 8 * part : part * (CK / 4))) * 2u
+                                  : kOobGx;
+    uint32_t code_off[R], sc_off[R], z_off[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = 16 * r + lr;
+        code_off[r] = row * row_bytes + part * LW;
+        sc_off[r] = row * ((FMT == FMT_INT4 || is_gguf(FMT)) ? GP : G);
+        z_off[r] = row * ZW;
+    }
+
+    const int nchunks = static_cast<int>(K / CK);
+    struct Unit {
+        uint32_t wq[NB][R][WPL];
+        uint32_t sv[R][FMT == FMT_Q4_0 ? 2 * NB : NB];
+        uint32_t zv[R];
+        uint4 xv[NB][XV];
+    };
+    // unit k of this wave: chunks c0 = (wave + k kWaves) NB .. + NB - 1; chunks past K read
+    // nothing (offsets past the descriptors), so every unit issues the same loads
+    auto load_unit = [&](Unit &u, int k) {
+        const int c0 = (wave + k * kWaves) * NB;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int c = c0 + j;
+            const bool in = c < nchunks;
+#pragma unroll
+            for (int h = 0; h < XV; ++h) {
+                const uint32_t xo = static_cast<uint32_t>(c * CK + (is_gguf(FMT) ? 32 * h : 8 * h)) * 2u;
+                u.xv[j][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           rx, in ? x_off + xo : kOobGx, 0, 0));
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                load_words<LW>(rc, in ? code_off[r] + static_cast<uint32_t>(c) * (CK / CPB) : kOobGx, u.wq[j][r]);
+                if constexpr (FMT == FMT_Q4_0) {
+                    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                                  rs, in ? (sc_off[r] + static_cast<uint32_t>(c) * 4u) * 2u : kOobGx, 0, 0));
+                    u.sv[r][2 * j] = v.x;
+                    u.sv[r][2 * j + 1] = v.y;
+                } else if constexpr (FMT == FMT_Q8_0) {
+                    u.sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(
+                        rs, in ? (sc_off[r] + static_cast<uint32_t>(c) * 2u) * 2u : kOobGx, 0, 0);
+                } else if constexpr (FMT == FMT_NF4) {
+                    u.sv[r][j] = __builtin_amdgcn_raw_buffer_load_b32(
+                        rs, in ? (sc_off[r] + (static_cast<uint32_t>(c) >> gshift)) * 4 : kOobGx, 0, 0);
+                }
+            }
+        }
+        if constexpr (FMT == FMT_INT4) {
+            // the unit's NB scales in one aligned load and its 8-group zero word (a unit past
+            // the end reads nothing)
+            const uint32_t um = c0 < nchunks ? 0u : kOobGx;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t so = ((sc_off[r] + static_cast<uint32_t>(c0)) * 2) | um;
+                if constexpr (NB == 4) {
+                    const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+                    u.sv[r][0] = v.x;
+                    u.sv[r][1] = v.y;
+                } else {
+                    static_assert(NB == 2, "INT4 units hold 2 or 4 chunks");
+                    u.sv[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
+                }
+                u.zv[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, ((z_off[r] + (static_cast<uint32_t>(c0) >> 3)) * 4) | um,
+                                                               0, 0);
+            }
+        }
+    };
+
+    // units of this wave (the same count for every path through the loop below)
+    const int U = __builtin_amdgcn_readfirstlane((nchunks + kWaves * NB - 1) / (kWaves * NB));
+    Unit ua, ub;
+    load_unit(ua, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FMT == FMT_NF4) {
+        for (int i = tid; i < 256; i += kThreads) {
+            const _Float16 h0 = static_cast<_Float16>(kNf4[i & 15]), h1 = static_cast<_Float16>(kNf4[i >> 4]);
+            const _Float16 l0 = static_cast<_Float16>(kNf4[i & 15] - static_cast<float>(h0));
+            const _Float16 l1 = static_cast<_Float16>(kNf4[i >> 4] - static_cast<float>(h1));
+            half2_t hi = {h0, h1}, lo = {l0, l1};
+            lut[i] = make_uint2(as_u(hi), as_u(lo));
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));  // the table's LDS writes
+        __builtin_amdgcn_s_barrier();
+    }
+
+    floatx4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const Int4Consts i4k = int4_consts();
+
+    // a chunk past K read zero codes, zero x and zero metadata; its sums are dropped by a select
+    auto process = [&](const Unit &u, int k) {
+        const int cb = (wave + k * kWaves) * NB;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int c = cb + j;
+            const bool live = c < nchunks;
+            // x of this chunk: f16, scaled by the row's power of two for the chunk
+            half8_t a[XV];
+            floatx4 post;
+            {
+                uint32_t e = 0;
+#pragma unroll
+                for (int h = 0; h < XV; ++h) {
+                    const uint32_t wv[4] = {u.xv[j][h].x, u.xv[j][h].y, u.xv[j][h].z, u.xv[j][h].w};
+                    e = max(e, bf16x8_emax(wv));
+                }
+                e = max(e, static_cast<uint32_t>(__shfl_xor(static_cast<int>(e), 16)));
+                e = max(e, static_cast<uint32_t>(__shfl_xor(static_cast<int>(e), 32)));
+                float pre, pst;
+                x_scale_of(e, pre, pst);
+#pragma unroll
+                for (int h = 0; h < XV; ++h) {
+                    const uint32_t wv[4] = {u.xv[j][h].x, u.xv[j][h].y, u.xv[j][h].z, u.xv[j][h].w};
+                    uint32_t o[4];
+                    bf16x8_to_f16_perm(FMT, wv, pre, o);
+                    a[h] = pack8(o[0], o[1], o[2], o[3]);
+                }
+                // output row m = 4 part + q of this lane: its post factor sits in lane m
+#pragma unroll
+                for (int q = 0; q < 4; ++q) post[q] = __shfl(pst, 4 * part + q);
+            }
+            if constexpr (FMT == FMT_INT4) {
+                const uint32_t gsh = 4 * (static_cast<uint32_t>(c) & 7u);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t z = (u.zv[r] >> gsh) & 15u;
+                    const uint32_t zc1024 = (0xE400u + z) * 0x00010001u, zc64 = (0xD400u + (z << 4)) * 0x00010001u;
+                    floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 0; t < WPL; ++t) {
+                        uint32_t hb[4];
+                        int4_word_to_h(u.wq[j][r][t], as_h2(zc1024), as_h2(zc64), i4k, hb);
+                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(hb[0], hb[1], hb[2], hb[3]), pacc, 0, 0, 0);
+                    }
+                    const float sc = f16_to_f32(static_cast<uint16_t>(u.sv[r][j >> 1] >> (16 * (j & 1))));
+                    const floatx4 v = (pacc * sc) * post;
+                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+            } else if constexpr (is_gguf(FMT)) {
+                constexpr int BPC = gguf_bpc(FMT);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    floatx4 cacc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int q = 0; q < BPC; ++q) {
+                        floatx4 pb = floatx4{0.f, 0.f, 0.f, 0.f};
+                        if constexpr (FMT == FMT_Q4_0) {
+                            uint32_t hb[4];
+                            int4_word_to_h(u.wq[j][r][q], as_h2(0xE408E408u), as_h2(0xD480D480u), i4k, hb);  // -1032, -72
+                            pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], pack8(hb[0], hb[1], hb[2], hb[3]), pb, 0, 0, 0);
+                        } else {
+                            uint32_t h0[2], h1[2];
+                            int8_word_to_h(u.wq[j][r][2 * q], h0);
+                            int8_word_to_h(u.wq[j][r][2 * q + 1], h1);
+                            pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], pack8(h0[0], h0[1], h1[0], h1[1]), pb, 0, 0, 0);
+                        }
+                        const uint32_t sw = FMT == FMT_Q4_0 ? u.sv[r][2 * j + (q >> 1)] : u.sv[r][j];
+                        cacc += pb * f16_to_f32(static_cast<uint16_t>(sw >> (16 * (q & 1))));
+                    }
+                    const floatx4 v = cacc * post;
+                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+            } else if constexpr (FMT == FMT_NF4) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 0; t < WPL; ++t) {
+                        const uint32_t w = u.wq[j][r][t];
+                        const uint2 e0 = lut[w & 255u], e1 = lut[(w >> 8) & 255u];
+                        const uint2 e2 = lut[(w >> 16) & 255u], e3 = lut[w >> 24];
+                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(e0.x, e1.x, e2.x, e3.x), pacc, 0, 0, 0);
+                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(e0.y, e1.y, e2.y, e3.y), pacc, 0, 0, 0);
+                    }
+                    const floatx4 v = (pacc * __builtin_bit_cast(float, u.sv[r][j])) * post;
+                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int t = 0; t < WPL / 2; ++t) {
+                        uint32_t h0[2], h1[2];
+                        int8_word_to_h(u.wq[j][r][2 * t], h0);
+                        int8_word_to_h(u.wq[j][r][2 * t + 1], h1);
+                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(h0[0], h0[1], h1[0], h1[1]), pacc, 0, 0, 0);
+                    }
+                    const floatx4 v = pacc * post;
+                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    };
+
+    // unit k in ua, unit k + 1 in ub: one exit, no branch and no load under a branch in the
+    // body, so the compiler's vmcnt waits cover only the unit being consumed
+    for (int k = 0; k < U; k += 2) {
+        load_unit(ub, k + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        process(ua, k);
+        load_unit(ua, k + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        process(ub, k + 1);
+    }
+
+    // ---- reduce the 4 waves' partial tiles and store ----
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) red[wave - 1][r][lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int w = 0; w < kWaves - 1; ++w) acc[r] += red[w][r][lane];
+            const int64_t nrow = n0 + 16 * r + lr;
+            if (nrow >= N) continue;
+            if constexpr (FMT == FMT_INT8) {
+                const float *s = static_cast<const float *>(P.scales);
+                acc[r] *= P.scale_per_row ? s[nrow] : s[0];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = part * 4 + q;
+                if (m < M) {
+                    if (b.y_bf16)
+                        static_cast<uint16_t *>(P.y)[static_cast<int64_t>(m) * N + nrow] = f32_to_bf16_rne(acc[r][q]);
+                    else
+                        static_cast<float *>(P.y)[static_cast<int64_t>(m) * N + nrow] = acc[r][q];
+                }
+            }
+        }
+    }
+}
+
 // ---- M = 1 split-K kernel ------------------------------------------------------------------
 // Decode (M = 1): one workgroup per 16-row tile, each of its 4 waves owning a contiguous
 // quarter of K (whole units of NB chunks) and its own LDS region, so no wave waits for
@@ -1076,6 +1383,27 @@ void launch_lw(int lw, const Batch &b, int64_t tiles, int64_t lds, hipStream_t s
     }
 }
 
+template <int FMT, int LW, int R>
+void launch_gx(const Batch &b, int64_t tiles, hipStream_t st) {
+    skinny_gx_kernel<FMT, LW, R, CFH_GX_NB><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, st>>>(b);
+}
+
+template <int FMT, int R>
+void launch_gx_lw(int lw, const Batch &b, int64_t tiles, hipStream_t st) {
+    if (lw == 16) launch_gx<FMT, 16, R>(b, tiles, st);
+    else if constexpr (FMT != FMT_INT8 && !is_gguf(FMT)) {
+        if (lw == 8) launch_gx<FMT, 8, R>(b, tiles, st);
+        else launch_gx<FMT, 4, R>(b, tiles, st);
+    }
+}
+
+template <int FMT>
+void launch_gx_r(int r, int lw, const Batch &b, int64_t tiles, hipStream_t st) {
+    if (r == 1) launch_gx_lw<FMT, 1>(lw, b, tiles, st);
+    else if (r == 2) launch_gx_lw<FMT, 2>(lw, b, tiles, st);
+    else launch_gx_lw<FMT, 4>(lw, b, tiles, st);
+}
+
 template <int FMT, int LW>
 void launch_split(const Batch &b, int64_t tiles, int64_t lds, hipStream_t st) {
     skinny_m1_split_kernel<FMT, LW><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), static_cast<size_t>(lds), st>>>(b);
@@ -1126,6 +1454,31 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
     }
     // 16-row tiles up to M = 4, 32 rows up to M = 8, 64 rows beyond (x is shared by more rows)
     const int R = m <= 4 ? CFH_GEMV_R_SMALL : m <= 8 ? 2 : 4;
+    if (m >= 2) {
+        const int Rg = m <= 4 ? CFH_GX_R_SMALL : m <= 8 ? CFH_GX_R_MID : CFH_GX_R_BIG;
+        // x read per wave from global memory (skinny_gx_kernel)
+        std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
+        Batch b{};
+        int64_t tiles = 0;
+        for (int i = 0; i < count; ++i) {
+            require(lw_for(fmt, ps[i].group) == lw, "batched problems must share the group size class");
+            b.p[i] = ps[i];
+            b.p[i].tile_begin = static_cast<int32_t>(tiles);
+            tiles += (ps[i].n + 16 * Rg - 1) / (16 * Rg);
+        }
+        require(tiles <= 0x7fffffff, "too many rows for one launch");
+        if (tiles == 0) return;
+        b.count = count;
+        b.m = static_cast<int32_t>(m);
+        b.y_bf16 = y_bf16;
+        if (fmt == FMT_INT4) launch_gx_r<FMT_INT4>(Rg, lw, b, tiles, st);
+        else if (fmt == FMT_NF4) launch_gx_r<FMT_NF4>(Rg, lw, b, tiles, st);
+        else if (fmt == FMT_Q4_0) launch_gx_r<FMT_Q4_0>(Rg, lw, b, tiles, st);
+        else if (fmt == FMT_Q8_0) launch_gx_r<FMT_Q8_0>(Rg, lw, b, tiles, st);
+        else launch_gx_r<FMT_INT8>(Rg, lw, b, tiles, st);
+        check_launch("skinny_gx");
+        return;
+    }
     // longest K first: its workgroups run longest, so they start first
     std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
     Batch b{};
