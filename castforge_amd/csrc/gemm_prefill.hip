@@ -1,4 +1,4 @@
-// Prefill (M > 16) dequant-fused GEMM for packed INT4 / INT8 / NF4 / GGUF weights on gfx950 MFMA.
+// Prefill (M > 64) dequant-fused GEMM for packed INT4 / INT8 / NF4 / GGUF weights on gfx950 MFMA.
 //
 // Y[m, n] = sum_k x[m, k] * dequant(W)[n, k]: x bf16 [M, K]; W packed [N, K] (the packed_rhs
 // layout, passes/weights/fold.rs:549-554).  This is the evaluation of `castforge.fused_qmatmul`

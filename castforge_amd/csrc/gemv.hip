@@ -1,4 +1,4 @@
-// Dequant-fused GEMV / skinny GEMM (M <= 16) for packed INT4 / INT8 / NF4 weights, gfx950.
+// Dequant-fused GEMV / skinny GEMM (M <= 64) for packed INT4 / INT8 / NF4 / GGUF weights, gfx950.
 //
 // Replaces the evaluation of `castforge.fused_qmatmul` (eval.rs:1145-1179 with
 // eval_matmul_2d, eval.rs:1465-1507) and the one-thread-per-row HIP text the reference emits
@@ -12,14 +12,16 @@
 //     group / NF4 block per row and its scale multiplies the fp32 MFMA result (no rounding of
 //     the scale into the f16 operand);
 //   * v_mfma_f32_16x16x32_f16 with dequantized W rows as B and the activation rows as A; x is
-//     converted from bf16 to f16 in LDS, in the permuted order the nibble extraction produces,
+//     converted from bf16 to f16 in the permuted order the nibble extraction produces,
 //     each (row, chunk) scaled by an exact power of two that the chunk's f32 partial undoes, so
 //     any finite bf16 activation is accepted (x_scale_of);
 //   * M = 1 (skinny_m1_split_kernel): each wave owns a contiguous quarter of K, copies its
 //     groups' scales / zero points and its x slice into its own LDS region up front, and then
 //     streams codes only, decoded to exact (q - z) f16 operands;
-//   * M = 2..16 (skinny_qgemm_kernel): the waves interleave over K in units of NB chunks,
-//     double-buffered per wave, with exact (q - z) / q / NF4 hi+lo operands;
+//   * M = 2..64 (skinny_gx_kernel): the waves interleave over K in units of NB chunks,
+//     double-buffered per wave, each wave reading its chunks' x fragments from global memory
+//     and converting them itself; up to 4 x tiles of 16 rows share every decoded weight word;
+//     exact (q - z) / q / NF4 hi+lo operands;
 //   * problems with the longest K are dispatched first so no long workgroup forms a tail.
 #include <algorithm>
 
@@ -51,7 +53,7 @@ constexpr uint32_t kOobGx = 0x80000000u;  // buffer offset past every range: rea
 #ifndef CFH_GEMV_NB_SMALL
 #define CFH_GEMV_NB_SMALL 4
 #endif
-// M = 2..16 (skinny_gx_kernel): rows per workgroup (16 R) by M, and chunks per unit
+// M = 2..16 (skinny_gx_kernel with one x tile): rows per workgroup (16 R) by M, and chunks per unit
 #ifndef CFH_GX_R_SMALL
 #define CFH_GX_R_SMALL 2
 #endif
@@ -621,7 +623,7 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
     }
 }
 
-// ---- M = 2..16 with x from global memory --------------------------------------------------
+// ---- M = 2..64 with x from global memory --------------------------------------------------
 // Each wave reads the activation fragments of its own chunks straight from global memory
 // (L2: x is a few KB per row) into registers, next to the weight codes of the same unit, and
 // converts them to f16 there: per (row, chunk) the power of two of x_scale_of, agreed on by
@@ -634,13 +636,14 @@ __global__ __launch_bounds__(kThreads) void skinny_qgemm_kernel(Batch b) {
 // VALU work of the x conversion (probe builds without any x or metadata loads run as fast).
 // Two waves per SIMD: measured faster than one wave with spill-free registers at R = 4 (52 vs
 // 57 us per block at M = 16); the conversion of x is the VALU cost that the second wave hides.
-template <int FMT, int LW, int R, int NB>
+// MT: 16-row tiles of x (M <= 16 MT); each weight word is decoded once for all of them.
+template <int FMT, int LW, int R, int NB, int MT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void skinny_gx_kernel(Batch b) {
     constexpr int WPL = LW / 4;
     constexpr int CPB = codes_per_byte<FMT>();
     constexpr int CK = 4 * LW * CPB;   // K elements per chunk
     constexpr int XV = CK / 32;        // 16-byte x loads per lane per chunk
-    __shared__ floatx4 red[kWaves - 1][R][64];
+    __shared__ floatx4 red[kWaves - 1][R][MT][64];
     __shared__ uint2 lut[FMT == FMT_NF4 ? 256 : 1];
 
     int pi = 0;
@@ -671,11 +674,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     } else if constexpr (FMT == FMT_NF4) {
         rs = make_rsrc(static_cast<const float *>(P.scales) + n0 * G, static_cast<uint32_t>(rows_here) * G * 4);
     }
-    // x [M, K] bf16: this lane's row lr (rows >= M read zero) and its part of each chunk
-    // (GGUF: elements 8 part .. + 7 of each 32-block; others: a contiguous quarter)
+    // x [M, K] bf16: this lane's rows 16 mt + lr (rows >= M read zero) and its part of each
+    // chunk (GGUF: elements 8 part .. + 7 of each 32-block; others: a contiguous quarter)
     const rsrc_t rx = make_rsrc(P.x, static_cast<uint32_t>(M * K * 2));
-    const uint32_t x_off = lr < M ? static_cast<uint32_t>(lr * K + (is_gguf(FMT) ? 8 * part : part * (CK / 4))) * 2u
-                                  : kOobGx;
+    uint32_t x_off[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int row = 16 * mt + lr;
+        x_off[mt] = row < M ? static_cast<uint32_t>(row * K + (is_gguf(FMT) ? 8 * part : part * (CK / 4))) * 2u
+                            : kOobGx;
+    }
     uint32_t code_off[R], sc_off[R], z_off[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -690,7 +698,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         uint32_t wq[NB][R][WPL];
         uint32_t sv[R][FMT == FMT_Q4_0 ? 2 * NB : NB];
         uint32_t zv[R];
-        uint4 xv[NB][XV];
+        uint4 xv[NB][MT][XV];
     };
     // unit k of this wave: chunks c0 = (wave + k kWaves) NB .. + NB - 1; chunks past K read
     // nothing (offsets past the descriptors), so every unit issues the same loads
@@ -701,11 +709,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             const int c = c0 + j;
             const bool in = c < nchunks;
 #pragma unroll
-            for (int h = 0; h < XV; ++h) {
-                const uint32_t xo = static_cast<uint32_t>(c * CK + (is_gguf(FMT) ? 32 * h : 8 * h)) * 2u;
-                u.xv[j][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                           rx, in ? x_off + xo : kOobGx, 0, 0));
-            }
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int h = 0; h < XV; ++h) {
+                    const uint32_t xo = static_cast<uint32_t>(c * CK + (is_gguf(FMT) ? 32 * h : 8 * h)) * 2u;
+                    u.xv[j][mt][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                   rx, in ? x_off[mt] + xo : kOobGx, 0, 0));
+                }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 load_words<LW>(rc, in ? code_off[r] + static_cast<uint32_t>(c) * (CK / CPB) : kOobGx, u.wq[j][r]);
@@ -734,9 +744,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                     const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
                     u.sv[r][0] = v.x;
                     u.sv[r][1] = v.y;
-                } else {
-                    static_assert(NB == 2, "INT4 units hold 2 or 4 chunks");
+                } else if constexpr (NB == 2) {
                     u.sv[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
+                } else {
+                    static_assert(NB == 1, "INT4 units hold 1, 2 or 4 chunks");
+                    u.sv[r][0] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
                 }
                 u.zv[r] = __builtin_amdgcn_raw_buffer_load_b32(rz, ((z_off[r] + (static_cast<uint32_t>(c0) >> 3)) * 4) | um,
                                                                0, 0);
@@ -761,10 +773,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         __builtin_amdgcn_s_barrier();
     }
 
-    floatx4 acc[R];
+    floatx4 acc[R][MT];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[r][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
     const Int4Consts i4k = int4_consts();
+    const floatx4 zero4 = floatx4{0.f, 0.f, 0.f, 0.f};
 
     // a chunk past K read zero codes, zero x and zero metadata; its sums are dropped by a select
     auto process = [&](const Unit &u, int k) {
@@ -773,14 +788,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         for (int j = 0; j < NB; ++j) {
             const int c = cb + j;
             const bool live = c < nchunks;
-            // x of this chunk: f16, scaled by the row's power of two for the chunk
-            half8_t a[XV];
-            floatx4 post;
-            {
+            // x of this chunk, per x tile: f16 scaled by each row's power of two for the chunk,
+            // and the post factor of this lane's output rows 16 mt + 4 part + q (from lane 4 part + q)
+            half8_t a[MT][XV];
+            floatx4 post[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
                 uint32_t e = 0;
 #pragma unroll
                 for (int h = 0; h < XV; ++h) {
-                    const uint32_t wv[4] = {u.xv[j][h].x, u.xv[j][h].y, u.xv[j][h].z, u.xv[j][h].w};
+                    const uint32_t wv[4] = {u.xv[j][mt][h].x, u.xv[j][mt][h].y, u.xv[j][mt][h].z, u.xv[j][mt][h].w};
                     e = max(e, bf16x8_emax(wv));
                 }
                 e = max(e, static_cast<uint32_t>(__shfl_xor(static_cast<int>(e), 16)));
@@ -789,14 +806,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 x_scale_of(e, pre, pst);
 #pragma unroll
                 for (int h = 0; h < XV; ++h) {
-                    const uint32_t wv[4] = {u.xv[j][h].x, u.xv[j][h].y, u.xv[j][h].z, u.xv[j][h].w};
+                    const uint32_t wv[4] = {u.xv[j][mt][h].x, u.xv[j][mt][h].y, u.xv[j][mt][h].z, u.xv[j][mt][h].w};
                     uint32_t o[4];
                     bf16x8_to_f16_perm(FMT, wv, pre, o);
-                    a[h] = pack8(o[0], o[1], o[2], o[3]);
+                    a[mt][h] = pack8(o[0], o[1], o[2], o[3]);
                 }
-                // output row m = 4 part + q of this lane: its post factor sits in lane m
 #pragma unroll
-                for (int q = 0; q < 4; ++q) post[q] = __shfl(pst, 4 * part + q);
+                for (int q = 0; q < 4; ++q) post[mt][q] = __shfl(pst, 4 * part + q);
             }
             if constexpr (FMT == FMT_INT4) {
                 const uint32_t gsh = 4 * (static_cast<uint32_t>(c) & 7u);
@@ -804,69 +820,103 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                 for (int r = 0; r < R; ++r) {
                     const uint32_t z = (u.zv[r] >> gsh) & 15u;
                     const uint32_t zc1024 = (0xE400u + z) * 0x00010001u, zc64 = (0xD400u + (z << 4)) * 0x00010001u;
-                    floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
+                    floatx4 pacc[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) pacc[mt] = zero4;
 #pragma unroll
                     for (int t = 0; t < WPL; ++t) {
                         uint32_t hb[4];
                         int4_word_to_h(u.wq[j][r][t], as_h2(zc1024), as_h2(zc64), i4k, hb);
-                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(hb[0], hb[1], hb[2], hb[3]), pacc, 0, 0, 0);
+                        const half8_t bw = pack8(hb[0], hb[1], hb[2], hb[3]);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            pacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][t], bw, pacc[mt], 0, 0, 0);
                     }
                     const float sc = f16_to_f32(static_cast<uint16_t>(u.sv[r][j >> 1] >> (16 * (j & 1))));
-                    const floatx4 v = (pacc * sc) * post;
-                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const floatx4 v = (pacc[mt] * sc) * post[mt];
+                        acc[r][mt] += live ? v : zero4;
+                    }
                 }
             } else if constexpr (is_gguf(FMT)) {
                 constexpr int BPC = gguf_bpc(FMT);
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    floatx4 cacc = floatx4{0.f, 0.f, 0.f, 0.f};
+                    floatx4 cacc[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) cacc[mt] = zero4;
 #pragma unroll
                     for (int q = 0; q < BPC; ++q) {
-                        floatx4 pb = floatx4{0.f, 0.f, 0.f, 0.f};
+                        half8_t bw;
                         if constexpr (FMT == FMT_Q4_0) {
                             uint32_t hb[4];
                             int4_word_to_h(u.wq[j][r][q], as_h2(0xE408E408u), as_h2(0xD480D480u), i4k, hb);  // -1032, -72
-                            pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], pack8(hb[0], hb[1], hb[2], hb[3]), pb, 0, 0, 0);
+                            bw = pack8(hb[0], hb[1], hb[2], hb[3]);
                         } else {
                             uint32_t h0[2], h1[2];
                             int8_word_to_h(u.wq[j][r][2 * q], h0);
                             int8_word_to_h(u.wq[j][r][2 * q + 1], h1);
-                            pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[q], pack8(h0[0], h0[1], h1[0], h1[1]), pb, 0, 0, 0);
+                            bw = pack8(h0[0], h0[1], h1[0], h1[1]);
                         }
                         const uint32_t sw = FMT == FMT_Q4_0 ? u.sv[r][2 * j + (q >> 1)] : u.sv[r][j];
-                        cacc += pb * f16_to_f32(static_cast<uint16_t>(sw >> (16 * (q & 1))));
+                        const float d = f16_to_f32(static_cast<uint16_t>(sw >> (16 * (q & 1))));
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            cacc[mt] += __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][q], bw, zero4, 0, 0, 0) * d;
                     }
-                    const floatx4 v = cacc * post;
-                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const floatx4 v = cacc[mt] * post[mt];
+                        acc[r][mt] += live ? v : zero4;
+                    }
                 }
             } else if constexpr (FMT == FMT_NF4) {
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
+                    floatx4 pacc[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) pacc[mt] = zero4;
 #pragma unroll
                     for (int t = 0; t < WPL; ++t) {
                         const uint32_t w = u.wq[j][r][t];
                         const uint2 e0 = lut[w & 255u], e1 = lut[(w >> 8) & 255u];
                         const uint2 e2 = lut[(w >> 16) & 255u], e3 = lut[w >> 24];
-                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(e0.x, e1.x, e2.x, e3.x), pacc, 0, 0, 0);
-                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(e0.y, e1.y, e2.y, e3.y), pacc, 0, 0, 0);
+                        const half8_t bh = pack8(e0.x, e1.x, e2.x, e3.x), bl = pack8(e0.y, e1.y, e2.y, e3.y);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) {
+                            pacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][t], bh, pacc[mt], 0, 0, 0);
+                            pacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][t], bl, pacc[mt], 0, 0, 0);
+                        }
                     }
-                    const floatx4 v = (pacc * __builtin_bit_cast(float, u.sv[r][j])) * post;
-                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+                    const float am = __builtin_bit_cast(float, u.sv[r][j]);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const floatx4 v = (pacc[mt] * am) * post[mt];
+                        acc[r][mt] += live ? v : zero4;
+                    }
                 }
             } else {
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    floatx4 pacc = floatx4{0.f, 0.f, 0.f, 0.f};
+                    floatx4 pacc[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) pacc[mt] = zero4;
 #pragma unroll
                     for (int t = 0; t < WPL / 2; ++t) {
                         uint32_t h0[2], h1[2];
                         int8_word_to_h(u.wq[j][r][2 * t], h0);
                         int8_word_to_h(u.wq[j][r][2 * t + 1], h1);
-                        pacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t], pack8(h0[0], h0[1], h1[0], h1[1]), pacc, 0, 0, 0);
+                        const half8_t bw = pack8(h0[0], h0[1], h1[0], h1[1]);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            pacc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][t], bw, pacc[mt], 0, 0, 0);
                     }
-                    const floatx4 v = pacc * post;
-                    acc[r] += live ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const floatx4 v = pacc[mt] * post[mt];
+                        acc[r][mt] += live ? v : zero4;
+                    }
                 }
             }
         }
@@ -886,28 +936,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // ---- reduce the 4 waves' partial tiles and store ----
     if (wave > 0) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) red[wave - 1][r][lane] = acc[r];
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) red[wave - 1][r][mt][lane] = acc[r][mt];
     }
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-#pragma unroll
-            for (int w = 0; w < kWaves - 1; ++w) acc[r] += red[w][r][lane];
             const int64_t nrow = n0 + 16 * r + lr;
-            if (nrow >= N) continue;
+            float s = 1.0f;
             if constexpr (FMT == FMT_INT8) {
-                const float *s = static_cast<const float *>(P.scales);
-                acc[r] *= P.scale_per_row ? s[nrow] : s[0];
+                const float *sp = static_cast<const float *>(P.scales);
+                s = nrow < N ? sp[P.scale_per_row ? nrow : 0] : 0.0f;
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int m = part * 4 + q;
-                if (m < M) {
-                    if (b.y_bf16)
-                        static_cast<uint16_t *>(P.y)[static_cast<int64_t>(m) * N + nrow] = f32_to_bf16_rne(acc[r][q]);
-                    else
-                        static_cast<float *>(P.y)[static_cast<int64_t>(m) * N + nrow] = acc[r][q];
+            for (int mt = 0; mt < MT; ++mt) {
+                floatx4 v = acc[r][mt];
+#pragma unroll
+                for (int w = 0; w < kWaves - 1; ++w) v += red[w][r][mt][lane];
+                if (nrow >= N) continue;
+                if constexpr (FMT == FMT_INT8) v *= s;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int m = 16 * mt + part * 4 + q;
+                    if (m < M) {
+                        if (b.y_bf16)
+                            static_cast<uint16_t *>(P.y)[static_cast<int64_t>(m) * N + nrow] = f32_to_bf16_rne(v[q]);
+                        else
+                            static_cast<float *>(P.y)[static_cast<int64_t>(m) * N + nrow] = v[q];
+                    }
                 }
             }
         }
@@ -1335,13 +1393,15 @@ int64_t split_region(int fmt, int lw, Problem &p) {
     return xbytes + tbytes + sbytes + zbytes;
 }
 
+// M = 1..64 (M = 1: split or per-tile kernel; M = 2..64: skinny_gx_kernel, whose x descriptor
+// spans M * K bf16 with 32-bit offsets)
 bool skinny_ok(int fmt, const Problem &p, int64_t m) {
+    if (m < 1 || m > 64 || m * p.k * 2 >= (int64_t{1} << 31)) return false;
     if (is_gguf(fmt)) {
-        if (m < 1 || m > 16 || p.group != 32) return false;
+        if (p.group != 32) return false;
         if (p.k % chunk_k(fmt, 16) != 0 || p.k >= (int64_t{1} << 24)) return false;
         return aligned(p.x, 16) && aligned(p.codes, 16) && aligned(p.scales, 16);
     }
-    if (m < 1 || m > 16) return false;
     const int lw = lw_for(fmt, p.group);
     if (lw == 0) return false;
     if (p.k % chunk_k(fmt, lw) != 0) return false;
@@ -1383,25 +1443,31 @@ void launch_lw(int lw, const Batch &b, int64_t tiles, int64_t lds, hipStream_t s
     }
 }
 
-template <int FMT, int LW, int R>
+template <int FMT, int LW, int R, int MT>
 void launch_gx(const Batch &b, int64_t tiles, hipStream_t st) {
-    skinny_gx_kernel<FMT, LW, R, CFH_GX_NB><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, st>>>(b);
+    // one chunk per unit beyond one x tile (the x fragments of a unit grow with MT)
+    constexpr int NB = MT == 1 ? CFH_GX_NB : 1;
+    skinny_gx_kernel<FMT, LW, R, NB, MT><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, st>>>(b);
 }
 
-template <int FMT, int R>
+template <int FMT, int R, int MT>
 void launch_gx_lw(int lw, const Batch &b, int64_t tiles, hipStream_t st) {
-    if (lw == 16) launch_gx<FMT, 16, R>(b, tiles, st);
+    if (lw == 16) launch_gx<FMT, 16, R, MT>(b, tiles, st);
     else if constexpr (FMT != FMT_INT8 && !is_gguf(FMT)) {
-        if (lw == 8) launch_gx<FMT, 8, R>(b, tiles, st);
-        else launch_gx<FMT, 4, R>(b, tiles, st);
+        if (lw == 8) launch_gx<FMT, 8, R, MT>(b, tiles, st);
+        else launch_gx<FMT, 4, R, MT>(b, tiles, st);
     }
 }
 
+// rows per workgroup 16 R and x tiles MT for M: R from the CFH_GX_R_* knobs up to M = 16;
+// beyond, 32 rows and 2 or 4 x tiles
 template <int FMT>
-void launch_gx_r(int r, int lw, const Batch &b, int64_t tiles, hipStream_t st) {
-    if (r == 1) launch_gx_lw<FMT, 1>(lw, b, tiles, st);
-    else if (r == 2) launch_gx_lw<FMT, 2>(lw, b, tiles, st);
-    else launch_gx_lw<FMT, 4>(lw, b, tiles, st);
+void launch_gx_r(int r, int64_t m, int lw, const Batch &b, int64_t tiles, hipStream_t st) {
+    if (m > 32) launch_gx_lw<FMT, 2, 4>(lw, b, tiles, st);
+    else if (m > 16) launch_gx_lw<FMT, 2, 2>(lw, b, tiles, st);
+    else if (r == 1) launch_gx_lw<FMT, 1, 1>(lw, b, tiles, st);
+    else if (r == 2) launch_gx_lw<FMT, 2, 1>(lw, b, tiles, st);
+    else launch_gx_lw<FMT, 4, 1>(lw, b, tiles, st);
 }
 
 template <int FMT, int LW>
@@ -1455,7 +1521,10 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
     // 16-row tiles up to M = 4, 32 rows up to M = 8, 64 rows beyond (x is shared by more rows)
     const int R = m <= 4 ? CFH_GEMV_R_SMALL : m <= 8 ? 2 : 4;
     if (m >= 2) {
-        const int Rg = m <= 4 ? CFH_GX_R_SMALL : m <= 8 ? CFH_GX_R_MID : CFH_GX_R_BIG;
+        // NF4 and Q4_0 at M = 9..16: 32 rows (NF4 62 against 72 us per gate / up / down at
+        // M = 16; Q4_0 spills registers at 64 rows)
+        const int rbig = fmt == FMT_NF4 || fmt == FMT_Q4_0 ? 2 : CFH_GX_R_BIG;
+        const int Rg = m <= 4 ? CFH_GX_R_SMALL : m <= 8 ? CFH_GX_R_MID : m <= 16 ? rbig : 2;
         // x read per wave from global memory (skinny_gx_kernel)
         std::stable_sort(ps, ps + count, [](const Problem &a, const Problem &c) { return a.k > c.k; });
         Batch b{};
@@ -1471,11 +1540,11 @@ void launch_skinny(int fmt, Problem *ps, int count, int64_t m, int y_bf16, hipSt
         b.count = count;
         b.m = static_cast<int32_t>(m);
         b.y_bf16 = y_bf16;
-        if (fmt == FMT_INT4) launch_gx_r<FMT_INT4>(Rg, lw, b, tiles, st);
-        else if (fmt == FMT_NF4) launch_gx_r<FMT_NF4>(Rg, lw, b, tiles, st);
-        else if (fmt == FMT_Q4_0) launch_gx_r<FMT_Q4_0>(Rg, lw, b, tiles, st);
-        else if (fmt == FMT_Q8_0) launch_gx_r<FMT_Q8_0>(Rg, lw, b, tiles, st);
-        else launch_gx_r<FMT_INT8>(Rg, lw, b, tiles, st);
+        if (fmt == FMT_INT4) launch_gx_r<FMT_INT4>(Rg, m, lw, b, tiles, st);
+        else if (fmt == FMT_NF4) launch_gx_r<FMT_NF4>(Rg, m, lw, b, tiles, st);
+        else if (fmt == FMT_Q4_0) launch_gx_r<FMT_Q4_0>(Rg, m, lw, b, tiles, st);
+        else if (fmt == FMT_Q8_0) launch_gx_r<FMT_Q8_0>(Rg, m, lw, b, tiles, st);
+        else launch_gx_r<FMT_INT8>(Rg, m, lw, b, tiles, st);
         check_launch("skinny_gx");
         return;
     }
@@ -1543,17 +1612,24 @@ void common_checks(const void *x, int64_t m, int64_t n, int64_t k, const void *c
 
 }  // namespace
 
-// Prefill MFMA kernel for M > 16 (gemm_prefill.hip); false when the shape does not fit it.
+// Prefill MFMA kernel (gemm_prefill.hip); false when the shape does not fit it.
 bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
                  const void *codes, const void *scales, const uint32_t *zeros, int per_row, void *y,
                  int y_bf16, hipStream_t st);
 
-// Routes one problem to the skinny MFMA kernel (M <= 16) when its shape allows it.
+// Largest M a single problem runs on the skinny kernels; beyond it the prefill kernel is
+// faster (measured on W_gate / W_up / W_down of a 7B block: INT8 and Q4_0 at M = 48 / 64 take
+// 138 / 149 and 309 / 323 us there against 103 / 100 and 200 / 197 us on the prefill kernel;
+// INT4, NF4 and Q8_0 stay faster on the skinny kernel up to M = 64).  Batched calls take the
+// skinny kernels up to M = 64 for every format.
+int64_t skinny_m_max(int fmt) { return fmt == FMT_INT8 || fmt == FMT_Q4_0 ? 32 : 64; }
+
+// Routes one problem to the skinny MFMA kernels when its shape allows it.
 bool gemv_try_skinny(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
                      const void *codes, const void *scales, const uint32_t *zeros, int per_row,
                      void *y, int y_bf16, hipStream_t st) {
     Problem p{x, codes, scales, zeros, y, n, k, static_cast<int32_t>(group), per_row, 0, 0};
-    if (!skinny_ok(fmt, p, m)) return false;
+    if (m > skinny_m_max(fmt) || !skinny_ok(fmt, p, m)) return false;
     launch_skinny(fmt, &p, 1, m, y_bf16, st);
     return true;
 }
@@ -1651,9 +1727,9 @@ int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m,
             launch_skinny(fmt, ps, 2, 1, yb, st);
             return;
         }
-        // M <= 16: split-K kernel at M = 1, the skinny kernel (x of all rows staged once) beyond
+        // split-K kernel at M = 1, the skinny kernel (x read per wave) beyond
         if (gemv_try_skinny(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st)) return;
-        // M > 16: the prefill MFMA kernel reads the planes directly
+        // larger M: the prefill MFMA kernel reads the planes directly
         if (prefill_try(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st)) return;
         gemv_generic(fmt, x, m, n, k, 32, codes, scales_f16, nullptr, 1, y, yb, st);
     });
@@ -1664,7 +1740,7 @@ int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_proble
     return guarded(out_error, [&] {
         require(ggml_type == CFH_GGML_Q4_0 || ggml_type == CFH_GGML_Q8_0,
                 "ggml_type must be CFH_GGML_Q4_0 or CFH_GGML_Q8_0");
-        require(m >= 1 && m <= 16, "batched GEMV requires 1 <= m <= 16");
+        require(m >= 1 && m <= 64, "batched GEMV requires 1 <= m <= 64");
         require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
         require(count == 0 || problems != nullptr, "problems must not be NULL");
         require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
@@ -1692,7 +1768,7 @@ int32_t castforge_hip_gemv_w4a16_batched(const cfh_w4a16_problem_t *problems, in
     return guarded(out_error, [&] {
         require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
         require(count == 0 || problems != nullptr, "problems must not be NULL");
-        require(m >= 1 && m <= 16, "batched GEMV requires 1 <= m <= 16");
+        require(m >= 1 && m <= 64, "batched GEMV requires 1 <= m <= 64");
         require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
         Problem ps[kMaxProblems];
         int used = 0;
@@ -1718,7 +1794,7 @@ int32_t castforge_hip_gemv_w8a16_batched(const cfh_w8a16_problem_t *problems, in
     return guarded(out_error, [&] {
         require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
         require(count == 0 || problems != nullptr, "problems must not be NULL");
-        require(m >= 1 && m <= 16, "batched GEMV requires 1 <= m <= 16");
+        require(m >= 1 && m <= 64, "batched GEMV requires 1 <= m <= 64");
         require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
         Problem ps[kMaxProblems];
         int used = 0;
@@ -1743,7 +1819,7 @@ int32_t castforge_hip_gemv_nf4_batched(const cfh_nf4_problem_t *problems, int32_
     return guarded(out_error, [&] {
         require(count >= 0 && count <= CFH_MAX_BATCH, "count must be in [0, CFH_MAX_BATCH]");
         require(count == 0 || problems != nullptr, "problems must not be NULL");
-        require(m >= 1 && m <= 16, "batched GEMV requires 1 <= m <= 16");
+        require(m >= 1 && m <= 64, "batched GEMV requires 1 <= m <= 64");
         require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
         Problem ps[kMaxProblems];
         int used = 0;

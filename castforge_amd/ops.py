@@ -309,7 +309,7 @@ def gemm_fp8(qa: torch.Tensor, sa: torch.Tensor, qw: torch.Tensor, sw: torch.Ten
 
 
 def gemv_w4a16_batched(xs: list[torch.Tensor], ps: list[Int4Packed], ys: list[torch.Tensor]) -> None:
-    """One launch for several W4A16 problems with the same M (1..16); outputs preallocated."""
+    """One launch for several W4A16 problems with the same M (1..64); outputs preallocated."""
     if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
         raise ValueError("xs, ps, ys must have the same length <= 8")
     if not ps:
@@ -573,8 +573,8 @@ def gguf_q4_0_to_int4g(p: GgufPacked) -> Int4Packed:
 
 
 def gemm_gguf(x: torch.Tensor, p: GgufPacked, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """y [M, n] = x [M, k] (bf16) times decode(W)^T over GGUF planes (split-K GEMV up to
-    M = 16, the prefill MFMA kernel beyond)."""
+    """y [M, n] = x [M, k] (bf16) times decode(W)^T over GGUF planes (split-K GEMV at M = 1 and
+    2, the skinny MFMA kernel up to M = 64 (Q4_0: 32), the prefill MFMA kernel beyond)."""
     x = _check_x(x, p.k)
     y = torch.empty((x.shape[0], p.n), dtype=out_dtype, device=x.device)
     ffi.call("castforge_hip_gemv_gguf", p.ggml_type, _ptr(x), x.shape[0], p.n, p.k, _ptr(p.codes),
@@ -583,7 +583,7 @@ def gemm_gguf(x: torch.Tensor, p: GgufPacked, out_dtype: torch.dtype = torch.bfl
 
 
 def gemv_gguf_batched(xs: list[torch.Tensor], ps: list[GgufPacked], ys: list[torch.Tensor]) -> None:
-    """One launch for up to 8 GGUF matrices of one type with the same M (1..16); outputs
+    """One launch for up to 8 GGUF matrices of one type with the same M (1..64); outputs
     preallocated."""
     if not (len(xs) == len(ps) == len(ys)) or len(ps) > ffi.MAX_BATCH:
         raise ValueError("xs, ps, ys must have the same length <= 8")

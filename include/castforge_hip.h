@@ -190,7 +190,7 @@ int32_t castforge_hip_quantize_int8_batched(const cfh_quant_problem_t *problems,
  * Replaces the evaluation of `castforge.fused_qmatmul` (passes/fuse/epilogue.rs:10-94,
  * codegen/eval.rs:1145-1179 -> eval_matmul_2d eval.rs:1465-1507, packed_rhs) and the HIP text
  * the reference emits for it (codegen/targets/gpu_c.rs:208-292, passes/loops/lower.rs:226-247).
- * M <= 16 runs the MFMA decode kernel; larger M runs the prefill GEMM. */
+ * M <= 64 (INT8: M <= 32) runs the MFMA decode / skinny kernels; larger M the prefill GEMM. */
 int32_t castforge_hip_gemv_w4a16(const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
                                  const uint32_t *codes, const uint16_t *scales_f16,
                                  const uint32_t *zeros, void *y, int32_t y_dtype, void *stream,
@@ -204,7 +204,7 @@ int32_t castforge_hip_gemv_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t 
                                const uint32_t *codes, const float *absmax, void *y, int32_t y_dtype,
                                void *stream, char **out_error);
 
-/* Several W4A16 problems with the same M (1..16) in ONE launch, e.g. the 7 projections of a
+/* Several W4A16 problems with the same M (1..64) in ONE launch, e.g. the 7 projections of a
  * decoder block; each needs k % 128 == 0, group % 128 == 0 and 16-byte aligned x / codes. */
 typedef struct cfh_w4a16_problem_t {
     const uint16_t *x;          /* bf16 [M, k] */
@@ -415,7 +415,7 @@ int32_t castforge_hip_gguf_unpack(int32_t ggml_type, const void *codes, const ui
 /* Q4_0 planes to the INT4g layout (group 32, every zero point 8): int4_codes u32 [rows, k/8],
  * zeros u32 [rows, ceil(k/32 / 8)] = 0x88888888; the planes' scales_f16 serve unchanged as
  * INT4g scales.  (q - 8) * d is the INT4g dequant of the same block, so castforge_hip_gemv_w4a16
- * (prefill MFMA kernel at M > 16) then computes the Q4_0 matmul. */
+ * (prefill MFMA kernel at M > 64) then computes the Q4_0 matmul. */
 int32_t castforge_hip_gguf_q4_0_to_int4g(const void *codes, int64_t rows, int64_t k, uint32_t *int4_codes,
                                          uint32_t *zeros, void *stream, char **out_error);
 /* Planes to f32 [rows, k]: the values decode_ggml_tensor gives for the same blocks. */
@@ -427,14 +427,14 @@ int32_t castforge_hip_dequantize_gguf(int32_t ggml_type, const void *codes, cons
  * dequant-GEMV of a GGUF weight: the reference decodes it to f32 (gguf.rs:513-550) and
  * evaluates the matmul (codegen/eval.rs:1465-1507).  x bf16 [m, k] 16-byte aligned; y f32 or
  * bf16.  M = 1 and 2 run the split-K MFMA kernel (one MFMA per block, scaled in f32 by its d;
- * M = 2 as two problems of one launch), M = 3..16 the skinny MFMA kernel (the same per-block
- * MFMA, x of all rows staged once in LDS); M > 16 the prefill MFMA kernel
+ * M = 2 as two problems of one launch), M = 3..64 (Q4_0: 3..32) the skinny MFMA kernel (the
+ * same per-block MFMA, x read per wave); larger M the prefill MFMA kernel
  * reading the planes directly (exact hi / lo f16 planes of the block values, which must lie
  * within f16 range); shapes neither fits take a generic kernel. */
 int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m, int64_t n, int64_t k,
                                 const void *codes, const uint16_t *scales_f16, void *y, int32_t y_dtype,
                                 void *stream, char **out_error);
-/* Up to CFH_MAX_BATCH matrices of one type with the same M (1..16) in one launch. */
+/* Up to CFH_MAX_BATCH matrices of one type with the same M (1..64) in one launch. */
 int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_problem_t *problems, int32_t count,
                                         int64_t m, int32_t y_dtype, void *stream, char **out_error);
 

@@ -26,7 +26,7 @@ def _x(seed, m, k, dev):
     return xb, torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(dev)
 
 
-@pytest.mark.parametrize("m", [1, 2, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 8, 16, 17, 33, 64])
 @pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (64, 11008), (4096, 4096)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
 def test_w4a16_skinny(cuda, m, n, k, out):
@@ -53,7 +53,7 @@ def test_w4a16_generic_paths(cuda, m, group, k):
     _close(y, ref)
 
 
-@pytest.mark.parametrize("m", [1, 5, 16])
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 32, 33])
 @pytest.mark.parametrize("gran", ["channel", "tensor"])
 @pytest.mark.parametrize("n,k", [(40, 192), (4096, 4096), (33, 11008)])
 def test_w8a16(cuda, m, gran, n, k):
@@ -66,7 +66,7 @@ def test_w8a16(cuda, m, gran, n, k):
     _close(y, O.gemm_w8a16(xb, q.cpu().numpy(), sc))
 
 
-@pytest.mark.parametrize("m", [1, 16, 40])
+@pytest.mark.parametrize("m", [1, 16, 17, 40, 64])
 @pytest.mark.parametrize("block", [64, 32, 16])
 def test_nf4(cuda, m, block):
     n, k = 96, 1024
@@ -146,6 +146,46 @@ def test_nf4_batched(cuda, block):
     for y, y1, ref in zip(ys, singles, refs):
         assert torch.equal(y, y1)
         _close(y, ref)
+
+
+@pytest.mark.parametrize("fmt", ["int4", "int8", "nf4"])
+@pytest.mark.parametrize("m", [17, 40, 64])
+def test_batched_mid_m(cuda, fmt, m):
+    """M = 17..64 in one batched launch (x tiles of 16 rows sharing each decoded weight word):
+    within tolerance of the oracle, and equal to one call per problem wherever that call runs
+    the same kernel (INT8 single calls above M = 32 run the prefill kernel)."""
+    shapes = [(96, 1024), (300, 2048), (64, 4096), (7, 512)]
+    xs, ps, ys, refs = [], [], [], []
+    for i, (n, k) in enumerate(shapes):
+        w = torch.from_numpy(synth.weight(700 + i, 1, n, k)).to(cuda)
+        xb, x = _x(710 + i, m, k, cuda)
+        xs.append(x)
+        ys.append(torch.empty((m, n), dtype=torch.float32, device=cuda))
+        if fmt == "int4":
+            p = ops.quantize_int4g(w, 128)
+            refs.append(O.gemm_w4a16(xb, p.codes.cpu().numpy().view(np.uint32), p.scales.cpu().numpy().view(np.uint16),
+                                     p.zeros.cpu().numpy().view(np.uint32), n, k, 128))
+        elif fmt == "int8":
+            p = ops.quantize_int8(w, 8, "channel", "half_even")
+            refs.append(O.gemm_w8a16(xb, p[0].cpu().numpy(), p[1].cpu().numpy()))
+        else:
+            p = ops.quantize_nf4(w, 64)
+            refs.append(O.gemm_nf4(xb, p.codes.cpu().numpy().view(np.uint32), p.absmax.cpu().numpy(), n, k, 64))
+        ps.append(p)
+    if fmt == "int4":
+        ops.gemv_w4a16_batched(xs, ps, ys)
+        singles = [ops.gemm_w4a16(x, p, torch.float32) for x, p in zip(xs, ps)]
+    elif fmt == "int8":
+        ops.gemv_w8a16_batched(xs, ps, ys, "channel")
+        singles = [ops.gemm_w8a16(x, q, s, "channel", torch.float32) for x, (q, s) in zip(xs, ps)]
+    else:
+        ops.gemv_nf4_batched(xs, ps, ys)
+        singles = [ops.gemm_nf4(x, p, torch.float32) for x, p in zip(xs, ps)]
+    for y, y1, ref in zip(ys, singles, refs):
+        if not (fmt == "int8" and m > 32):
+            assert torch.equal(y, y1)
+        _close(y, ref)
+        _close(y1, ref)
 
 
 def test_nf4_batched_rejects_mixed_blocks(cuda):

@@ -177,7 +177,7 @@ def test_planes_reject_bad_shapes(cuda):
 
 # -------------------------------------------------------------------------------- GEMV ----
 @pytest.mark.parametrize("ty", [Q4_0, Q8_0])
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 16, 17])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8, 9, 16, 17, 33, 64])
 @pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (64, 11008), (4096, 4096)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
 def test_gemv_matches_oracle(cuda, ty, m, n, k, out):
@@ -246,7 +246,7 @@ def test_gemv_batched_block_matches_single_and_torch(cuda, ty):
 
 
 @pytest.mark.parametrize("ty", [Q4_0, Q8_0])
-@pytest.mark.parametrize("m", [4, 16])
+@pytest.mark.parametrize("m", [4, 16, 40, 64])
 def test_gemv_batched_block_m_gt_1(cuda, ty, m):
     """The seven block projections at M > 1 in one launch equal one call per matrix and the
     oracle's decode-then-matmul (sampled rows of each matrix, to keep the CPU side short)."""
@@ -260,7 +260,8 @@ def test_gemv_batched_block_m_gt_1(cuda, ty, m):
     ops.gemv_gguf_batched([x for _, x in xs], ps, ys)
     rng = np.random.default_rng(ty + m)
     for (xb, x), p, y, raw in zip(xs, ps, ys, raws):
-        assert torch.equal(ops.gemm_gguf(x, p, torch.float32), y)
+        if not (ty == Q4_0 and m > 32):  # single Q4_0 calls above M = 32 run the prefill kernel
+            assert torch.equal(ops.gemm_gguf(x, p, torch.float32), y)
         rows = np.sort(rng.choice(p.n, 24, replace=False))
         sub = raw.reshape(p.n, -1)[rows].reshape(-1)  # whole rows of blocks (k % 32 == 0)
         w = O.gguf_decode(ty, sub, 24 * p.k).reshape(24, p.k)
