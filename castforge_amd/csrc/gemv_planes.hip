@@ -1,8 +1,8 @@
-// W4A16 decode GEMV (M = 1) over INT4 g128 weights in the GEMV planes layout, gfx950.
+// W4A16 decode GEMV (M = 1..4) over INT4 g128 weights in the GEMV planes layout, gfx950.
 //
 // Replaces the evaluation of `castforge.fused_qmatmul` at decode (eval.rs:1145-1179 with
 // eval_matmul_2d, eval.rs:1465-1507; packed_rhs [N, K] weights, fold.rs:549-554) for the
-// asymmetric INT4 group-128 format: y[n] = sum_k x[k] * (q[n, k] - z[n, g]) * s[n, g].
+// asymmetric INT4 group-128 format: y[m, n] = sum_k x[m, k] * (q[n, k] - z[n, g]) * s[n, g].
 //
 // GEMV planes.  The canonical INT4g arrays (codes u32 [N, K/8], f16 scales [N, GP], u4 zero
 // points [N, ceil(G/8)]) are rewritten once, at load time, so that one wave-wide 16-byte load
@@ -23,20 +23,26 @@
 //     of bytes of one matrix.  A workgroup's chunk sequence is, tile after tile, each tile's G
 //     chunks; wave i processes positions i, i + 16, i + 32, ... (balanced to one chunk), with
 //     a D-deep ring of loads that runs across tile boundaries.
-//   * x (bf16) is copied into LDS once and converted to f16 in the order the nibble decode
-//     produces, with a per-chunk power of two that brings the chunk's largest |x| into
-//     [2^14, 2^15): every finite bf16 x is then exact in f16 (down to 2^-38 of the chunk's
+//   * x (bf16, M rows) is copied into LDS once and converted to f16 in the order the nibble
+//     decode produces, with a per-(row, chunk) power of two that brings the chunk's largest |x|
+//     into [2^14, 2^15): every finite bf16 x is then exact in f16 (down to 2^-38 of the chunk's
 //     largest value), and the scale is undone on the chunk's f32 partial.
+//   * M = 1: every row of the MFMA's A operand is x (a broadcast LDS read); M = 2..4: A row i
+//     is x row min(i mod 4, M - 1), rows 16 B apart in LDS beyond their G * 256 bytes so that
+//     the 16 distinct fragments of a read fall in distinct banks; D rows 0..M-1 (lanes 0..15)
+//     are the outputs, the other rows are discarded.  The MFMA count per chunk is the same
+//     for every M, so M = 2..4 costs little more than M = 1.
 //   * Decode: (w & 0x000F000F) | 0x64006400 is the f16 pair (1024 + q, 1024 + q'), the 0x00F0
 //     nibbles give 1024 + 16 q; one packed f16 add of -(1024 + z) (or fma by 1/16 and add of
 //     -(64 + z)) leaves the exact integers q - z, so every product x (q - z) is exact and the
 //     MFMA's f32 sums carry the only rounding, as the reference's f32 loop does.
-//   * Each wave keeps one f32 partial per row of its current tile (lanes 0..15 of the MFMA
-//     result) and stores it into its own LDS slot of that tile when it moves to another tile;
+//   * Each wave keeps MR f32 partials per row of its current tile (lanes 0..15 of the MFMA
+//     result) and stores them into its own LDS slot of that tile when it moves to another tile;
 //     no barrier inside the loop.  After the loop one barrier, then the workgroup sums each
 //     row's partials in wave order (the same bits on every run) and stores its rows.
 #include <algorithm>
 #include <map>
+#include <type_traits>
 #include <mutex>
 #include <vector>
 
@@ -79,7 +85,7 @@ struct PProblem {
     const uint8_t *codes;
     const uint16_t *scales;
     const uint8_t *zeros;
-    const uint16_t *x;  // bf16 [K]
+    const uint16_t *x;  // bf16 [M, K]
     void *y;
     int32_t n, G;       // rows, groups (K / 128)
     int32_t units;      // ceil(n / 8)
@@ -89,7 +95,7 @@ struct PProblem {
 
 struct PBatch {
     PProblem p[kMaxP];
-    int32_t count, y_bf16;
+    int32_t count, y_bf16, m;
 };
 
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -130,10 +136,15 @@ struct Stage {
     uint32_t sc, zb;
 };
 
-// LDS: [x as f16, G * 256 B][per chunk 2^sh, G * 4 B (16-byte padded)][partials: tiles x NW x 16 f32]
-template <int NW, int D>
+// x rows staged in LDS (M = 1: one row; M = 2..4: four fragment rows) and their row stride
+template <int MR>
+__host__ __device__ constexpr uint32_t x_row_stride(uint32_t G) { return MR == 1 ? G * 256 : G * 256 + 16; }
+
+// LDS: [x as f16, M rows of G * 256 B at x_row_stride][per (chunk, row) 2^sh, G * MR * 4 B
+// (16-byte padded)][partials: tiles x NW x 16 x MR f32]
+template <int NW, int D, int MR>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW * kWgPerCu / 4)))
-void planes_m1_kernel(PBatch b) {
+void planes_kernel(PBatch b) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = uni(tid >> 6);
@@ -153,21 +164,26 @@ void planes_m1_kernel(PBatch b) {
     const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
     const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
     const int ntiles = t1 - t0, npos = ntiles * G;
-    const uint32_t xbytes = static_cast<uint32_t>(G) * (kGroup * 2);
-    const uint32_t soff = xbytes, aoff = xbytes + ((static_cast<uint32_t>(G) * 4 + 15) & ~15u);
+    const int M = MR == 1 ? 1 : b.m;
+    const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2), RS = x_row_stride<MR>(static_cast<uint32_t>(G));
+    const uint32_t soff = (RS * static_cast<uint32_t>(M) + 15) & ~15u;
+    const uint32_t aoff = soff + ((static_cast<uint32_t>(G) * MR * 4 + 15) & ~15u);
     float *const accs = reinterpret_cast<float *>(lds + aoff);
 
     // partials to zero, before any copy into LDS is in flight (an LDS write after an LDS-bound
     // copy is made to wait for every load in flight)
-    for (int i = tid; i < ntiles * NW * 16; i += 64 * NW) accs[i] = 0.0f;
+    for (int i = tid; i < ntiles * NW * 16 * MR; i += 64 * NW) accs[i] = 0.0f;
 
-    // x (bf16) straight into LDS, 1 KB per wave-wide copy
-    for (int blk = wave; blk * 1024u < xbytes; blk += NW) {
+    // x (bf16) straight into LDS, 1 KB per wave-wide copy, row m at m * RS
+    const int nblk = static_cast<int>((rowb + 1023u) / 1024u);
+    for (int i = wave; i < M * nblk; i += NW) {
+        const int m = i / nblk, blk = i - m * nblk;
         const uint32_t e = blk * 1024u + lane * 16u;
-        if (e < xbytes)
+        if (e < rowb)
             __builtin_amdgcn_global_load_lds(
-                static_cast<const void *>(P.x + (e >> 1)),
-                reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds) + blk * 1024),
+                static_cast<const void *>(P.x + static_cast<size_t>(m) * G * kGroup + (e >> 1)),
+                reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds) + m * RS +
+                                                                           blk * 1024),
                 16, 0, 0);
     }
 
@@ -231,12 +247,13 @@ void planes_m1_kernel(PBatch b) {
     // is then exact in f16 down to 2^-38 of that value); 2^sh is kept per chunk.
     {
         constexpr int kPerm[16] = {0, 4, 1, 5, 2, 6, 3, 7, 8, 12, 9, 13, 10, 14, 11, 15};
-        const int total = G * 8;
+        const int per_row = G * 8, total = M * per_row;
         for (int base = 0; base < total; base += 64 * NW) {  // uniform trip count
             const int i = base + tid;
             const bool act = i < total;
-            const int j = act ? i : 0;
-            uint16_t *px = reinterpret_cast<uint16_t *>(lds) + j * 16;
+            const int ii = act ? i : 0;
+            const int m = ii / per_row, j = ii - m * per_row;  // 8 | per_row: a chunk's 8 lanes share m
+            uint16_t *px = reinterpret_cast<uint16_t *>(lds + m * RS) + j * 16;
             const uint4 r0 = *reinterpret_cast<const uint4 *>(px);
             const uint4 r1 = *reinterpret_cast<const uint4 *>(px + 8);
             const uint32_t wv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
@@ -270,14 +287,18 @@ void planes_m1_kernel(PBatch b) {
             if (act) {
                 *reinterpret_cast<uint4 *>(px) = make_uint4(o[0], o[1], o[2], o[3]);
                 *reinterpret_cast<uint4 *>(px + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-                if ((i & 7) == 0) reinterpret_cast<float *>(lds + soff)[j >> 3] = post;
+                if ((i & 7) == 0) reinterpret_cast<float *>(lds + soff)[(j >> 3) * MR + m] = post;
             }
         }
     }
     lds_barrier<63>();
 
     const uint32_t LO = vgpr_const(0x000F000Fu), HI = vgpr_const(0x00F000F0u), MG = vgpr_const(0x64006400u);
-    float acc = 0.0f;
+    // this lane's x fragment row (D rows 0..M-1 of lanes 0..15 are the outputs)
+    const uint32_t xrow = MR == 1 ? 0u : static_cast<uint32_t>(min(r16 & (MR - 1), M - 1)) * RS;
+    // per lane: the running partial of D rows 0..MR-1 (MR = 1: a scalar, as D rows are equal)
+    typedef typename std::conditional<MR == 1, float, floatx4>::type acc_t;
+    acc_t acc = acc_t{};
     const int steps = npos > wave ? (npos - wave + NW - 1) / NW : 0;
     // the oldest stage is consumed, then refilled with the position D steps ahead (keeping
     // about 48 KB in flight per CU: deeper rings measured slower); every step of the loop runs
@@ -289,17 +310,20 @@ void planes_m1_kernel(PBatch b) {
             const bool live = pt < ntiles;
             const Stage &s = st[i];
             const int g = live ? pg : 0;  // a step past the end reads chunk 0 (in range)
-            const uint8_t *xa = lds + g * (kGroup * 2) + part * 64;
+            const uint8_t *xa = lds + xrow + g * (kGroup * 2) + part * 64;
             const half8_t a0 = *reinterpret_cast<const half8_t *>(xa);
             const half8_t a1 = *reinterpret_cast<const half8_t *>(xa + 16);
             const half8_t a2 = *reinterpret_cast<const half8_t *>(xa + 32);
             const half8_t a3 = *reinterpret_cast<const half8_t *>(xa + 48);
-            const float post = reinterpret_cast<const float *>(lds + soff)[g];
+            // 2^sh of rows 0..MR-1 for this chunk
+            acc_t post;
+            if constexpr (MR == 1) post = reinterpret_cast<const float *>(lds + soff)[g];
+            else post = *reinterpret_cast<const floatx4 *>(lds + soff + g * 16);
             const uint32_t w0 = s.w[0], w1 = s.w[1], w2 = s.w[2], w3 = s.w[3];
             const uint32_t w08 = w0 >> 8, w18 = w1 >> 8, w28 = w2 >> 8, w38 = w3 >> 8;
             const uint32_t zi = (s.zb >> (4 * (r16 & 1))) & 15u;
             const float sc = f16_to_f32(static_cast<uint16_t>(s.sc));
-            float part_sum;
+            acc_t part_sum;
             {
                 // (1024 + q) - (1024 + z) and (1024 + 16 q) / 16 - (64 + z): exact small integers
                 const half2_t zc1024 = as_h2((0xE400u + zi) * 0x00010001u);
@@ -317,9 +341,19 @@ void planes_m1_kernel(PBatch b) {
                 pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, dec(w3, w38), pb, 0, 0, 0);
                 // a separate multiply and add (no contraction): chunk results that cancel
                 // exactly sum to exactly zero
-                part_sum = __fmul_rn(pa[0] + pb[0], sc * post);
+                if constexpr (MR == 1) {
+                    part_sum = __fmul_rn(pa[0] + pb[0], sc * post);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < MR; ++q) part_sum[q] = __fmul_rn(pa[q] + pb[q], sc * post[q]);
+                }
             }
-            acc = __fadd_rn(acc, live ? part_sum : 0.0f);
+            if constexpr (MR == 1) {
+                acc = __fadd_rn(acc, live ? part_sum : 0.0f);
+            } else {
+#pragma unroll
+                for (int q = 0; q < MR; ++q) acc[q] = __fadd_rn(acc[q], live ? part_sum[q] : 0.0f);
+            }
             // next position; a wave's positions in one tile are consecutive steps, so one store
             // of its partials per tile
             const int tile = pt;
@@ -329,8 +363,12 @@ void planes_m1_kernel(PBatch b) {
                 ++pt;
             }
             if (live && pt != tile) {
-                if (lane < 16) accs[(tile * NW + wave) * 16 + lane] = acc;
-                acc = 0.0f;
+                if (lane < 16) {
+                    float *dst = accs + ((tile * NW + wave) * 16 + lane) * MR;
+                    if constexpr (MR == 1) dst[0] = acc;
+                    else *reinterpret_cast<floatx4 *>(dst) = acc;
+                }
+                acc = acc_t{};
             }
             load(st[i]);
             __builtin_amdgcn_sched_barrier(0);
@@ -339,15 +377,17 @@ void planes_m1_kernel(PBatch b) {
     lds_barrier<63>();  // every wave's partials are in LDS
 
     // rows of this workgroup: the waves' partials in wave order (the same bits on every run)
-    for (int i = tid; i < ntiles * 16; i += 64 * NW) {
-        const int row = (t0 + (i >> 4)) * 16 + (i & 15);
+    for (int i = tid; i < ntiles * 16 * M; i += 64 * NW) {
+        const int r = i / M, m = i - r * M;
+        const int row = (t0 + (r >> 4)) * 16 + (r & 15);
         if (row >= rlo && row < rhi) {
-            const float *pa = accs + (i >> 4) * NW * 16 + (i & 15);
+            const float *pa = accs + ((r >> 4) * NW * 16 + (r & 15)) * MR + m;
             float v = 0.0f;
 #pragma unroll
-            for (int q = 0; q < NW; ++q) v += pa[q * 16];
-            if (b.y_bf16) static_cast<uint16_t *>(P.y)[row] = f32_to_bf16_rne(v);
-            else static_cast<float *>(P.y)[row] = v;
+            for (int w2 = 0; w2 < NW; ++w2) v += pa[w2 * 16 * MR];
+            const int64_t o = static_cast<int64_t>(m) * P.n + row;
+            if (b.y_bf16) static_cast<uint16_t *>(P.y)[o] = f32_to_bf16_rne(v);
+            else static_cast<float *>(P.y)[o] = v;
         }
     }
 }
@@ -445,11 +485,31 @@ std::vector<int> workgroups_per_problem(const std::vector<int64_t> &bytes, const
     return wgs;
 }
 
+template <int MR>
+void launch_planes(const PBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
+    static std::mutex mu;
+    static std::map<int, bool> attr_set;  // per device
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    {
+        std::lock_guard<std::mutex> g(mu);
+        if (!attr_set[dev]) {
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_kernel<kWaves, kDepth, MR>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
+                      "hipFuncSetAttribute");
+            attr_set[dev] = true;
+        }
+    }
+    planes_kernel<kWaves, kDepth, MR>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), static_cast<size_t>(lds), st>>>(b);
+    check_launch("planes_kernel");
+}
+
 void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
                     hipStream_t st) {
     require(count >= 1 && count <= kMaxP, "count must be in 1..8");
     require(problems != nullptr, "problems must not be NULL");
-    require(m == 1, "the GEMV planes kernel takes M = 1");
+    require(m >= 1 && m <= 4, "the GEMV planes kernel takes M = 1..4");
     require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
     const int W = cu_count() * kWgPerCu;
     PBatch b{};
@@ -485,24 +545,19 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
         grid += P.wgs;
         // a workgroup's units span at most ceil(units / wgs) / 2 + 2 tiles
         const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
-        lds_max = std::max<int64_t>(lds_max, static_cast<int64_t>(P.G) * 256 + (P.G * 4 + 15) / 16 * 16 + tiles * kWaves * 64);
+        const int64_t mr = m == 1 ? 1 : 4;
+        const int64_t rs = m == 1 ? x_row_stride<1>(static_cast<uint32_t>(P.G)) : x_row_stride<4>(static_cast<uint32_t>(P.G));
+        lds_max = std::max<int64_t>(lds_max, (rs * m + 15) / 16 * 16 + (P.G * mr * 4 + 15) / 16 * 16 +
+                                                 tiles * kWaves * 64 * mr);
     }
     b.count = count;
     b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
-    require(lds_max <= kLdsMax / kWgPerCu, "a problem of the batch exceeds the GEMV planes kernel's LDS (k too large or too "
-                                "many rows per workgroup)");
+    b.m = static_cast<int32_t>(m);
+    require(lds_max <= kLdsMax / kWgPerCu, "a problem of the batch exceeds the GEMV planes kernel's LDS (m * k too large "
+                                "or too many rows per workgroup)");
     const int64_t req = std::max<int64_t>(lds_max, kLdsFloor);
-    static bool attr_set = false;
-    if (!attr_set) {
-        check_hip(hipFuncSetAttribute(
-                      reinterpret_cast<const void *>(&planes_m1_kernel<kWaves, kDepth>),
-                      hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
-                  "hipFuncSetAttribute");
-        attr_set = true;
-    }
-    planes_m1_kernel<kWaves, kDepth>
-        <<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), static_cast<size_t>(req), st>>>(b);
-    check_launch("planes_m1_kernel");
+    if (m == 1) launch_planes<1>(b, grid, req, st);
+    else launch_planes<4>(b, grid, req, st);
 }
 
 void planes_checks(const void *codes, const void *scales, const void *zeros, int64_t rows, int64_t k,

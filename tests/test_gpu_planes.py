@@ -1,4 +1,4 @@
-"""GEMV planes: the INT4 g128 layout the M = 1 decode kernel streams, and that kernel.
+"""GEMV planes: the INT4 g128 layout the decode kernel (M = 1..4) streams, and that kernel.
 
 * The planes equal a numpy construction from the canonical arrays and convert back bit for bit.
 * y matches the oracle's evaluator semantics (dequantize, then eval_matmul_2d, eval.rs:1465-1507)
@@ -77,13 +77,14 @@ def test_planes_layout_and_round_trip(cuda, n, k):
     assert np.array_equal(back.zeros.cpu().numpy().view(np.uint32), zeros)
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (7, 128), (4097, 4096), (64, 11008), (4096, 4096)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
-def test_planes_gemv_matches_oracle(cuda, n, k, out):
+def test_planes_gemv_matches_oracle(cuda, m, n, k, out):
     w = synth.weight(62, 1, n, k)
     p, (codes, scales, zeros) = _packed(w, cuda)
     pl = ops.int4g_to_planes(p)
-    xb = synth.activations_bf16(63, 7, 1, k)
+    xb = synth.activations_bf16(63, 7, m, k)
     y = ops.gemv_w4a16_planes(_xdev(xb, cuda), pl, out)
     torch.cuda.synchronize()
     ref = O.gemm_w4a16(xb, codes, scales, zeros, n, k, 128)
@@ -92,8 +93,9 @@ def test_planes_gemv_matches_oracle(cuda, n, k, out):
     _close(y, ref)
 
 
+@pytest.mark.parametrize("m", [1, 4])
 @pytest.mark.parametrize("shared_x", [True, False])
-def test_planes_llama_block_batched(cuda, shared_x):
+def test_planes_llama_block_batched(cuda, shared_x, m):
     """The 7 projections of a LLaMA-7B block in one launch (x shared by q/k/v and by gate/up as in
     a decoder, or 7 distinct x); every row against the oracle."""
     xs_h, xs, pls, ys, refs = {}, [], [], [], []
@@ -107,11 +109,11 @@ def test_planes_llama_block_batched(cuda, shared_x):
         elif shared_x and name in ("w_gate", "w_up"):
             key = "gate_up"
         if key not in xs_h:
-            xb = synth.activations_bf16(80 + len(xs_h), 7, 1, k)
+            xb = synth.activations_bf16(80 + len(xs_h), 7, m, k)
             xs_h[key] = (xb, _xdev(xb, cuda))
         xb, x = xs_h[key]
         xs.append(x)
-        ys.append(torch.empty((1, n), dtype=torch.float32, device=cuda))
+        ys.append(torch.empty((m, n), dtype=torch.float32, device=cuda))
         refs.append(O.gemm_w4a16(xb, codes, scales, zeros, n, k, 128))
     ops.gemv_w4a16_planes_batched(xs, pls, ys)
     torch.cuda.synchronize()
@@ -124,7 +126,8 @@ def test_planes_llama_block_batched(cuda, shared_x):
         assert torch.equal(y, y2)
 
 
-def test_planes_power_of_two_scale_invariance(cuda):
+@pytest.mark.parametrize("m", [1, 3])
+def test_planes_power_of_two_scale_invariance(cuda, m):
     """y(2^e x) == 2^e y(x) bit for bit for every row, e in -100..100: each chunk of x is brought
     to the same f16 values whatever its power-of-two scale.  e >= 16 puts |x| beyond f16's
     65504 (the rows would be inf without the pre-scale); e = -30 puts it below f16's subnormals."""
@@ -132,7 +135,7 @@ def test_planes_power_of_two_scale_invariance(cuda):
     w = synth.weight(64, 1, n, k)
     p, (codes, scales, zeros) = _packed(w, cuda)
     pl = ops.int4g_to_planes(p)
-    xb = synth.activations_bf16(65, 7, 1, k)
+    xb = synth.activations_bf16(65, 7, m, k)
     x32 = O.bf16_bits_to_f32(xb)
     y0 = ops.gemv_w4a16_planes(_xdev(xb, cuda), pl, torch.float32).cpu().numpy()
     _close(torch.from_numpy(y0), O.gemm_w4a16(xb, codes, scales, zeros, n, k, 128))
@@ -171,7 +174,8 @@ def test_planes_large_and_tiny_activations_vs_oracle(cuda):
     assert np.all(np.abs(y - exact) <= ATOL + RTOL * np.abs(exact) + ref_err)
 
 
-def test_planes_exact_cancellation(cuda):
+@pytest.mark.parametrize("m", [1, 4])
+def test_planes_exact_cancellation(cuda, m):
     """x = [v, -v] with |v| up to 6e4 against weights whose two K halves are equal: the exact
     answer is 0 for every row, reached only through partial sums of order 1e4.  The oracle's
     sequential f32 loop leaves rounding noise of up to ~1e-1 there; every row must be within
@@ -182,13 +186,14 @@ def test_planes_exact_cancellation(cuda):
     w = np.concatenate([wh, wh], axis=1)
     p, (codes, scales, zeros) = _packed(w, cuda)
     pl = ops.int4g_to_planes(p)
-    v = rng.standard_normal(kh).astype(np.float32)
-    v[rng.choice(kh, 40, replace=False)] *= np.float32(6e4)
-    xb = O.f32_to_bf16_bits(np.concatenate([v, -v])).reshape(1, 2 * kh)
-    y = ops.gemv_w4a16_planes(_xdev(xb, cuda), pl, torch.float32).cpu().numpy().reshape(-1)
-    ref = O.gemm_w4a16(xb, codes, scales, zeros, n, 2 * kh, 128).reshape(-1)
-    mag = np.abs(O.dequantize_int4g(codes, scales, zeros, n, 2 * kh, 128).astype(np.float64)) @ \
-        np.abs(O.bf16_bits_to_f32(xb).reshape(-1).astype(np.float64))
+    v = rng.standard_normal((m, kh)).astype(np.float32)
+    for r in range(m):
+        v[r, rng.choice(kh, 40, replace=False)] *= np.float32(6e4)
+    xb = O.f32_to_bf16_bits(np.concatenate([v, -v], axis=1)).reshape(m, 2 * kh)
+    y = ops.gemv_w4a16_planes(_xdev(xb, cuda), pl, torch.float32).cpu().numpy()
+    ref = O.gemm_w4a16(xb, codes, scales, zeros, n, 2 * kh, 128).reshape(m, n)
+    mag = np.abs(O.bf16_bits_to_f32(xb).astype(np.float64)) @ \
+        np.abs(O.dequantize_int4g(codes, scales, zeros, n, 2 * kh, 128).astype(np.float64)).T
     assert np.all(np.abs(y) <= ATOL + 2.0 ** -22 * mag), (np.abs(y).max(), np.abs(ref).max())
     assert np.abs(y).max() <= np.abs(ref).max()
 
@@ -213,8 +218,10 @@ def test_planes_rejects_bad_arguments(cuda):
     arr = (ffi.W4A16Problem * 1)()
     arr[0] = ffi.W4A16Problem(x.data_ptr(), pl.codes.data_ptr(), pl.scales.data_ptr(), pl.zeros.data_ptr(),
                               y.data_ptr(), 32, 256, 128)
-    with pytest.raises(ffi.CastForgeHipError, match="M = 1"):
-        ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 2, ffi.DTYPE_F32, None)
+    with pytest.raises(ffi.CastForgeHipError, match="M = 1..4"):
+        ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 5, ffi.DTYPE_F32, None)
+    with pytest.raises(ValueError, match="1..4 rows"):
+        ops.gemv_w4a16_planes(torch.zeros((5, 256), dtype=torch.bfloat16, device=cuda), pl)
     arr[0].group = 64
     with pytest.raises(ffi.CastForgeHipError, match="groups of 128"):
         ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 1, ffi.DTYPE_F32, None)
