@@ -58,7 +58,7 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 constexpr int kGroup = 128;
 constexpr uint32_t kOob = 0x80000000u;  // past every descriptor's range: reads 0, no traffic
-constexpr int kMaxP = CFH_MAX_BATCH;
+constexpr int kMaxP = 4 * CFH_MAX_BATCH;  // problems of a launch after splitting rows of x
 
 #ifndef CFH_PLANES_WAVES
 #define CFH_PLANES_WAVES 16
@@ -66,8 +66,15 @@ constexpr int kMaxP = CFH_MAX_BATCH;
 #ifndef CFH_PLANES_DEPTH
 #define CFH_PLANES_DEPTH 3
 #endif
+// M = 5..8: 8 waves per workgroup (the partials of 8 rows per wave and tile would not fit
+// LDS next to x at 16) and their ring depth
+#ifndef CFH_PLANES_WAVES8
+#define CFH_PLANES_WAVES8 8
+#endif
+#ifndef CFH_PLANES_DEPTH8
+#define CFH_PLANES_DEPTH8 4
+#endif
 constexpr int kWaves = CFH_PLANES_WAVES;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kDepth = CFH_PLANES_DEPTH;
 // workgroups per CU (their LDS request keeps any more off a CU) and the cache policy of the
 // streamed loads (2 = non-temporal: each byte is read once)
@@ -90,12 +97,12 @@ struct PProblem {
     int32_t n, G;       // rows, groups (K / 128)
     int32_t units;      // ceil(n / 8)
     int32_t wg0, wgs;   // this problem's workgroups [wg0, wg0 + wgs)
-    int32_t pad;
+    int32_t m;          // rows of x (and y) of this problem
 };
 
 struct PBatch {
     PProblem p[kMaxP];
-    int32_t count, y_bf16, m;
+    int32_t count, y_bf16;
 };
 
 __device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -136,12 +143,14 @@ struct Stage {
     uint32_t sc, zb;
 };
 
-// x rows staged in LDS (M = 1: one row; M = 2..4: four fragment rows) and their row stride
+// x rows staged in LDS (M = 1: one row; otherwise up to MR = 4 or 8 fragment rows) and their
+// row stride
 template <int MR>
 __host__ __device__ constexpr uint32_t x_row_stride(uint32_t G) { return MR == 1 ? G * 256 : G * 256 + 16; }
 
 // LDS: [x as f16, M rows of G * 256 B at x_row_stride][per (chunk, row) 2^sh, G * MR * 4 B
 // (16-byte padded)][partials: tiles x NW x 16 x MR f32]
+// MR = 8: A row i is x row min(i mod 8, M - 1); D rows 0..7 are lanes 0..31 (4 rows each).
 template <int NW, int D, int MR>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW * kWgPerCu / 4)))
 void planes_kernel(PBatch b) {
@@ -164,7 +173,7 @@ void planes_kernel(PBatch b) {
     const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
     const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
     const int ntiles = t1 - t0, npos = ntiles * G;
-    const int M = MR == 1 ? 1 : b.m;
+    const int M = MR == 1 ? 1 : P.m;
     const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2), RS = x_row_stride<MR>(static_cast<uint32_t>(G));
     const uint32_t soff = (RS * static_cast<uint32_t>(M) + 15) & ~15u;
     const uint32_t aoff = soff + ((static_cast<uint32_t>(G) * MR * 4 + 15) & ~15u);
@@ -202,14 +211,14 @@ void planes_kernel(PBatch b) {
     // per-lane offsets within a chunk, pushed out of range (OR kOob) for rows outside
     // [rlo, rhi) and for positions past the workgroup's tiles: recomputed when the tile changes.
     // Every lane needs its row's zero point (its codes are decoded as exact q - z); the scale
-    // multiplies the MFMA result, which lanes 0..15 hold.
+    // multiplies the MFMA result, whose output rows lanes 0..15 hold (0..31 at MR = 8).
     uint32_t vcode, vscale, vzero;
     auto lane_offsets = [&]() __attribute__((always_inline)) {
         const int row = (t0 + lt) * 16 + r16;
         const bool ok = lt < ntiles && row >= rlo && row < rhi;
         const uint32_t m = ok ? 0u : kOob;
         vcode = (static_cast<uint32_t>(lane) * 16u) | m;
-        vscale = (static_cast<uint32_t>(r16) * 2u) | (lane < 16 ? m : kOob);
+        vscale = (static_cast<uint32_t>(r16) * 2u) | (lane < (MR == 8 ? 32 : 16) ? m : kOob);
         vzero = static_cast<uint32_t>(r16 >> 1) | m;
     };
     lane_offsets();
@@ -294,8 +303,10 @@ void planes_kernel(PBatch b) {
     lds_barrier<63>();
 
     const uint32_t LO = vgpr_const(0x000F000Fu), HI = vgpr_const(0x00F000F0u), MG = vgpr_const(0x64006400u);
-    // this lane's x fragment row (D rows 0..M-1 of lanes 0..15 are the outputs)
+    // this lane's x fragment row (D rows 0..M-1 of lanes 0..4 MR - 1 are the outputs) and the
+    // first of the 4 D rows it holds
     const uint32_t xrow = MR == 1 ? 0u : static_cast<uint32_t>(min(r16 & (MR - 1), M - 1)) * RS;
+    const uint32_t prow = MR == 1 ? 0u : 4u * static_cast<uint32_t>(part & (MR / 4 - 1));
     // per lane: the running partial of D rows 0..MR-1 (MR = 1: a scalar, as D rows are equal)
     typedef typename std::conditional<MR == 1, float, floatx4>::type acc_t;
     acc_t acc = acc_t{};
@@ -318,7 +329,7 @@ void planes_kernel(PBatch b) {
             // 2^sh of rows 0..MR-1 for this chunk
             acc_t post;
             if constexpr (MR == 1) post = reinterpret_cast<const float *>(lds + soff)[g];
-            else post = *reinterpret_cast<const floatx4 *>(lds + soff + g * 16);
+            else post = *reinterpret_cast<const floatx4 *>(lds + soff + (g * MR + prow) * 4);
             const uint32_t w0 = s.w[0], w1 = s.w[1], w2 = s.w[2], w3 = s.w[3];
             const uint32_t w08 = w0 >> 8, w18 = w1 >> 8, w28 = w2 >> 8, w38 = w3 >> 8;
             const uint32_t zi = (s.zb >> (4 * (r16 & 1))) & 15u;
@@ -345,14 +356,14 @@ void planes_kernel(PBatch b) {
                     part_sum = __fmul_rn(pa[0] + pb[0], sc * post);
                 } else {
 #pragma unroll
-                    for (int q = 0; q < MR; ++q) part_sum[q] = __fmul_rn(pa[q] + pb[q], sc * post[q]);
+                    for (int q = 0; q < 4; ++q) part_sum[q] = __fmul_rn(pa[q] + pb[q], sc * post[q]);
                 }
             }
             if constexpr (MR == 1) {
                 acc = __fadd_rn(acc, live ? part_sum : 0.0f);
             } else {
 #pragma unroll
-                for (int q = 0; q < MR; ++q) acc[q] = __fadd_rn(acc[q], live ? part_sum[q] : 0.0f);
+                for (int q = 0; q < 4; ++q) acc[q] = __fadd_rn(acc[q], live ? part_sum[q] : 0.0f);
             }
             // next position; a wave's positions in one tile are consecutive steps, so one store
             // of its partials per tile
@@ -363,8 +374,8 @@ void planes_kernel(PBatch b) {
                 ++pt;
             }
             if (live && pt != tile) {
-                if (lane < 16) {
-                    float *dst = accs + ((tile * NW + wave) * 16 + lane) * MR;
+                if (lane < (MR == 1 ? 16 : 4 * MR)) {
+                    float *dst = accs + (tile * NW + wave) * 16 * MR + (MR == 1 ? lane : 4 * lane);
                     if constexpr (MR == 1) dst[0] = acc;
                     else *reinterpret_cast<floatx4 *>(dst) = acc;
                 }
@@ -381,7 +392,8 @@ void planes_kernel(PBatch b) {
         const int r = i / M, m = i - r * M;
         const int row = (t0 + (r >> 4)) * 16 + (r & 15);
         if (row >= rlo && row < rhi) {
-            const float *pa = accs + ((r >> 4) * NW * 16 + (r & 15)) * MR + m;
+            const float *pa = accs + (r >> 4) * NW * 16 * MR +
+                              (MR == 1 ? (r & 15) : ((r & 15) + 16 * (m >> 2)) * 4 + (m & 3));
             float v = 0.0f;
 #pragma unroll
             for (int w2 = 0; w2 < NW; ++w2) v += pa[w2 * 16 * MR];
@@ -485,7 +497,7 @@ std::vector<int> workgroups_per_problem(const std::vector<int64_t> &bytes, const
     return wgs;
 }
 
-template <int MR>
+template <int NW, int D, int MR>
 void launch_planes(const PBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
     static std::mutex mu;
     static std::map<int, bool> attr_set;  // per device
@@ -494,26 +506,41 @@ void launch_planes(const PBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
     {
         std::lock_guard<std::mutex> g(mu);
         if (!attr_set[dev]) {
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_kernel<kWaves, kDepth, MR>),
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_kernel<NW, D, MR>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
                       "hipFuncSetAttribute");
             attr_set[dev] = true;
         }
     }
-    planes_kernel<kWaves, kDepth, MR>
-        <<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), static_cast<size_t>(lds), st>>>(b);
+    planes_kernel<NW, D, MR>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), static_cast<size_t>(lds), st>>>(b);
     check_launch("planes_kernel");
 }
 
+// LDS bytes of one problem: its x rows, their post factors and the partials of the tiles one
+// of its workgroups spans (at most ceil(units / wgs) / 2 + 2)
+int64_t planes_lds(int mr, int nw, const PProblem &P) {
+    const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
+    const int64_t rs = mr == 1 ? x_row_stride<1>(static_cast<uint32_t>(P.G)) : x_row_stride<4>(static_cast<uint32_t>(P.G));
+    return (rs * P.m + 15) / 16 * 16 + (P.G * mr * 4 + 15) / 16 * 16 + tiles * nw * 64 * mr;
+}
+
+// M = 1: one row of x per problem (16 waves); M = 2..4: up to 4 rows (16 waves); M = 5..8:
+// up to 8 rows (8 waves), a problem whose 8 rows of x do not fit LDS next to its partials
+// split into two problems of 4 rows that stream the same planes.  Beyond M = 8 the partials of
+// a workgroup (16 rows per tile and wave) outgrow LDS for matrices that get few workgroups,
+// and every further group of rows would stream the planes again: the canonical-layout kernels
+// serve M > 8.
 void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
                     hipStream_t st) {
-    require(count >= 1 && count <= kMaxP, "count must be in 1..8");
+    require(count >= 1 && count <= CFH_MAX_BATCH, "count must be in 1..8");
     require(problems != nullptr, "problems must not be NULL");
-    require(m >= 1 && m <= 4, "the GEMV planes kernel takes M = 1..4");
+    require(m >= 1 && m <= 8, "the GEMV planes kernel takes M = 1..8");
     require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+    const int mr = m == 1 ? 1 : m <= 4 ? 4 : 8;
+    const int nw = mr == 8 ? CFH_PLANES_WAVES8 : kWaves;
     const int W = cu_count() * kWgPerCu;
-    PBatch b{};
-    std::vector<int64_t> bytes, units;
+    const int esz = y_dtype == CFH_DTYPE_BF16 ? 2 : 4;
     for (int i = 0; i < count; ++i) {
         const cfh_w4a16_problem_t &q = problems[i];
         require(q.group == kGroup, "GEMV planes hold INT4 groups of 128");
@@ -521,43 +548,68 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
         require(q.x && q.codes && q.scales_f16 && q.zeros && q.y, "x, planes and y must not be NULL");
         require(aligned(q.x, 16) && aligned(q.codes, 16) && aligned(q.scales_f16, 4) && aligned(q.y, 4),
                 "x and codes planes must be 16-byte aligned, scales and y 4-byte aligned");
-        const int64_t T = (q.n + 15) / 16, G = q.k / kGroup;
-        require(T * G * 1024 < (int64_t(1) << 31), "GEMV planes of one matrix must stay below 2 GiB");
-        bytes.push_back(T * G * 1024);
-        units.push_back((q.n + 7) / 8);
+        require(((q.n + 15) / 16) * (q.k / kGroup) * 1024 < (int64_t(1) << 31),
+                "GEMV planes of one matrix must stay below 2 GiB");
     }
-    const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+    // row groups: rows [r0, r0 + rows) of problem src
+    struct Group {
+        int src, r0, rows;
+    };
+    std::vector<int> split4(static_cast<size_t>(count), 0);  // problems whose groups hold 4 rows
+    PBatch b{};
     int64_t lds_max = 0, grid = 0;
-    for (int i = 0; i < count; ++i) {
-        const cfh_w4a16_problem_t &q = problems[i];
-        PProblem &P = b.p[i];
-        P.codes = reinterpret_cast<const uint8_t *>(q.codes);
-        P.scales = q.scales_f16;
-        P.zeros = reinterpret_cast<const uint8_t *>(q.zeros);
-        P.x = q.x;
-        P.y = q.y;
-        P.n = static_cast<int32_t>(q.n);
-        P.G = static_cast<int32_t>(q.k / kGroup);
-        P.units = static_cast<int32_t>(units[static_cast<size_t>(i)]);
-        P.wg0 = static_cast<int32_t>(grid);
-        P.wgs = wgs[static_cast<size_t>(i)];
-        require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
-        grid += P.wgs;
-        // a workgroup's units span at most ceil(units / wgs) / 2 + 2 tiles
-        const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
-        const int64_t mr = m == 1 ? 1 : 4;
-        const int64_t rs = m == 1 ? x_row_stride<1>(static_cast<uint32_t>(P.G)) : x_row_stride<4>(static_cast<uint32_t>(P.G));
-        lds_max = std::max<int64_t>(lds_max, (rs * m + 15) / 16 * 16 + (P.G * mr * 4 + 15) / 16 * 16 +
-                                                 tiles * kWaves * 64 * mr);
+    for (int attempt = 0; attempt <= count; ++attempt) {  // each retry splits at least one more problem
+        std::vector<Group> groups;
+        for (int i = 0; i < count; ++i) {
+            const int gr = mr == 8 && split4[static_cast<size_t>(i)] ? 4 : mr;
+            for (int r0 = 0; r0 < m; r0 += gr) groups.push_back({i, r0, static_cast<int>(std::min<int64_t>(gr, m - r0))});
+        }
+        require(groups.size() <= static_cast<size_t>(kMaxP), "too many problems for one launch");
+        std::vector<int64_t> bytes, units;
+        for (const Group &g : groups) {
+            const cfh_w4a16_problem_t &q = problems[g.src];
+            bytes.push_back(((q.n + 15) / 16) * (q.k / kGroup) * 1024);
+            units.push_back((q.n + 7) / 8);
+        }
+        const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+        b = PBatch{};
+        lds_max = 0;
+        grid = 0;
+        bool retry = false;
+        for (size_t j = 0; j < groups.size(); ++j) {
+            const Group &g = groups[j];
+            const cfh_w4a16_problem_t &q = problems[g.src];
+            PProblem &P = b.p[j];
+            P.codes = reinterpret_cast<const uint8_t *>(q.codes);
+            P.scales = q.scales_f16;
+            P.zeros = reinterpret_cast<const uint8_t *>(q.zeros);
+            P.x = q.x + static_cast<int64_t>(g.r0) * q.k;
+            P.y = static_cast<uint8_t *>(q.y) + static_cast<int64_t>(g.r0) * q.n * esz;
+            P.n = static_cast<int32_t>(q.n);
+            P.G = static_cast<int32_t>(q.k / kGroup);
+            P.units = static_cast<int32_t>(units[j]);
+            P.wg0 = static_cast<int32_t>(grid);
+            P.wgs = wgs[j];
+            P.m = g.rows;
+            require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
+            grid += P.wgs;
+            const int64_t need = planes_lds(mr, nw, P);
+            if (need > kLdsMax / kWgPerCu && mr == 8 && g.rows > 4 && !split4[static_cast<size_t>(g.src)]) {
+                split4[static_cast<size_t>(g.src)] = 1;
+                retry = true;
+            }
+            lds_max = std::max<int64_t>(lds_max, need);
+        }
+        b.count = static_cast<int32_t>(groups.size());
+        if (!retry) break;
     }
-    b.count = count;
     b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
-    b.m = static_cast<int32_t>(m);
     require(lds_max <= kLdsMax / kWgPerCu, "a problem of the batch exceeds the GEMV planes kernel's LDS (m * k too large "
                                 "or too many rows per workgroup)");
     const int64_t req = std::max<int64_t>(lds_max, kLdsFloor);
-    if (m == 1) launch_planes<1>(b, grid, req, st);
-    else launch_planes<4>(b, grid, req, st);
+    if (mr == 1) launch_planes<kWaves, kDepth, 1>(b, grid, req, st);
+    else if (mr == 4) launch_planes<kWaves, kDepth, 4>(b, grid, req, st);
+    else launch_planes<CFH_PLANES_WAVES8, CFH_PLANES_DEPTH8, 8>(b, grid, req, st);
 }
 
 void planes_checks(const void *codes, const void *scales, const void *zeros, int64_t rows, int64_t k,

@@ -1,4 +1,4 @@
-"""GEMV planes: the INT4 g128 layout the decode kernel (M = 1..4) streams, and that kernel.
+"""GEMV planes: the INT4 g128 layout the decode kernel (M = 1..8) streams, and that kernel.
 
 * The planes equal a numpy construction from the canonical arrays and convert back bit for bit.
 * y matches the oracle's evaluator semantics (dequantize, then eval_matmul_2d, eval.rs:1465-1507)
@@ -77,7 +77,7 @@ def test_planes_layout_and_round_trip(cuda, n, k):
     assert np.array_equal(back.zeros.cpu().numpy().view(np.uint32), zeros)
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 8])
 @pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (7, 128), (4097, 4096), (64, 11008), (4096, 4096)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
 def test_planes_gemv_matches_oracle(cuda, m, n, k, out):
@@ -93,7 +93,7 @@ def test_planes_gemv_matches_oracle(cuda, m, n, k, out):
     _close(y, ref)
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 5, 8])
 @pytest.mark.parametrize("shared_x", [True, False])
 def test_planes_llama_block_batched(cuda, shared_x, m):
     """The 7 projections of a LLaMA-7B block in one launch (x shared by q/k/v and by gate/up as in
@@ -126,7 +126,7 @@ def test_planes_llama_block_batched(cuda, shared_x, m):
         assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 7])
 def test_planes_power_of_two_scale_invariance(cuda, m):
     """y(2^e x) == 2^e y(x) bit for bit for every row, e in -100..100: each chunk of x is brought
     to the same f16 values whatever its power-of-two scale.  e >= 16 puts |x| beyond f16's
@@ -174,7 +174,7 @@ def test_planes_large_and_tiny_activations_vs_oracle(cuda):
     assert np.all(np.abs(y - exact) <= ATOL + RTOL * np.abs(exact) + ref_err)
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 8])
 def test_planes_exact_cancellation(cuda, m):
     """x = [v, -v] with |v| up to 6e4 against weights whose two K halves are equal: the exact
     answer is 0 for every row, reached only through partial sums of order 1e4.  The oracle's
@@ -218,10 +218,10 @@ def test_planes_rejects_bad_arguments(cuda):
     arr = (ffi.W4A16Problem * 1)()
     arr[0] = ffi.W4A16Problem(x.data_ptr(), pl.codes.data_ptr(), pl.scales.data_ptr(), pl.zeros.data_ptr(),
                               y.data_ptr(), 32, 256, 128)
-    with pytest.raises(ffi.CastForgeHipError, match="M = 1..4"):
-        ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 5, ffi.DTYPE_F32, None)
-    with pytest.raises(ValueError, match="1..4 rows"):
-        ops.gemv_w4a16_planes(torch.zeros((5, 256), dtype=torch.bfloat16, device=cuda), pl)
+    with pytest.raises(ffi.CastForgeHipError, match="M = 1..8"):
+        ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 9, ffi.DTYPE_F32, None)
+    with pytest.raises(ValueError, match="1..8 rows"):
+        ops.gemv_w4a16_planes(torch.zeros((9, 256), dtype=torch.bfloat16, device=cuda), pl)
     arr[0].group = 64
     with pytest.raises(ffi.CastForgeHipError, match="groups of 128"):
         ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 1, ffi.DTYPE_F32, None)
