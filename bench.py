@@ -7,8 +7,8 @@ activations.  Steps rotate over `--copies` distinct copies of the packed block s
 set (16 x 105 MB) exceeds the 256 MB MALL and every step streams from HBM.
 
 Also reported (`components`): quantize GB/s (INT4 g128 and INT8 per-channel over the f32
-block), W4A16 GEMV at M=8/16, W8A16 GEMV at M=1 (config 1), NF4 GEMV at M=1 and NF4 GEMM at
-M=64/512 (config 3), W4A16 prefill GEMM at M=4096 (config 5), FP8 W8A8 GEMM (config 4), and
+block), W4A16 GEMV at M=4/8 over the GEMV planes and at M=8/16 over the canonical layout,
+W8A16 GEMV at M=1 (config 1), NF4 GEMV at M=1 and NF4 GEMM at M=64/512 (config 3), W4A16 prefill GEMM at M=4096 (config 5), FP8 W8A8 GEMM (config 4), and
 the 32-layer AWQ-style INT4 model (config 5): quantize, decode GEMV and prefill GEMM over all
 layers.
 
@@ -236,10 +236,10 @@ def main():
             tot += n * k // 2 + n * ((g + 7) // 8 * 8) * 2 + n * ((g + 7) // 8) * 4 + 2 * m * k + 2 * m * n
         return tot
 
-    def planes_bytes():
-        """Compulsory bytes of one M = 1 step over GEMV planes: codes, one f16 scale and one u4
-        zero point per row and group, x and y (bf16)."""
-        return sum(n * k // 2 + n * (k // 128) * 2 + n * (k // 128) // 2 + 2 * k + 2 * n
+    def planes_bytes(m=1):
+        """Compulsory bytes of one step over GEMV planes: codes, one f16 scale and one u4 zero
+        point per row and group (once, whatever M), x and y (bf16, M rows)."""
+        return sum(n * k // 2 + n * (k // 128) * 2 + n * (k // 128) // 2 + 2 * m * k + 2 * m * n
                    for (_, n, k) in synth.LLAMA7B_BLOCK)
 
     copies = [packed0] + [[ops.Int4Packed(p.codes.clone(), p.scales.clone(), p.zeros.clone(),
@@ -254,11 +254,11 @@ def main():
         ys = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
         return lambda i: ops.gemv_w4a16_batched(xs, copies[i % len(copies)], ys)
 
-    def planes_case():
+    def planes_case(m=1):
         # a decoder's activations: q/k/v share one x, gate/up another
-        xk = {tid: x_for(1, k, tid) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)}
+        xk = {tid: x_for(m, k, tid) for tid, (_, n, k) in enumerate(synth.LLAMA7B_BLOCK)}
         xs = [xk[0], xk[0], xk[0], xk[3], xk[4], xk[4], xk[6]]
-        ys = [torch.empty((1, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
+        ys = [torch.empty((m, n), dtype=torch.bfloat16, device=dev) for (_, n, k) in synth.LLAMA7B_BLOCK]
         return lambda i: ops.gemv_w4a16_planes_batched(xs, planes[i % len(planes)], ys)
 
     components = {}
@@ -288,10 +288,19 @@ def main():
         del src, dst
 
     if not args.only_headline:
+        # small-batch decode over the planes (M = 2..8; W_down's 8 rows of x run as two halves
+        # at M > 4, each streaming its planes: the bytes below count them once)
+        for m in (4, 8):
+            st = time_steps(planes_case(m), max(20, args.steps // 4), 5, min_ms=20.0, replays=3)
+            components[f"w4a16_planes_gemv_m{m}_GBps"] = round(planes_bytes(m) / (st * 1e-3) / 1e9, 1)
+            components[f"w4a16_planes_gemv_m{m}_us"] = round(st * 1e3, 2)
+            log(f"[bench] W4A16 GEMV M={m} (planes): {st * 1e3:.1f} us/step "
+                f"{components[f'w4a16_planes_gemv_m{m}_GBps']} GB/s")
         for m in (8, 16):
-            st = time_steps(gemv_case(m), max(20, args.steps // 4), 5)
+            st = time_steps(gemv_case(m), max(20, args.steps // 4), 5, min_ms=20.0, replays=3)
             components[f"w4a16_gemv_m{m}_GBps"] = round(w4_bytes(m) / (st * 1e-3) / 1e9, 1)
-            log(f"[bench] W4A16 GEMV M={m}: {st * 1e3:.1f} us/step {components[f'w4a16_gemv_m{m}_GBps']} GB/s")
+            log(f"[bench] W4A16 GEMV M={m} (canonical layout): {st * 1e3:.1f} us/step "
+                f"{components[f'w4a16_gemv_m{m}_GBps']} GB/s")
 
         # quantize over the f32 block (809 MB in, > MALL)
         nel = sum(n * k for (_, n, k) in synth.LLAMA7B_BLOCK)
@@ -379,16 +388,24 @@ def main():
                 f"{components[f'w4a16_prefill_m{m}_n{n}_k{k}_TFLOPs']} TFLOP/s")
             del xp, yp
         nf3 = [ops.quantize_nf4(w, 64) for w in block_f32[4:]]
+        # M = 64: one launch over the three matrices on the skinny kernel, rotating over 4 copies
+        # of the weights (270 MB, beyond the 256 MB MALL); M = 512: one prefill GEMM per matrix
+        nf3c = [nf3] + [[ops.Nf4Packed(p.codes.clone(), p.absmax.clone(), p.n, p.k, p.block) for p in nf3]
+                        for _ in range(3)]
         for m in (64, 512):
             xs3 = [torch.randn((m, p.k), generator=gen, device=dev).to(torch.bfloat16) for p in nf3]
-            st = time_steps(lambda i: [ops.gemm_nf4(x, p, torch.bfloat16) for x, p in zip(xs3, nf3)], 10, 2)
+            if m == 64:
+                ys3 = [torch.empty((m, p.n), dtype=torch.bfloat16, device=dev) for p in nf3]
+                st = time_steps(lambda i: ops.gemv_nf4_batched(xs3, nf3c[i % len(nf3c)], ys3), 20, 3)
+            else:
+                st = time_steps(lambda i: [ops.gemm_nf4(x, p, torch.bfloat16) for x, p in zip(xs3, nf3)], 10, 2)
             fl = sum(2.0 * m * p.n * p.k for p in nf3)
             by = sum(p.nbytes() + 2 * m * p.k + 2 * m * p.n for p in nf3)
             components[f"nf4_gemm_m{m}_TFLOPs"] = round(fl / (st * 1e-3) / 1e12, 1)
             components[f"nf4_gemm_m{m}_GBps"] = round(by / (st * 1e-3) / 1e9, 1)
             log(f"[bench] NF4 GEMM M={m} (Wg, Wu, Wd): {st * 1e3:.1f} us, "
                 f"{components[f'nf4_gemm_m{m}_TFLOPs']} TFLOP/s, {components[f'nf4_gemm_m{m}_GBps']} GB/s")
-        del nf3
+        del nf3, nf3c
 
         # Config 5: a 32-layer LLaMA-7B-shaped f32 weight set (6.476 B linear params, 25.9 GB),
         # quantized end to end INT4 g128 with the AWQ-style per-input-channel pre-scale
