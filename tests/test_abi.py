@@ -62,8 +62,8 @@ def test_batched_rejects_bad_count_and_m():
     arr = (ffi.W4A16Problem * 1)()
     rc, msg = _status("castforge_hip_gemv_w4a16_batched", arr, 9, 1, 0, None)
     assert rc == 1 and "count" in msg
-    rc, msg = _status("castforge_hip_gemv_w4a16_batched", arr, 1, 17, 0, None)
-    assert rc == 1 and "m <= 16" in msg
+    rc, msg = _status("castforge_hip_gemv_w4a16_batched", arr, 1, 65, 0, None)
+    assert rc == 1 and "m <= 64" in msg
 
 
 def test_error_pointer_optional():
