@@ -506,6 +506,57 @@ __device__ __forceinline__ void hadamard16_lanes(float (&x)[16], int rot_b, floa
     for (int i = 0; i < 16; ++i) x[i] *= norm;
 }
 
+// Sub-block (of 16 values) that thread t holds when a Hadamard block spans 32 .. 256 values:
+// within each 16-lane DPP row, lane bits (l0, l1, l2, l3) hold sub-block bits
+// (l0 ^ l2, l1 ^ l2, l2, l3).  The cross-lane stages h = 16, 32, 64, 128 pair sub-blocks that
+// differ in bit 0, 1, 2, 3, and in this layout the partners are lane ^ 1, lane ^ 2 (quad
+// permutations), lane ^ 7 (the half-row mirror) and lane ^ 8 (row rotation by 8): one DPP
+// read each.  An involution, and the identity on bits above 3.
+__device__ __forceinline__ int hsub16(int t) { return t ^ (((t >> 2) & 1) * 3); }
+
+// One cross-lane stage in the hsub16 layout: the partner's value (DPP control CTRL) times
+// c = +1 on the lane whose sub-block has the stage's bit clear, -1 on the other, plus the
+// lane's own value.
+template <int CTRL>
+__device__ __forceinline__ void hstage16(float (&x)[16], float c) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float p = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x[i]), CTRL, 0xF, 0xF, false));
+        x[i] = __builtin_fmaf(p, c, x[i]);
+    }
+}
+
+// hadamard16_lanes for blocks of 32 .. 256 values in the hsub16 layout (thread t holds
+// sub-block hsub16(t)).  A cross-lane stage is one fma per value: on the lane that keeps the
+// sum it is the reference's x + y, on its partner it is y - x = -(x - y), and that value
+// carries the opposite sign from then on (the next stages add and subtract it with the same
+// rule, so the signs compose).  Every value ends as (-1)^(number of stages its lane took the
+// difference on) times the reference's, and the final multiply by that sign times norm
+// restores it.  Products by +-1 are exact, so each value is rounded once per stage as in the
+// reference; only the sign of an exact zero or of a NaN can differ, and no INT4 code depends
+// on either.
+__device__ __forceinline__ void hadamard16_lanes_fast(float (&x)[16], int rot_b, float norm, int t) {
+#pragma unroll
+    for (int h = 1; h < 16; h *= 2) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 2 * h)
+#pragma unroll
+            for (int j = i; j < i + h; ++j) {
+                const float a = x[j], b = x[j + h];
+                x[j] = a + b;
+                x[j + h] = a - b;
+            }
+    }
+    const int sb = hsub16(t) & 15 & ((rot_b >> 4) - 1);  // the sub-block bits the stages use
+    hstage16<0xB1>(x, (sb & 1) ? -1.0f : 1.0f);                      // h = 16: lane ^ 1
+    if (rot_b >= 64) hstage16<0x4E>(x, (sb & 2) ? -1.0f : 1.0f);     // h = 32: lane ^ 2
+    if (rot_b >= 128) hstage16<0x141>(x, (sb & 4) ? -1.0f : 1.0f);   // h = 64: lane ^ 7
+    if (rot_b >= 256) hstage16<0x128>(x, (sb & 8) ? -1.0f : 1.0f);   // h = 128: lane ^ 8
+    const float f = (__builtin_popcount(static_cast<unsigned>(sb)) & 1) ? -norm : norm;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] *= f;
+}
+
 template <int GROUP>
 __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> sets, int64_t cols, int rot_b,
                                                                float rot_norm) {
@@ -527,7 +578,11 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
     uint32_t *rcodes = codes + row * KW;
     uint16_t *rscales = scales + row * GP;
     const uint32_t zw = blockIdx.x * TPB + threadIdx.x / T;  // zero-point word (task) in the row
-    const int t = threadIdx.x % T;
+    // the task's sub-block this thread holds: its own index, or hsub16 of it for the one-fma
+    // Hadamard stages (which keeps every group on the same lanes: hsub16 only swaps sub-blocks
+    // within aligned runs of 8, and within runs of 2 and 4 it maps runs onto runs)
+    const bool fast_rot = rot_b >= 32 && rot_b <= 256;  // uniform
+    const int t = fast_rot ? hsub16(static_cast<int>(threadIdx.x % T)) : static_cast<int>(threadIdx.x % T);
     const bool task_ok = zw < ZW;
     const uint32_t w0 = zw * (2 * T) + 2 * t;  // this thread's first code word
     const bool ok0 = task_ok && w0 < KW, ok1 = task_ok && w0 + 1 < KW;
@@ -551,7 +606,8 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
             }
         }
     }
-    if (rot_b > 1) hadamard16_lanes(x, rot_b, rot_norm);  // uniform: every lane takes part
+    if (fast_rot) hadamard16_lanes_fast(x, rot_b, rot_norm, static_cast<int>(threadIdx.x));  // uniform
+    else if (rot_b > 1) hadamard16_lanes(x, rot_b, rot_norm);  // uniform: every lane takes part
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         if (h == 0 ? ok0 : ok1) {

@@ -57,14 +57,38 @@ def test_rotate_in_place_and_unaligned(cuda):
         ops.rotate_hadamard(_t(w, cuda), 64, 0)
 
 
-@pytest.mark.parametrize("group", [16, 32, 128, 256])
-@pytest.mark.parametrize("b", [2, 16, 64, 128, 1024])
+@pytest.mark.parametrize("group", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("b", [2, 16, 32, 64, 128, 256, 1024])
 def test_fused_hadamard_int4g_equals_two_pass(cuda, group, b):
     w = _t(synth.weight(73, group, 96, 4096), cuda)
     fused = ops.quantize_int4g_hadamard(w, group, b)
     two = ops.quantize_int4g(ops.rotate_hadamard(w, b, 1), group)
     for a, c in ((fused.codes, two.codes), (fused.scales, two.scales), (fused.zeros, two.zeros)):
         assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("b", [32, 128, 256])
+def test_fused_hadamard_int4g_special_values(cuda, b):
+    """Exact zeros, -0, +-inf, NaN, values whose butterflies overflow, and blocks that cancel to
+    exact zeros: the fused quantizer's codes, scales and zero points equal the two-pass ones
+    (its Hadamard stages may give a zero or a NaN the other sign, which no code depends on)."""
+    rng = np.random.default_rng(75)
+    w = (rng.standard_normal((24, 2048)) * 0.02).astype(np.float32)
+    w[0, :] = 0.0
+    w[1, :] = -0.0
+    w[2, ::7] = np.inf
+    w[3, 5::11] = -np.inf
+    w[4, 3::13] = np.nan
+    w[5, ::3] = 3e38
+    w[6, :] = 1.0                        # every block sums to b, every difference to exactly 0
+    w[7, 0::2], w[7, 1::2] = 0.5, -0.5   # cancellations at h = 1
+    w[8, :1024] = -0.0
+    w = _t(w, cuda)
+    for group in (32, 128):
+        fused = ops.quantize_int4g_hadamard(w, group, b)
+        two = ops.quantize_int4g(ops.rotate_hadamard(w, b, 1), group)
+        for a, c in ((fused.codes, two.codes), (fused.scales, two.scales), (fused.zeros, two.zeros)):
+            assert torch.equal(a, c), (group, b)
 
 
 def test_fused_hadamard_int4g_many_rows(cuda):
