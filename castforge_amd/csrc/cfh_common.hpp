@@ -109,6 +109,15 @@ __device__ __forceinline__ float lane_xor(float v) {
     else return __shfl_xor(v, D);
 }
 
+// Sub-block that lane t holds when a Walsh-Hadamard block spans 2..16 lanes of sub-blocks:
+// within each 16-lane DPP row, lane bits (l0, l1, l2, l3) hold sub-block bits
+// (l0 ^ l2, l1 ^ l2, l2, l3).  The cross-lane stages pair sub-blocks that differ in bit 0, 1,
+// 2, 3, and in this layout the partners are lane ^ 1, lane ^ 2 (quad permutations), lane ^ 7
+// (the half-row mirror, DPP 0x141) and lane ^ 8 (row rotation by 8, DPP 0x128): one DPP read
+// each.  An involution, the identity on bits above 3, and it maps aligned runs of 2, 4, 8 and
+// 16 lanes onto aligned runs of sub-blocks.
+__device__ __forceinline__ int hsub16(int t) { return t ^ (((t >> 2) & 1) * 3); }
+
 // One cross-lane butterfly stage over N values per lane against lane ^ D: the lane with bit D
 // clear holds position j and keeps x + y, its partner holds j + h and keeps x - y (x the lower
 // lane's value, y the upper's), exactly the reference's buf[j] / buf[j + h] update.

@@ -506,14 +506,6 @@ __device__ __forceinline__ void hadamard16_lanes(float (&x)[16], int rot_b, floa
     for (int i = 0; i < 16; ++i) x[i] *= norm;
 }
 
-// Sub-block (of 16 values) that thread t holds when a Hadamard block spans 32 .. 256 values:
-// within each 16-lane DPP row, lane bits (l0, l1, l2, l3) hold sub-block bits
-// (l0 ^ l2, l1 ^ l2, l2, l3).  The cross-lane stages h = 16, 32, 64, 128 pair sub-blocks that
-// differ in bit 0, 1, 2, 3, and in this layout the partners are lane ^ 1, lane ^ 2 (quad
-// permutations), lane ^ 7 (the half-row mirror) and lane ^ 8 (row rotation by 8): one DPP
-// read each.  An involution, and the identity on bits above 3.
-__device__ __forceinline__ int hsub16(int t) { return t ^ (((t >> 2) & 1) * 3); }
-
 // One cross-lane stage in the hsub16 layout: the partner's value (DPP control CTRL) times
 // c = +1 on the lane whose sub-block has the stage's bit clear, -1 on the other, plus the
 // lane's own value.

@@ -121,6 +121,86 @@ __global__ __launch_bounds__(kBlock) void fwht_rows_wave_kernel(const float *src
     }
 }
 
+// Rows rotation for b = 16 .. 128 in one phase, 8 values per lane: lane l of each 16-lane DPP
+// row holds the 8-value sub-block hsub16(l) of its 128 values, so the cross-lane stages
+// h = 8, 16, 32, 64 read lane ^ 1, ^ 2, ^ 7, ^ 8, one DPP move each.
+//  * A wave whose inputs are all finite, none -0 and all below 2^117 in magnitude (no
+//    intermediate can overflow) runs each cross-lane stage as one fma: the partner's value
+//    times +1 on the lane keeping the sum, -1 on the other, plus its own, so the second lane
+//    holds -(x - y) from then on; every value ends as (-1)^popcount(its lane's stage bits)
+//    times the reference's, and the final fma by that sign times norm plus +0 restores it,
+//    -0 included: from such inputs the reference never produces -0 (a sum or difference is -0
+//    only with a -0 operand), and +0 turns any -0 of ours into +0.
+//  * Any other wave runs x + y and x - y per stage in the same layout: the reference's
+//    operations on its operands, NaN and zero signs included.
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ void stage_fast(float (&v)[8], float c) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(dpp_read<CTRL>(v[i]), c, v[i]);
+}
+template <int CTRL>
+__device__ __forceinline__ void stage_exact(float (&v)[8], bool lower) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float p = dpp_read<CTRL>(v[i]);
+        v[i] = lower ? v[i] + p : p - v[i];
+    }
+}
+template <int B>
+__global__ __launch_bounds__(kBlock) void fwht_rows_fast_kernel(const float *__restrict__ src, float *__restrict__ dst,
+                                                                int64_t n, float norm) {
+    static_assert(B >= 16 && B <= 128, "one to four cross-lane stages");
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int sb = hsub16(static_cast<int>(threadIdx.x & 15)) & (B / 8 - 1);  // the stage bits
+    const int64_t e = ((t & ~int64_t{15}) + hsub16(static_cast<int>(t & 15))) * 8;
+    const bool in = e + 8 <= n;  // n is a multiple of B: a block is wholly in or out
+    float v[8];
+    if (in) {
+        const float4 a = *reinterpret_cast<const float4 *>(src + e), b = *reinterpret_cast<const float4 *>(src + e + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    bool odd = false;  // -0, +-inf, NaN (class bits 0, 1, 2, 5, 9) or |v| >= 2^117
+#pragma unroll
+    for (int i = 0; i < 8; ++i) odd |= __builtin_amdgcn_classf(v[i], 0x227) || __builtin_fabsf(v[i]) >= 0x1p117f;
+#pragma unroll
+    for (int h = 1; h < 8; h *= 2)
+#pragma unroll
+        for (int i = 0; i < 8; i += 2 * h)
+#pragma unroll
+            for (int j = i; j < i + h; ++j) {
+                const float x = v[j], y = v[j + h];
+                v[j] = x + y;
+                v[j + h] = x - y;
+            }
+    if (__builtin_amdgcn_ballot_w64(odd) == 0) {  // wave-uniform
+        stage_fast<0xB1>(v, (sb & 1) ? -1.0f : 1.0f);                     // h = 8: lane ^ 1
+        if constexpr (B >= 32) stage_fast<0x4E>(v, (sb & 2) ? -1.0f : 1.0f);   // h = 16: lane ^ 2
+        if constexpr (B >= 64) stage_fast<0x141>(v, (sb & 4) ? -1.0f : 1.0f);  // h = 32: lane ^ 7
+        if constexpr (B >= 128) stage_fast<0x128>(v, (sb & 8) ? -1.0f : 1.0f); // h = 64: lane ^ 8
+        const float f = (__builtin_popcount(static_cast<unsigned>(sb)) & 1) ? -norm : norm;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(v[i], f, 0.0f);
+    } else {
+        stage_exact<0xB1>(v, (sb & 1) == 0);
+        if constexpr (B >= 32) stage_exact<0x4E>(v, (sb & 2) == 0);
+        if constexpr (B >= 64) stage_exact<0x141>(v, (sb & 4) == 0);
+        if constexpr (B >= 128) stage_exact<0x128>(v, (sb & 8) == 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] *= norm;
+    }
+    if (in) {
+        *reinterpret_cast<float4 *>(dst + e) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4 *>(dst + e + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
 template <int G>
 void launch_strided(const float *src, float *dst, int64_t O, int64_t o_stride, int64_t L, int64_t ax_stride,
                     int64_t h_lo, int o_fast, float norm, hipStream_t st) {
@@ -178,7 +258,13 @@ void rotate_hadamard_impl(const float *src, float *dst, int64_t d0, int64_t d1, 
         const int64_t grid = ((n + 7) / 8 + kBlock - 1) / kBlock;
         require(grid <= 0x7fffffff, "tensor too large for one launch");
         const float nm = ext == b ? norm : 0.0f;
-        if (aligned(in, 16) && aligned(dst, 16))
+        const bool vec = aligned(in, 16) && aligned(dst, 16);
+        if (vec && b >= 16 && b <= 128) {
+            if (b == 16) fwht_rows_fast_kernel<16><<<static_cast<unsigned>(grid), kBlock, 0, st>>>(in, dst, n, norm);
+            else if (b == 32) fwht_rows_fast_kernel<32><<<static_cast<unsigned>(grid), kBlock, 0, st>>>(in, dst, n, norm);
+            else if (b == 64) fwht_rows_fast_kernel<64><<<static_cast<unsigned>(grid), kBlock, 0, st>>>(in, dst, n, norm);
+            else fwht_rows_fast_kernel<128><<<static_cast<unsigned>(grid), kBlock, 0, st>>>(in, dst, n, norm);
+        } else if (vec)
             fwht_rows_wave_kernel<true><<<static_cast<unsigned>(grid), kBlock, 0, st>>>(in, dst, n, ext, nm);
         else
             fwht_rows_wave_kernel<false><<<static_cast<unsigned>(grid), kBlock, 0, st>>>(in, dst, n, ext, nm);

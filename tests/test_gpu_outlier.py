@@ -34,13 +34,42 @@ def test_rotate_columns_bit_exact(cuda, k, n, b):
 
 
 @pytest.mark.parametrize("d0,d1,b", [(3, 16, 2), (5, 4096, 8), (7, 4096, 512), (4, 4096, 1024), (2, 8192, 4096),
-                                     (33, 11008, 256), (1, 64, 64)])
+                                     (33, 11008, 256), (1, 64, 64), (9, 4096, 16), (6, 4096, 32),
+                                     (40, 4096, 128), (3, 128, 128), (5, 11008, 64)])
 def test_rotate_rows_bit_exact(cuda, d0, d1, b):
     w = synth.weight(71, d1, d0, d1)
     got = ops.rotate_hadamard(_t(w, cuda), b, 1)
     torch.cuda.synchronize()
     want, _ = O.rotate_hadamard(np.ascontiguousarray(w.T), b)
     np.testing.assert_array_equal(_bits(got.cpu().numpy()), _bits(np.ascontiguousarray(want.T)))
+
+
+@pytest.mark.parametrize("b", [16, 32, 64, 128])
+def test_rotate_rows_special_values(cuda, b):
+    """Exact zeros, -0 (whole rows and half rows: one 512-value wave with and one without),
+    +-inf, NaN, values whose butterflies overflow, values just below the kernel's 2^117
+    overflow guard, and blocks that cancel to exact zeros: every non-NaN output has the
+    oracle's bits, -0 and +0 included, and NaN outputs are where the oracle's are."""
+    d0, d1 = 12, 1024
+    rng = np.random.default_rng(76)
+    w = rng.standard_normal((d0, d1)).astype(np.float32)
+    w[0] = 0.0
+    w[1] = -0.0
+    w[2, :512] = -0.0
+    w[3, ::5] = np.inf
+    w[4, 3::7] = np.nan
+    w[5, ::3] = 3e38
+    w[6] = 1.0                              # every difference of the first stage is exactly 0
+    w[7, 0::2], w[7, 1::2] = 0.5, -0.5
+    w[8] = np.float32(2.0 ** 117)           # at the guard: the exact path
+    w[9] = np.float32(2.0 ** 116)           # below it: the one-fma path, no overflow
+    w[10, ::2] = -w[10, 1::2]
+    got = ops.rotate_hadamard(_t(w, cuda), b, 1).cpu().numpy()
+    want, _ = O.rotate_hadamard(np.ascontiguousarray(w.T), b)
+    want = np.ascontiguousarray(want.T)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(_bits(got)[~nan], _bits(want)[~nan])
 
 
 def test_rotate_in_place_and_unaligned(cuda):
