@@ -19,6 +19,9 @@ constexpr int kBlock = 256;  // 4 waves
 #ifndef CFH_INT4Q16
 #define CFH_INT4Q16 1  // 0: the 8-codes-per-thread INT4 kernel for every group size
 #endif
+#ifndef CFH_INT4Q16_AWQ_ROWS
+#define CFH_INT4Q16_AWQ_ROWS 4  // rows per thread of the 16-codes INT4 kernel with an AWQ pre-scale
+#endif
 
 __device__ __forceinline__ float round_sel(float x, int mode) {
     return mode == CFH_ROUND_HALF_EVEN ? rintf(x) : roundf(x);
@@ -538,18 +541,20 @@ __device__ __forceinline__ float group_reduce_min(float v) {
 // (<= 1024) against lane ^ (h / 16), the lower lane keeping x + y and the upper x - y.  The
 // lanes of a wave hold 1024 consecutive elements of one row, so every block lies in one wave.
 __device__ __forceinline__ void hadamard16_lanes(float (&x)[16], int rot_b, float norm) {
+    // stages as compile-time constants, so x stays in registers (no dynamic index)
+    static_for<4>([&](auto S) {
+        constexpr int h = 1 << decltype(S)::value;
+        if (h < rot_b) {
 #pragma unroll
-    for (int h = 1; h < 16; h *= 2) {
-        if (h >= rot_b) break;
+            for (int i = 0; i < 16; i += 2 * h)
 #pragma unroll
-        for (int i = 0; i < 16; i += 2 * h)
-#pragma unroll
-            for (int j = i; j < i + h; ++j) {
-                const float a = x[j], b = x[j + h];
-                x[j] = a + b;
-                x[j + h] = a - b;
-            }
-    }
+                for (int j = i; j < i + h; ++j) {
+                    const float a = x[j], b = x[j + h];
+                    x[j] = a + b;
+                    x[j + h] = a - b;
+                }
+        }
+    });
     lane_butterflies<16>(x, rot_b >> 4);  // stages h = 16 .. rot_b / 2 (wave-uniform)
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] *= norm;
@@ -598,16 +603,19 @@ __device__ __forceinline__ void hadamard16_lanes_fast(float (&x)[16], int rot_b,
     for (int i = 0; i < 16; ++i) x[i] *= f;
 }
 
-template <int GROUP>
+// R rows per grid row (R > 1 when every matrix of the launch has a multiple of R rows): the
+// AWQ pre-scale of the thread's 16 columns is loaded once and serves all R rows.
+template <int GROUP, int R>
 __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> sets, int64_t cols, int rot_b,
                                                                float rot_norm) {
     constexpr int TPG = GROUP / 16;   // threads per group
     constexpr int T = 8 * TPG;        // threads per task (8 groups: one zero-point word)
     constexpr int TPB = kBlock / T;   // tasks per block
-    __shared__ uint32_t zpart[kBlock / 64];
-    // one row per grid row: the row's bases are uniform and every offset below is 32-bit
-    int64_t row;
-    const int set = sets.find(blockIdx.y, row);
+    __shared__ uint32_t zpart[2][kBlock / 64];
+    // R rows of one matrix per grid row: the rows' bases are uniform and every offset below
+    // is 32-bit
+    int64_t row0;
+    const int set = sets.find(static_cast<int64_t>(blockIdx.y) * R, row0);
     const float *__restrict__ src = sets.src[set];
     const float *__restrict__ in_scale = sets.in_scale[set];
     uint32_t *__restrict__ codes = static_cast<uint32_t *>(sets.codes[set]);
@@ -615,9 +623,6 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
     uint32_t *__restrict__ zeros = sets.zeros[set];
     const uint32_t KW = static_cast<uint32_t>(cols >> 3);
     const uint32_t G = static_cast<uint32_t>((cols + GROUP - 1) / GROUP), ZW = (G + 7) >> 3, GP = ZW * 8;
-    const float *rsrc = src + row * cols;
-    uint32_t *rcodes = codes + row * KW;
-    uint16_t *rscales = scales + row * GP;
     const uint32_t zw = blockIdx.x * TPB + threadIdx.x / T;  // zero-point word (task) in the row
     // the task's sub-block this thread holds: its own index, or hsub16 of it for the one-fma
     // Hadamard stages (which keeps every group on the same lanes: hsub16 only swaps sub-blocks
@@ -627,80 +632,109 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
     const bool task_ok = zw < ZW;
     const uint32_t w0 = zw * (2 * T) + 2 * t;  // this thread's first code word
     const bool ok0 = task_ok && w0 < KW, ok1 = task_ok && w0 + 1 < KW;
-    float x[16];
+    // the thread's 16 AWQ pre-scales (1 outside the row): loaded once for R > 1, after the
+    // row's own loads for R = 1 so that they are not waited for before those are issued
+    float sc[16];
+    auto load_scales = [&]() {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = 0.0f;
-    float mx = -INFINITY, mn = INFINITY;
+        for (int i = 0; i < 16; ++i) sc[i] = 1.0f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        if (h == 0 ? ok0 : ok1) {
-            const float4 *p = reinterpret_cast<const float4 *>(rsrc + (w0 + h) * 8);
-            const float4 a = p[0], b = p[1];
-            float *xx = x + 8 * h;
-            xx[0] = a.x; xx[1] = a.y; xx[2] = a.z; xx[3] = a.w;
-            xx[4] = b.x; xx[5] = b.y; xx[6] = b.z; xx[7] = b.w;
-            if (in_scale) {
+        for (int h = 0; h < 2; ++h) {
+            if (h == 0 ? ok0 : ok1) {
                 const float4 *q = reinterpret_cast<const float4 *>(in_scale + (w0 + h) * 8);
                 const float4 c = q[0], d = q[1];
-                xx[0] *= c.x; xx[1] *= c.y; xx[2] *= c.z; xx[3] *= c.w;
-                xx[4] *= d.x; xx[5] *= d.y; xx[6] *= d.z; xx[7] *= d.w;
+                float *ss = sc + 8 * h;
+                ss[0] = c.x; ss[1] = c.y; ss[2] = c.z; ss[3] = c.w;
+                ss[4] = d.x; ss[5] = d.y; ss[6] = d.z; ss[7] = d.w;
             }
         }
+    };
+    if constexpr (R > 1) {
+        if (in_scale) load_scales();
     }
-    if (fast_rot) hadamard16_lanes_fast(x, rot_b, rot_norm, static_cast<int>(threadIdx.x));  // uniform
-    else if (rot_b > 1) hadamard16_lanes(x, rot_b, rot_norm);  // uniform: every lane takes part
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        if (h == 0 ? ok0 : ok1) {
+    for (int rr = 0; rr < R; ++rr) {
+        const int64_t row = row0 + rr;
+        const float *rsrc = src + row * cols;
+        uint32_t *rcodes = codes + row * KW;
+        uint16_t *rscales = scales + row * GP;
+        float x[16];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, x[8 * h + i]); mn = fminf(mn, x[8 * h + i]); }
-        }
-    }
-    mx = group_reduce_max<TPG>(mx);
-    mn = group_reduce_min<TPG>(mn);
-    const uint16_t hs = int4_scale_bits(mx, mn);
-    const float s = f16_to_f32(hs);
-    float zf = rintf(-mn / s);
-    if (zf != zf) zf = 0.0f;
-    zf = fminf(fmaxf(zf, 0.0f), 15.0f);
-    const float y = 1.0f / s;
-    const int gi = t / TPG;  // group within the task
+        for (int i = 0; i < 16; ++i) x[i] = 0.0f;
+        float mx = -INFINITY, mn = INFINITY;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        if (h == 0 ? ok0 : ok1) {
-            uint32_t word = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float r = rintf(div_by_scale(x[8 * h + i], s, y, 64.0f));
-                if (r != r) r = 0.0f;
-                const float qf = fminf(fmaxf(r + zf, 0.0f), 15.0f);
-                word |= static_cast<uint32_t>(qf) << (4 * i);
+        for (int h = 0; h < 2; ++h) {
+            if (h == 0 ? ok0 : ok1) {
+                const float4 *p = reinterpret_cast<const float4 *>(rsrc + (w0 + h) * 8);
+                const float4 a = p[0], b = p[1];
+                float *xx = x + 8 * h;
+                xx[0] = a.x; xx[1] = a.y; xx[2] = a.z; xx[3] = a.w;
+                xx[4] = b.x; xx[5] = b.y; xx[6] = b.z; xx[7] = b.w;
             }
-            rcodes[w0 + h] = word;
         }
-    }
-    uint32_t zn = 0;
-    if (t % TPG == 0) {
-        if (ok0) {
-            rscales[zw * 8 + gi] = hs;
-            zn = static_cast<uint32_t>(zf) << (4 * gi);
-        } else if (task_ok && zw * 8 + gi >= G) {
-            rscales[zw * 8 + gi] = 0;  // pad scale slots of the last 8-group block
-        }
-    }
-    if constexpr (T <= 64) {
-        zn = wave_or<T>(zn);
-        if (t == 0 && task_ok) zeros[row * ZW + zw] = zn;
-    } else {
-        zn = wave_or<64>(zn);
-        if ((threadIdx.x & 63) == 0) zpart[threadIdx.x >> 6] = zn;
-        __syncthreads();
-        if (t == 0 && task_ok) {
-            uint32_t z = 0;
-            const int w0i = (threadIdx.x >> 6);
+        if (in_scale) {  // uniform
+            if constexpr (R == 1) load_scales();
 #pragma unroll
-            for (int i = 0; i < T / 64; ++i) z |= zpart[w0i + i];
-            zeros[row * ZW + zw] = z;
+            for (int i = 0; i < 16; ++i) x[i] *= sc[i];  // 0 * 1 outside the row
+        }
+        if (fast_rot) hadamard16_lanes_fast(x, rot_b, rot_norm, static_cast<int>(threadIdx.x));  // uniform
+        else if (rot_b > 1) hadamard16_lanes(x, rot_b, rot_norm);  // uniform: every lane takes part
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h == 0 ? ok0 : ok1) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, x[8 * h + i]); mn = fminf(mn, x[8 * h + i]); }
+            }
+        }
+        mx = group_reduce_max<TPG>(mx);
+        mn = group_reduce_min<TPG>(mn);
+        const uint16_t hs = int4_scale_bits(mx, mn);
+        const float s = f16_to_f32(hs);
+        float zf = rintf(-mn / s);
+        if (zf != zf) zf = 0.0f;
+        zf = fminf(fmaxf(zf, 0.0f), 15.0f);
+        const float y = 1.0f / s;
+        const int gi = t / TPG;  // group within the task
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h == 0 ? ok0 : ok1) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    float r = rintf(div_by_scale(x[8 * h + i], s, y, 64.0f));
+                    if (r != r) r = 0.0f;
+                    const float qf = fminf(fmaxf(r + zf, 0.0f), 15.0f);
+                    word |= static_cast<uint32_t>(qf) << (4 * i);
+                }
+                rcodes[w0 + h] = word;
+            }
+        }
+        uint32_t zn = 0;
+        if (t % TPG == 0) {
+            if (ok0) {
+                rscales[zw * 8 + gi] = hs;
+                zn = static_cast<uint32_t>(zf) << (4 * gi);
+            } else if (task_ok && zw * 8 + gi >= G) {
+                rscales[zw * 8 + gi] = 0;  // pad scale slots of the last 8-group block
+            }
+        }
+        if constexpr (T <= 64) {
+            zn = wave_or<T>(zn);
+            if (t == 0 && task_ok) zeros[row * ZW + zw] = zn;
+        } else {
+            // alternate buffers: a row's readers finish before the barrier of the next row,
+            // which comes before the row after it overwrites their buffer
+            uint32_t *zp = zpart[rr & 1];
+            zn = wave_or<64>(zn);
+            if ((threadIdx.x & 63) == 0) zp[threadIdx.x >> 6] = zn;
+            __syncthreads();
+            if (t == 0 && task_ok) {
+                uint32_t z = 0;
+                const int w0i = (threadIdx.x >> 6);
+#pragma unroll
+                for (int i = 0; i < T / 64; ++i) z |= zp[w0i + i];
+                zeros[row * ZW + zw] = z;
+            }
         }
     }
 }
@@ -918,14 +952,28 @@ void launch_int4g16(const RowSets<float> &sets, int64_t rows, int64_t cols, int6
     // 16 codes per thread: a task (8 groups) takes group / 2 threads; one grid row per row
     const int64_t G = (cols + group - 1) / group, ZW = (G + 7) / 8;
     const int64_t tpb = kBlock / (group / 2);
-    dim3 g(static_cast<unsigned>((ZW + tpb - 1) / tpb), static_cast<unsigned>(rows)), b(kBlock);
-    switch (group) {
-    case 16: int4g_quant16_kernel<16><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
-    case 32: int4g_quant16_kernel<32><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
-    case 64: int4g_quant16_kernel<64><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
-    case 128: int4g_quant16_kernel<128><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
-    default: int4g_quant16_kernel<256><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm); break;
+    // with an AWQ pre-scale, CFH_INT4Q16_AWQ_ROWS rows per grid row when every matrix allows
+    bool awq = false, even = true;
+    for (int i = 0; i < sets.count; ++i) {
+        awq = awq || sets.in_scale[i] != nullptr;
+        even = even && (sets.row_end[i] - (i > 0 ? sets.row_end[i - 1] : 0)) % CFH_INT4Q16_AWQ_ROWS == 0;
     }
+    const int R = awq && even ? CFH_INT4Q16_AWQ_ROWS : 1;
+    dim3 g(static_cast<unsigned>((ZW + tpb - 1) / tpb), static_cast<unsigned>(rows / R)), b(kBlock);
+    auto go = [&](auto grp, auto r) {
+        int4g_quant16_kernel<decltype(grp)::value, decltype(r)::value><<<g, b, 0, st>>>(sets, cols, rot_b, rot_norm);
+    };
+    auto by_group = [&](auto r) {
+        switch (group) {
+        case 16: go(std::integral_constant<int, 16>{}, r); break;
+        case 32: go(std::integral_constant<int, 32>{}, r); break;
+        case 64: go(std::integral_constant<int, 64>{}, r); break;
+        case 128: go(std::integral_constant<int, 128>{}, r); break;
+        default: go(std::integral_constant<int, 256>{}, r); break;
+        }
+    };
+    if (R == 1) by_group(std::integral_constant<int, 1>{});
+    else by_group(std::integral_constant<int, CFH_INT4Q16_AWQ_ROWS>{});
     check_launch("int4g_quant16");
 }
 

@@ -161,11 +161,12 @@ def test_int4g_edge_groups(cuda):
     assert np.array_equal(_u32(p.zeros), z_ref)
 
 
-@pytest.mark.parametrize("group", [32, 128])
-@pytest.mark.parametrize("n,k", [(16, 1024), (3, 11008), (4096, 4096)])
+@pytest.mark.parametrize("group", [32, 128, 256])
+@pytest.mark.parametrize("n,k", [(16, 1024), (3, 11008), (12, 2304), (4096, 4096)])
 def test_int4g_awq_prescale_bit_exact(cuda, group, n, k):
     """BASELINE config 5: W' = W * a^0.5 per input channel, quantized INT4 g128 in one pass;
-    codes / scales / zeros equal the oracle's quantization of f32(W * s)."""
+    codes / scales / zeros equal the oracle's quantization of f32(W * s).  Row counts that are
+    multiples of 4 take the kernel's several-rows-per-thread form, 3 rows the one-row form."""
     w = _w(23, n, k, specials=(n * k >= 1024))
     s = synth.awq_channel_scales(23, 9, k)
     c_ref, s_ref, z_ref = O.quantize_int4g_awq(w, s, group)
