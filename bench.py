@@ -350,8 +350,14 @@ def main():
         st = time_steps(nf_step, 50, 5)
         nf_bytes = sum(p.nbytes() + 2 * p.k + 2 * p.n for p in nf)
         components["nf4_gemv_m1_GBps"] = round(nf_bytes / (st * 1e-3) / 1e9, 1)
-        log(f"[bench] W8A16 M=1 {components['w8a16_gemv_m1_GBps']} GB/s, NF4 M=1 {components['nf4_gemv_m1_GBps']} GB/s")
-        del nf, nfc
+        # the same launch over NF4 planes (castforge_hip_gemv_nf4_planes_batched); the same
+        # algorithmic bytes (the canonical codes, absmax, x and y)
+        nfp = [[ops.nf4_to_planes(p) for p in c] for c in nfc]
+        st = time_steps(lambda i: ops.gemv_nf4_planes_batched(xsn, nfp[i % len(nfp)], ysn), 50, 5)
+        components["nf4_planes_gemv_m1_GBps"] = round(nf_bytes / (st * 1e-3) / 1e9, 1)
+        log(f"[bench] W8A16 M=1 {components['w8a16_gemv_m1_GBps']} GB/s, NF4 M=1 {components['nf4_gemv_m1_GBps']} GB/s "
+            f"(planes {components['nf4_planes_gemv_m1_GBps']} GB/s)")
+        del nf, nfc, nfp
 
         # GGUF Q4_0 / Q8_0 GEMV M=1 over the block (gguf.rs block formats, GEMV planes), seeded
         # random blocks with f16 d ~ N(0, 0.003); rotating copies keep the set above the MALL

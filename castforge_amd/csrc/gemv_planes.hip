@@ -1,4 +1,5 @@
-// W4A16 decode GEMV (M = 1..4) over INT4 g128 weights in the GEMV planes layout, gfx950.
+// W4A16 decode GEMV (M = 1..8) over INT4 g128 weights in the GEMV planes layout, and the NF4
+// decode GEMV (M = 1) over NF4 planes (at the end of the device code), gfx950.
 //
 // Replaces the evaluation of `castforge.fused_qmatmul` at decode (eval.rs:1145-1179 with
 // eval_matmul_2d, eval.rs:1465-1507; packed_rhs [N, K] weights, fold.rs:549-554) for the
@@ -404,6 +405,280 @@ void planes_kernel(PBatch b) {
     }
 }
 
+// ---- NF4 over GEMV planes (M = 1) -----------------------------------------------------------
+// NF4 planes.  Codes: the same T x G chunks of 1024 bytes, but the piece of lane (p, r) holds
+// canonical words 16 g + p, 16 g + 4 + p, 16 g + 8 + p, 16 g + 12 + p of row 16 t + r, so that
+// the q-th words of the four parts, which one MFMA takes, are codes 32 q .. 32 q + 31 of the
+// chunk: one block for every block size >= 32.  absmax: f32 [T][G][16][NBPC], NBPC = max(1,
+// 128 / block) values per chunk and row (a block longer than a chunk repeats its absmax in each
+// of its chunks).  Rows past N are zero.
+//
+// The decode table (code byte -> f16 hi and lo of its two codes' table values, 8 bytes, so
+// hi + lo is the f32 table value exactly) is kept in LDS as 32 interleaved copies: lane l reads
+// entry e at (e * 32 + l % 32) * 8, so the 32 lanes an LDS cycle serves hit 32 distinct bank
+// pairs whatever the codes.  The persistent grid writes the 64 KB once per CU.
+#ifndef CFH_NF4_PLANES_DEPTH
+#define CFH_NF4_PLANES_DEPTH 2  // positions in flight per wave (3 and 4 measured slower)
+#endif
+constexpr int kNf4Depth = CFH_NF4_PLANES_DEPTH;
+constexpr int kNf4LutCopies = 32;
+constexpr int kNf4LutBytes = 256 * kNf4LutCopies * 8;
+constexpr float kNf4Values[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f, 0.33791524171829224f,
+    0.44070982933044434f, 0.5626170039176941f, 0.7229568362236023f, 1.0f};
+
+struct NProblem {
+    const uint8_t *codes;
+    const float *absmax;
+    const uint16_t *x;  // bf16 [1, K]
+    void *y;
+    int32_t n, G, units, wg0, wgs, pad;
+};
+
+struct NBatch {
+    NProblem p[CFH_MAX_BATCH];
+    int32_t count, y_bf16;
+};
+
+struct NStage {
+    uint32_t w[4];
+    uint32_t am[4];
+};
+
+// LDS: [decode table, 64 KB][x as f16, G * 256 B][per chunk 2^sh, G * 4 B (16-byte padded)]
+// [partials: tiles x NW x 16 f32]
+template <int NW, int D, int NBPC>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)))
+void nf4_planes_kernel(NBatch b) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = uni(tid >> 6);
+    const int w = blockIdx.x;
+    const int r16 = lane & 15, part = lane >> 4;
+
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < CFH_MAX_BATCH; ++i)
+        if (i < b.count && w >= b.p[i].wg0) pi = i;
+    const NProblem &P = b.p[pi];
+    const int G = P.G, local = w - P.wg0;
+    const int u0 = static_cast<int>(static_cast<uint32_t>(local * P.units) / static_cast<uint32_t>(P.wgs));
+    const int u1 = static_cast<int>(static_cast<uint32_t>((local + 1) * P.units) / static_cast<uint32_t>(P.wgs));
+    const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
+    const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
+    const int ntiles = t1 - t0, npos = ntiles * G;
+    const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2);
+    constexpr uint32_t xoff = kNf4LutBytes;
+    const uint32_t soff = xoff + rowb;
+    const uint32_t aoff = soff + ((static_cast<uint32_t>(G) * 4 + 15) & ~15u);
+    float *const accs = reinterpret_cast<float *>(lds + aoff);
+
+    // the decode table and the partials, before any copy into LDS is in flight
+    for (int i = tid; i < 256 * kNf4LutCopies; i += 64 * NW) {
+        const int e = i / kNf4LutCopies;
+        const float v0 = kNf4Values[e & 15], v1 = kNf4Values[e >> 4];
+        const _Float16 h0 = static_cast<_Float16>(v0), h1 = static_cast<_Float16>(v1);
+        const _Float16 l0 = static_cast<_Float16>(v0 - static_cast<float>(h0));
+        const _Float16 l1 = static_cast<_Float16>(v1 - static_cast<float>(h1));
+        const half2_t hi = {h0, h1}, lo = {l0, l1};
+        reinterpret_cast<uint2 *>(lds)[i] = make_uint2(as_u(hi), as_u(lo));
+    }
+    for (int i = tid; i < ntiles * NW * 16; i += 64 * NW) accs[i] = 0.0f;
+
+    // x (bf16) straight into LDS, 1 KB per wave-wide copy
+    const int nblk = static_cast<int>((rowb + 1023u) / 1024u);
+    for (int i = wave; i < nblk; i += NW) {
+        const uint32_t e = i * 1024u + lane * 16u;
+        if (e < rowb)
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void *>(P.x + (e >> 1)),
+                reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds) + xoff +
+                                                                           i * 1024),
+                16, 0, 0);
+    }
+
+    const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
+    const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
+    const rsrc_t ramax = make_rsrc(P.absmax, chunks * 64u * NBPC);
+    int lt = 0, lg = wave;
+    while (lg >= G) {
+        lg -= G;
+        ++lt;
+    }
+    int pt = lt, pg = lg;
+    // per-lane offsets, pushed out of range (OR kOob) for rows outside [rlo, rhi) and past the
+    // workgroup's tiles; the absmax values multiply the MFMA result, whose rows lanes 0..15 hold
+    uint32_t vcode, vam;
+    auto lane_offsets = [&]() __attribute__((always_inline)) {
+        const int row = (t0 + lt) * 16 + r16;
+        const bool ok = lt < ntiles && row >= rlo && row < rhi;
+        const uint32_t m = ok ? 0u : kOob;
+        vcode = (static_cast<uint32_t>(lane) * 16u) | m;
+        vam = (static_cast<uint32_t>(r16) * (4u * NBPC)) | (lane < 16 ? m : kOob);
+    };
+    lane_offsets();
+    auto load = [&](NStage &st) __attribute__((always_inline)) {
+        const uint32_t chunk = static_cast<uint32_t>((t0 + lt) * G + lg);
+        const uint4 v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, vcode + chunk * 1024u, 0, CFH_PLANES_CPOL));
+        st.w[0] = v.x;
+        st.w[1] = v.y;
+        st.w[2] = v.z;
+        st.w[3] = v.w;
+        const uint32_t ao = vam + chunk * (64u * NBPC);
+        if constexpr (NBPC == 1) {
+            st.am[0] = __builtin_amdgcn_raw_buffer_load_b32(ramax, ao, 0, 0);
+        } else if constexpr (NBPC == 2) {
+            const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ramax, ao, 0, 0));
+            st.am[0] = a.x;
+            st.am[1] = a.y;
+        } else {
+            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ramax, ao, 0, 0));
+            st.am[0] = a.x;
+            st.am[1] = a.y;
+            st.am[2] = a.z;
+            st.am[3] = a.w;
+        }
+        lg += NW;
+        if (lg >= G) {
+            do {
+                lg -= G;
+                ++lt;
+            } while (lg >= G);
+            lane_offsets();
+        }
+    };
+    NStage st[D];
+    static_for<D>([&](auto i) __attribute__((always_inline)) {
+        load(st[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    lds_barrier<2 * D>();  // this wave's copies of x have landed; the table is written
+
+    // x to f16 in natural order, each chunk of 128 scaled by the power of two that brings its
+    // largest |x| into [2^14, 2^15) (every finite bf16 is then exact in f16 down to 2^-38 of
+    // that value); 2^sh is kept per chunk.  Eight lanes (16 values each) hold one chunk.
+    {
+        const int total = G * 8;
+        for (int base = 0; base < total; base += 64 * NW) {  // uniform trip count
+            const int i = base + tid;
+            const bool act = i < total;
+            const int j = act ? i : 0;
+            uint16_t *px = reinterpret_cast<uint16_t *>(lds + xoff) + j * 16;
+            const uint4 r0 = *reinterpret_cast<const uint4 *>(px);
+            const uint4 r1 = *reinterpret_cast<const uint4 *>(px + 8);
+            const uint32_t wv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+            uint32_t emax = 0;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                emax = max(emax, (wv[q] >> 7) & 0xFFu);
+                emax = max(emax, (wv[q] >> 23) & 0xFFu);
+            }
+            {
+                int e = static_cast<int>(emax);
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0xB1, 0xF, 0xF, false));
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x4E, 0xF, 0xF, false));
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x141, 0xF, 0xF, false));
+                emax = static_cast<uint32_t>(e);
+            }
+            int sh = static_cast<int>(emax) - 127 - 14;
+            sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
+            const float pre = __uint_as_float(static_cast<uint32_t>(127 - sh) << 23);
+            const float post = __uint_as_float(static_cast<uint32_t>(127 + sh) << 23);
+            uint32_t o[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float f0 = __uint_as_float(wv[q] << 16) * pre;
+                const float f1 = __uint_as_float(wv[q] & 0xffff0000u) * pre;
+                o[q] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f0))) |
+                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f1))) << 16);
+            }
+            if (act) {
+                *reinterpret_cast<uint4 *>(px) = make_uint4(o[0], o[1], o[2], o[3]);
+                *reinterpret_cast<uint4 *>(px + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+                if ((i & 7) == 0) reinterpret_cast<float *>(lds + soff)[j >> 3] = post;
+            }
+        }
+    }
+    lds_barrier<63>();
+
+    const uint32_t lbase = static_cast<uint32_t>(lane & (kNf4LutCopies - 1)) * 8u;  // < 256
+    // table entry of byte B of word v for this lane, at (byte * 32 + lane % 32) * 8: one byte
+    // permute puts the byte at bits 8..15 and the lane's copy offset at bits 0..7
+    auto entry = [&](uint32_t v, auto B) __attribute__((always_inline)) {
+        constexpr uint32_t sel = 0x0C0C0000u | ((4u + decltype(B)::value) << 8);
+        return *reinterpret_cast<const uint2 *>(lds + __builtin_amdgcn_perm(v, lbase, sel));
+    };
+    float acc = 0.0f;
+    const int steps = npos > wave ? (npos - wave + NW - 1) / NW : 0;
+    for (int k = 0; k < steps; k += D) {
+        static_for<D>([&](auto ii) __attribute__((always_inline)) {
+            constexpr int i = decltype(ii)::value;
+            const bool live = pt < ntiles;
+            const NStage &s = st[i];
+            const int g = live ? pg : 0;
+            // A fragment of MFMA q: x[128 g + 32 q + 8 p .. + 7]
+            const uint8_t *xa = lds + xoff + g * (kGroup * 2) + part * 16;
+            const float post = reinterpret_cast<const float *>(lds + soff)[g];
+            // one accumulation chain per block of the chunk (two for a single block, to halve the
+            // MFMA dependency latency)
+            constexpr int NC = NBPC == 1 ? 2 : NBPC;
+            floatx4 c[NC];
+#pragma unroll
+            for (int j = 0; j < NC; ++j) c[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const half8_t a = *reinterpret_cast<const half8_t *>(xa + 64 * q);
+                const uint32_t wq = s.w[q];
+                const uint2 e0 = entry(wq, std::integral_constant<uint32_t, 0>{});
+                const uint2 e1 = entry(wq, std::integral_constant<uint32_t, 1>{});
+                const uint2 e2 = entry(wq, std::integral_constant<uint32_t, 2>{});
+                const uint2 e3 = entry(wq, std::integral_constant<uint32_t, 3>{});
+                const int j = NBPC == 1 ? (q & 1) : q * NBPC / 4;
+                c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pack8(e0.x, e1.x, e2.x, e3.x), c[j], 0, 0, 0);
+                c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pack8(e0.y, e1.y, e2.y, e3.y), c[j], 0, 0, 0);
+            }
+            float v;
+            if constexpr (NBPC == 1) {
+                v = __fmul_rn(__fmul_rn(c[0][0] + c[1][0], __uint_as_float(s.am[0])), post);
+            } else {
+                float t = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NBPC; ++j) t = __fadd_rn(t, __fmul_rn(c[j][0], __uint_as_float(s.am[j])));
+                v = __fmul_rn(t, post);
+            }
+            acc = __fadd_rn(acc, live ? v : 0.0f);
+            const int tile = pt;
+            pg += NW;
+            while (pg >= G) {
+                pg -= G;
+                ++pt;
+            }
+            if (live && pt != tile) {
+                if (lane < 16) accs[(tile * NW + wave) * 16 + lane] = acc;
+                acc = 0.0f;
+            }
+            load(st[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    lds_barrier<63>();
+
+    for (int i = tid; i < ntiles * 16; i += 64 * NW) {
+        const int row = (t0 + (i >> 4)) * 16 + (i & 15);
+        if (row >= rlo && row < rhi) {
+            const float *pa = accs + (i >> 4) * NW * 16 + (i & 15);
+            float v = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) v += pa[w2 * 16];
+            if (b.y_bf16) static_cast<uint16_t *>(P.y)[row] = f32_to_bf16_rne(v);
+            else static_cast<float *>(P.y)[row] = v;
+        }
+    }
+}
+
 // ---- canonical <-> planes ------------------------------------------------------------------
 // One thread per 16-byte unit of the codes planes / per (tile, group, row) of the metadata.
 __global__ void to_planes_kernel(const uint32_t *codes, const uint16_t *scales, const uint32_t *zeros, int64_t n,
@@ -451,6 +726,53 @@ __global__ void from_planes_kernel(const uint8_t *pc, const uint16_t *ps, const 
             scales[row * GP + gg] = sv;
         }
         zeros[row * ZW + g / 8] = zw;
+    }
+}
+
+// NF4 canonical (codes u32 [N, K/8], absmax f32 [N, K/block]) <-> NF4 planes; nbpc =
+// max(1, 128 / block) absmax values per chunk and row.  One thread per 16-byte piece.
+__global__ void nf4_to_planes_kernel(const uint32_t *codes, const float *absmax, int64_t n, int64_t k,
+                                     int64_t block, uint8_t *pc, float *pa) {
+    const int64_t G = k / kGroup, T = (n + 15) / 16, NB = (k + block - 1) / block;
+    const int64_t nbpc = block >= kGroup ? 1 : kGroup / block;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (u >= T * G * 64) return;
+    const int64_t chunk = u >> 6, l = u & 63;
+    const int64_t t = chunk / G, g = chunk % G, p = l >> 4, r = l & 15, row = t * 16 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < n) {
+        const uint32_t *src = codes + row * (k / 8) + 16 * g + p;
+        v = make_uint4(src[0], src[4], src[8], src[12]);
+    }
+    *reinterpret_cast<uint4 *>(pc + u * 16) = v;
+    if (p == 0) {
+        for (int64_t j = 0; j < nbpc; ++j) {
+            const int64_t blk = block >= kGroup ? (g * kGroup) / block : g * nbpc + j;
+            pa[(chunk * 16 + r) * nbpc + j] = row < n ? absmax[row * NB + blk] : 0.0f;
+        }
+    }
+}
+
+__global__ void nf4_from_planes_kernel(const uint8_t *pc, const float *pa, int64_t n, int64_t k, int64_t block,
+                                       uint32_t *codes, float *absmax) {
+    const int64_t G = k / kGroup, NB = (k + block - 1) / block;
+    const int64_t nbpc = block >= kGroup ? 1 : kGroup / block;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // over n * G * 4
+    if (u >= n * G * 4) return;
+    const int64_t row = u / (G * 4), c = u % (G * 4), g = c / 4, p = c % 4, t = row / 16, r = row % 16;
+    const int64_t chunk = t * G + g;
+    const uint4 v = *reinterpret_cast<const uint4 *>(pc + (chunk * 64 + p * 16 + r) * 16);
+    uint32_t *dst = codes + row * (k / 8) + 16 * g + p;
+    dst[0] = v.x;
+    dst[4] = v.y;
+    dst[8] = v.z;
+    dst[12] = v.w;
+    if (p == 0) {
+        for (int64_t j = 0; j < nbpc; ++j) {
+            const int64_t blk = block >= kGroup ? (g * kGroup) / block : g * nbpc + j;
+            // a block longer than a chunk is written by the thread of its first chunk
+            if (block < kGroup || (g * kGroup) % block == 0) absmax[row * NB + blk] = pa[(chunk * 16 + r) * nbpc + j];
+        }
     }
 }
 
@@ -612,6 +934,95 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
     else launch_planes<CFH_PLANES_WAVES8, CFH_PLANES_DEPTH8, 8>(b, grid, req, st);
 }
 
+template <int NBPC>
+void launch_nf4_planes(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
+    static std::mutex mu;
+    static std::map<int, bool> attr_set;  // per device
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    {
+        std::lock_guard<std::mutex> g(mu);
+        if (!attr_set[dev]) {
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&nf4_planes_kernel<kWaves, kNf4Depth, NBPC>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
+                      "hipFuncSetAttribute");
+            attr_set[dev] = true;
+        }
+    }
+    nf4_planes_kernel<kWaves, kNf4Depth, NBPC>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), static_cast<size_t>(lds), st>>>(b);
+    check_launch("nf4_planes_kernel");
+}
+
+bool nf4_block_ok(int64_t block) { return block >= 32 && block <= (int64_t(1) << 20) && (block & (block - 1)) == 0; }
+
+// NF4 decode GEMV (M = 1) over NF4 planes: one workgroup of 16 waves per CU, problems sharing
+// the CUs in proportion to their bytes (as the INT4 planes kernel).
+void nf4_planes_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
+                        hipStream_t st) {
+    require(count >= 1 && count <= CFH_MAX_BATCH, "count must be in 1..8");
+    require(problems != nullptr, "problems must not be NULL");
+    require(m == 1, "the NF4 planes kernel takes M = 1");
+    require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+    const int64_t block = problems[0].block;
+    require(nf4_block_ok(block), "NF4 block must be a power of two >= 32");
+    const int64_t nbpc = block >= kGroup ? 1 : kGroup / block;
+    const int W = cu_count();
+    std::vector<int64_t> bytes, units;
+    for (int i = 0; i < count; ++i) {
+        const cfh_nf4_problem_t &q = problems[i];
+        require(q.block == block, "every problem of a batch must have the same NF4 block");
+        require(q.n >= 1 && q.k >= kGroup && q.k % kGroup == 0, "NF4 planes need n >= 1 and k % 128 == 0");
+        require(q.x && q.codes && q.absmax && q.y, "x, planes and y must not be NULL");
+        require(aligned(q.x, 16) && aligned(q.codes, 16) && aligned(q.absmax, 4 * nbpc) && aligned(q.y, 4),
+                "x and codes planes must be 16-byte aligned, absmax planes aligned to their per-row values, "
+                "y 4-byte aligned");
+        require(((q.n + 15) / 16) * (q.k / kGroup) * 1024 < (int64_t(1) << 31),
+                "NF4 planes of one matrix must stay below 2 GiB");
+        bytes.push_back(((q.n + 15) / 16) * (q.k / kGroup) * (1024 + 64 * nbpc));
+        units.push_back((q.n + 7) / 8);
+    }
+    const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+    NBatch b{};
+    int64_t lds_max = 0, grid = 0;
+    for (int j = 0; j < count; ++j) {
+        const cfh_nf4_problem_t &q = problems[j];
+        NProblem &P = b.p[j];
+        P.codes = reinterpret_cast<const uint8_t *>(q.codes);
+        P.absmax = q.absmax;
+        P.x = q.x;
+        P.y = q.y;
+        P.n = static_cast<int32_t>(q.n);
+        P.G = static_cast<int32_t>(q.k / kGroup);
+        P.units = static_cast<int32_t>(units[j]);
+        P.wg0 = static_cast<int32_t>(grid);
+        P.wgs = wgs[j];
+        require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
+        grid += P.wgs;
+        const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
+        const int64_t need = kNf4LutBytes + int64_t(P.G) * 256 + (int64_t(P.G) * 4 + 15) / 16 * 16 + tiles * kWaves * 64;
+        lds_max = std::max<int64_t>(lds_max, need);
+    }
+    b.count = count;
+    b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
+    require(lds_max <= kLdsMax, "a problem of the batch exceeds the NF4 planes kernel's LDS (k too large)");
+    if (nbpc == 1) launch_nf4_planes<1>(b, grid, lds_max, st);
+    else if (nbpc == 2) launch_nf4_planes<2>(b, grid, lds_max, st);
+    else launch_nf4_planes<4>(b, grid, lds_max, st);
+}
+
+void nf4_planes_checks(const void *codes, const void *absmax, int64_t rows, int64_t k, int64_t block, const void *pc,
+                       const void *pa) {
+    require(nf4_block_ok(block), "NF4 block must be a power of two >= 32");
+    require(rows >= 0 && k >= 0 && k % kGroup == 0, "rows >= 0 and k % 128 == 0 are required");
+    if (rows > 0 && k > 0) {
+        require(codes && absmax && pc && pa, "buffers must not be NULL");
+        require(aligned(codes, 4) && aligned(pc, 16), "codes must be 4-byte and codes planes 16-byte aligned");
+        require(aligned(absmax, 4) && aligned(pa, 4), "absmax arrays must be 4-byte aligned");
+        require(((rows + 15) / 16) * (k / kGroup) * 1024 < (int64_t(1) << 31), "planes must stay below 2 GiB");
+    }
+}
+
 void planes_checks(const void *codes, const void *scales, const void *zeros, int64_t rows, int64_t k,
                    int64_t group, const void *pc, const void *ps, const void *pz) {
     require(group == kGroup, "GEMV planes hold INT4 groups of 128");
@@ -666,6 +1077,38 @@ int32_t castforge_hip_int4g_from_planes(const void *planes_codes, const uint16_t
 int32_t castforge_hip_gemv_w4a16_planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m,
                                                 int32_t y_dtype, void *stream, char **out_error) {
     return guarded(out_error, [&] { planes_batched(problems, count, m, y_dtype, static_cast<hipStream_t>(stream)); });
+}
+
+int32_t castforge_hip_nf4_to_planes(const uint32_t *codes, const float *absmax, int64_t rows, int64_t k,
+                                    int64_t block, void *planes_codes, float *planes_absmax, void *stream,
+                                    char **out_error) {
+    return guarded(out_error, [&] {
+        nf4_planes_checks(codes, absmax, rows, k, block, planes_codes, planes_absmax);
+        const int64_t units = ((rows + 15) / 16) * (k / kGroup) * 64;
+        if (units == 0) return;
+        nf4_to_planes_kernel<<<dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0,
+                               static_cast<hipStream_t>(stream)>>>(codes, absmax, rows, k, block,
+                                                                   static_cast<uint8_t *>(planes_codes), planes_absmax);
+        check_launch("nf4_to_planes_kernel");
+    });
+}
+
+int32_t castforge_hip_nf4_from_planes(const void *planes_codes, const float *planes_absmax, int64_t rows, int64_t k,
+                                      int64_t block, uint32_t *codes, float *absmax, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        nf4_planes_checks(codes, absmax, rows, k, block, planes_codes, planes_absmax);
+        const int64_t units = rows * (k / kGroup) * 4;
+        if (units == 0) return;
+        nf4_from_planes_kernel<<<dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0,
+                                 static_cast<hipStream_t>(stream)>>>(static_cast<const uint8_t *>(planes_codes),
+                                                                     planes_absmax, rows, k, block, codes, absmax);
+        check_launch("nf4_from_planes_kernel");
+    });
+}
+
+int32_t castforge_hip_gemv_nf4_planes_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_t m,
+                                              int32_t y_dtype, void *stream, char **out_error) {
+    return guarded(out_error, [&] { nf4_planes_batched(problems, count, m, y_dtype, static_cast<hipStream_t>(stream)); });
 }
 
 }  // extern "C"

@@ -119,6 +119,9 @@ SIGNATURES = {
     "castforge_hip_int4g_from_planes": (c_int32, [_P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _E]),
     "castforge_hip_gemv_w4a16_planes_batched": (c_int32, [POINTER(W4A16Problem), c_int32, c_int64, c_int32, _P, _E]),
     "castforge_hip_gemv_nf4_batched": (c_int32, [POINTER(Nf4Problem), c_int32, c_int64, c_int32, _P, _E]),
+    "castforge_hip_nf4_to_planes": (c_int32, [_P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _E]),
+    "castforge_hip_nf4_from_planes": (c_int32, [_P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _E]),
+    "castforge_hip_gemv_nf4_planes_batched": (c_int32, [POINTER(Nf4Problem), c_int32, c_int64, c_int32, _P, _E]),
     "castforge_hip_quantize_int4g_batched": (c_int32, [POINTER(QuantProblem), c_int32, c_int64, _P, _E]),
     "castforge_hip_quantize_int4g_awq_batched": (c_int32, [POINTER(QuantProblem), POINTER(_P), c_int32, c_int64, _P,
                                                            _E]),

@@ -417,6 +417,72 @@ def gemv_nf4_batched(xs: list[torch.Tensor], ps: list["Nf4Packed"], ys: list[tor
     ffi.call("castforge_hip_gemv_nf4_batched", arr, len(ps), m, yd, _stream(xs[0]))
 
 
+@dataclass
+class Nf4Planes:
+    """NF4 weights in the GEMV planes layout (castforge_hip_nf4_to_planes): codes u8
+    [T * G * 1024], absmax f32 [T, G, 16, nbpc] with T = ceil(N/16), G = K/128 and
+    nbpc = max(1, 128 / block)."""
+    codes: torch.Tensor
+    absmax: torch.Tensor
+    n: int
+    k: int
+    block: int
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.codes, self.absmax))
+
+
+def _nf4_planes_block_ok(block: int) -> bool:
+    return block >= 32 and block & (block - 1) == 0
+
+
+def nf4_to_planes(p: Nf4Packed) -> Nf4Planes:
+    """The GEMV planes of canonical NF4 weights (built once, at load time)."""
+    if p.k % 128 or not _nf4_planes_block_ok(p.block):
+        raise ValueError("NF4 planes need k % 128 == 0 and a power-of-two block >= 32")
+    t, g = (p.n + 15) // 16, p.k // 128
+    nbpc = max(1, 128 // p.block)
+    dev = p.codes.device
+    pl = Nf4Planes(torch.empty(t * g * 1024, dtype=torch.uint8, device=dev),
+                   torch.empty((t, g, 16, nbpc), dtype=torch.float32, device=dev), p.n, p.k, p.block)
+    ffi.call("castforge_hip_nf4_to_planes", _ptr(_dev(p.codes)), _ptr(_dev(p.absmax)), p.n, p.k, p.block,
+             _ptr(pl.codes), _ptr(pl.absmax), _stream(p.codes))
+    return pl
+
+
+def nf4_from_planes(pl: Nf4Planes) -> Nf4Packed:
+    """Canonical NF4 codes and absmax back from NF4 planes (bit for bit)."""
+    n, k, block = pl.n, pl.k, pl.block
+    dev = pl.codes.device
+    p = Nf4Packed(torch.empty((n, k // 8), dtype=torch.int32, device=dev),
+                  torch.empty((n, (k + block - 1) // block), dtype=torch.float32, device=dev), n, k, block)
+    ffi.call("castforge_hip_nf4_from_planes", _ptr(_dev(pl.codes)), _ptr(_dev(pl.absmax)), n, k, block,
+             _ptr(p.codes), _ptr(p.absmax), _stream(pl.codes))
+    return p
+
+
+def gemv_nf4_planes_batched(xs: list[torch.Tensor], ps: list[Nf4Planes], ys: list[torch.Tensor]) -> None:
+    """NF4 decode (x of one row) over NF4 planes, all problems in one launch (one workgroup per
+    CU); every problem has the same block size."""
+    if not (len(xs) == len(ps) == len(ys)) or not 1 <= len(ps) <= ffi.MAX_BATCH:
+        raise ValueError("xs, ps, ys must have the same length in 1..8")
+    m = xs[0].shape[0] if xs[0].dim() == 2 else 0
+    if m != 1:
+        raise ValueError("the NF4 planes kernel takes x of one row")
+    yd = _check_batch(xs, ys, m, [p.n for p in ps], [p.k for p in ps])
+    arr = (ffi.Nf4Problem * len(ps))()
+    for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
+        arr[i] = ffi.Nf4Problem(_ptr(x), _ptr(p.codes), _ptr(p.absmax), _ptr(y), p.n, p.k, p.block)
+    ffi.call("castforge_hip_gemv_nf4_planes_batched", arr, len(ps), m, yd, _stream(xs[0]))
+
+
+def gemv_nf4_planes(x: torch.Tensor, p: Nf4Planes, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """y [1, n] for x bf16 [1, k] over NF4 planes."""
+    y = torch.empty((1, p.n), dtype=out_dtype, device=x.device)
+    gemv_nf4_planes_batched([x], [p], [y])
+    return y
+
+
 # -------------------------------------------------------------- outlier suppression ----
 def rotate_hadamard(w: torch.Tensor, block: int, axis: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
     """Walsh-Hadamard rotation of f32 [d0, d1] in blocks of `block` along `axis` (0: down the

@@ -278,6 +278,34 @@ typedef struct cfh_nf4_problem_t {
 int32_t castforge_hip_gemv_nf4_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_t m,
                                        int32_t y_dtype, void *stream, char **out_error);
 
+/* NF4 GEMV planes: the layout of NF4 weights (block a power of two >= 32, K % 128 == 0) that
+ * the M = 1 kernel below streams, built once at load time (no reference counterpart: the
+ * reference keeps one i8 code per element, ir/tensor_store.rs:44-48).  T = ceil(N/16), G = K/128:
+ *   planes_codes : T x G chunks of 1024 bytes; chunk (t, g) holds, at byte 16 * (16 p + r),
+ *                  canonical code words 16 g + p, 16 g + 4 + p, 16 g + 8 + p, 16 g + 12 + p of
+ *                  row 16 t + r (p = 0..3), so that the q-th words of the four parts are codes
+ *                  32 q .. 32 q + 31 of the chunk;
+ *   planes_absmax: f32 [T][G][16][nbpc], nbpc = max(1, 128 / block): the absmax of row
+ *                  16 t + r for the blocks of chunk g (a block longer than 128 codes repeats its
+ *                  absmax in each of its chunks).
+ * Rows past N are zero.  from_planes restores the canonical codes u32 [N, K/8] and absmax f32
+ * [N, K/block] bit for bit.  planes_codes 16-byte aligned. */
+int32_t castforge_hip_nf4_to_planes(const uint32_t *codes, const float *absmax, int64_t rows, int64_t k,
+                                    int64_t block, void *planes_codes, float *planes_absmax, void *stream,
+                                    char **out_error);
+int32_t castforge_hip_nf4_from_planes(const void *planes_codes, const float *planes_absmax, int64_t rows, int64_t k,
+                                      int64_t block, uint32_t *codes, float *absmax, void *stream, char **out_error);
+
+/* castforge_hip_gemv_nf4_batched at M = 1 over NF4 planes (codes / absmax of each problem point
+ * at its planes; one block size for the batch; x [1, k] and codes 16-byte aligned): the decode
+ * GEMV of `castforge.fused_qmatmul` over NF4 weights (codegen/eval.rs:1145-1179, eval_matmul_2d
+ * eval.rs:1465-1507, the NF4 dequant of schemes.rs) in one launch of one workgroup per CU.  The
+ * weight operands are the exact f16 hi + lo pair of each table value; x is handled as in
+ * castforge_hip_gemv_w4a16_planes_batched (power-of-two pre-scale per 128 activations).  A
+ * problem's activations must fit LDS next to the 64 KB decode table (k up to about 40000). */
+int32_t castforge_hip_gemv_nf4_planes_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_t m,
+                                              int32_t y_dtype, void *stream, char **out_error);
+
 /* FP8 E4M3 W8A8 GEMM: y[m, n] = (sum_k e4m3(qa[m,k]) * e4m3(qw[n,k])) * sa[m] * sw[n], stored
  * as bf16 (RNE) or f32 per y_dtype.
  * qa/sa come from castforge_hip_quantize_fp8 on the activations (per token), qw/sw on the
