@@ -563,13 +563,38 @@ __device__ __forceinline__ void hadamard16_lanes(float (&x)[16], int rot_b, floa
 // One cross-lane stage in the hsub16 layout: the partner's value (DPP control CTRL) times
 // c = +1 on the lane whose sub-block has the stage's bit clear, -1 on the other, plus the
 // lane's own value.
+#ifndef CFH_HSTAGE_ASM
+#define CFH_HSTAGE_ASM 1
+#endif
+// One v_fmac_f32 per value with the partner read through DPP (x = partner * c + x, the same
+// fused multiply-add as fmaf): the compiler's DPP combine does not fold a DPP move into an
+// fmac, whose accumulator is tied to its result, and would spend two instructions.  s_nop 1
+// gives the two wait states a DPP read needs after a VALU write of its source; inside the
+// block each value's source was written 16 instructions before.  CTL: the DPP control.
+#define CFH_HS(i, CTL) "v_fmac_f32_dpp %" #i ", %" #i ", %16 " CTL " row_mask:0xf bank_mask:0xf\n"
+#define CFH_HSTAGE_BLOCK(CTL)                                                                          \
+    asm volatile("s_nop 1\n" CFH_HS(0, CTL) CFH_HS(1, CTL) CFH_HS(2, CTL) CFH_HS(3, CTL) CFH_HS(4, CTL)      \
+                 CFH_HS(5, CTL) CFH_HS(6, CTL) CFH_HS(7, CTL) CFH_HS(8, CTL) CFH_HS(9, CTL) CFH_HS(10, CTL)   \
+                 CFH_HS(11, CTL) CFH_HS(12, CTL) CFH_HS(13, CTL) CFH_HS(14, CTL) CFH_HS(15, CTL)            \
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]),    \
+                   "+v"(x[7]), "+v"(x[8]), "+v"(x[9]), "+v"(x[10]), "+v"(x[11]), "+v"(x[12]), "+v"(x[13]), \
+                   "+v"(x[14]), "+v"(x[15])                                                             \
+                 : "v"(c))
 template <int CTRL>
 __device__ __forceinline__ void hstage16(float (&x)[16], float c) {
+    static_assert(CTRL == 0xB1 || CTRL == 0x4E || CTRL == 0x141 || CTRL == 0x128, "DPP control");
+#if CFH_HSTAGE_ASM
+    if constexpr (CTRL == 0xB1) CFH_HSTAGE_BLOCK("quad_perm:[1,0,3,2]");
+    else if constexpr (CTRL == 0x4E) CFH_HSTAGE_BLOCK("quad_perm:[2,3,0,1]");
+    else if constexpr (CTRL == 0x141) CFH_HSTAGE_BLOCK("row_half_mirror");
+    else CFH_HSTAGE_BLOCK("row_ror:8");
+#else
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const float p = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x[i]), CTRL, 0xF, 0xF, false));
         x[i] = __builtin_fmaf(p, c, x[i]);
     }
+#endif
 }
 
 // hadamard16_lanes for blocks of 32 .. 256 values in the hsub16 layout (thread t holds
