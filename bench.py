@@ -379,6 +379,13 @@ def main():
             gb = sum(p.nbytes() + 2 * p.k + 2 * p.n for p in gc[0])
             components[f"gguf_{tag}_gemv_m1_GBps"] = round(gb / (st * 1e-3) / 1e9, 1)
             log(f"[bench] GGUF {tag} GEMV M=1: {st * 1e3:.1f} us, {components[f'gguf_{tag}_gemv_m1_GBps']} GB/s")
+            if ty == 2:  # the same launch over Q4_0 GEMV planes (same algorithmic bytes)
+                gpl = [[ops.gguf_q4_0_to_gemv_planes(p) for p in row] for row in gc]
+                st = time_steps(lambda i: ops.gemv_gguf_q4_0_planes_batched(xs8, gpl[i % len(gpl)], ysg), 50, 5)
+                components["gguf_q4_0_planes_gemv_m1_GBps"] = round(gb / (st * 1e-3) / 1e9, 1)
+                log(f"[bench] GGUF q4_0 GEMV M=1 over Q4_0 GEMV planes: {st * 1e3:.1f} us, "
+                    f"{components['gguf_q4_0_planes_gemv_m1_GBps']} GB/s")
+                del gpl
             del gc, ysg
 
         # prefill GEMMs on MFMA: W4A16 INT4 g128 at M=4096 (config 5 follow-on) and NF4 b64 at
@@ -504,7 +511,7 @@ def main():
                    "value_is": "W4A16 GEMV GB/s at M=1 (algorithmic bytes / whole-job time per step)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "planes_kernel<16, 3, 1>", "bytes_per_launch": bytes_m1,
+                     "kernel": "planes_m1_kernel<16, 2, 1, 2>", "bytes_per_launch": bytes_m1,
                      "us_per_launch": round(ms_step * 1e3, 2), "timing": timing},
         "cpu_baseline": cpu,
         "components": components,

@@ -421,6 +421,13 @@ void planes_kernel(PBatch b) {
 #define CFH_NF4_PLANES_DEPTH 2  // positions in flight per wave (3 and 4 measured slower)
 #endif
 constexpr int kNf4Depth = CFH_NF4_PLANES_DEPTH;
+#ifndef CFH_PLANES_I4_DEPTH
+#define CFH_PLANES_I4_DEPTH 2  // the INT4 kind of the kernel below (M = 1 over INT4 GEMV planes)
+#endif
+constexpr int kI4Depth = CFH_PLANES_I4_DEPTH;
+#ifndef CFH_PLANES_M1_GENERIC
+#define CFH_PLANES_M1_GENERIC 1  // M = 1 over INT4 GEMV planes on planes_m1_kernel (0: planes_kernel)
+#endif
 constexpr int kNf4LutCopies = 32;
 constexpr int kNf4LutBytes = 256 * kNf4LutCopies * 8;
 constexpr float kNf4Values[16] = {
@@ -431,11 +438,18 @@ constexpr float kNf4Values[16] = {
 
 struct NProblem {
     const uint8_t *codes;
-    const float *absmax;
-    const uint16_t *x;  // bf16 [1, K]
+    const float *absmax;   // NF4: absmax planes; Q4_0: d planes; INT4: scale planes
+    const uint8_t *zeros;  // INT4: zero-point planes
+    const uint16_t *x;     // bf16 [1, K]
     void *y;
     int32_t n, G, units, wg0, wgs, pad;
 };
+static_assert(sizeof(NProblem) == 64, "one problem record, 64 bytes");
+
+// what planes_m1_kernel decodes
+constexpr int kKindNf4 = 0;   // NF4 planes, table decode
+constexpr int kKindQ40 = 1;   // GGUF Q4_0 GEMV planes, exact q - 8
+constexpr int kKindInt4 = 2;  // INT4 g128 GEMV planes, exact q - z (the M = 1 form of planes_kernel)
 
 struct NBatch {
     NProblem p[CFH_MAX_BATCH];
@@ -447,11 +461,19 @@ struct NStage {
     uint32_t am[4];
 };
 
-// LDS: [decode table, 64 KB][x as f16, G * 256 B][per chunk 2^sh, G * 4 B (16-byte padded)]
-// [partials: tiles x NW x 16 f32]
-template <int NW, int D, int NBPC>
+// LDS: [decode table, 64 KB (NF4 only)][x as f16, G * 256 B][per chunk 2^sh, G * 4 B (16-byte
+// padded)][partials: tiles x NW x 16 f32]
+// Q40: the GGUF Q4_0 form over Q4_0 GEMV planes (below): codes decoded to the exact f16
+// q - 8 like INT4, one f16 d per block of 32 (NBPC = 4 blocks per chunk), x in the INT4
+// decode's order.
+// INT4 (NBPC = 1): the INT4 g128 GEMV planes (planes_kernel's layout and arithmetic at M = 1,
+// bit for bit: per chunk two MFMA chains over words 0, 2 and 1, 3, then RN(RN(pa + pb) * RN(s *
+// post))), with x in the INT4 decode's order.
+template <int NW, int D, int NBPC, int KIND = kKindNf4>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)))
-void nf4_planes_kernel(NBatch b) {
+void planes_m1_kernel(NBatch b) {
+    constexpr bool Q40 = KIND == kKindQ40, I4 = KIND == kKindInt4;
+    static_assert(!I4 || NBPC == 1, "INT4: one group per chunk");
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = uni(tid >> 6);
@@ -470,13 +492,13 @@ void nf4_planes_kernel(NBatch b) {
     const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
     const int ntiles = t1 - t0, npos = ntiles * G;
     const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2);
-    constexpr uint32_t xoff = kNf4LutBytes;
+    constexpr uint32_t xoff = KIND == kKindNf4 ? kNf4LutBytes : 0u;
     const uint32_t soff = xoff + rowb;
     const uint32_t aoff = soff + ((static_cast<uint32_t>(G) * 4 + 15) & ~15u);
     float *const accs = reinterpret_cast<float *>(lds + aoff);
 
     // the decode table and the partials, before any copy into LDS is in flight
-    for (int i = tid; i < 256 * kNf4LutCopies; i += 64 * NW) {
+    for (int i = tid; i < (KIND == kKindNf4 ? 256 * kNf4LutCopies : 0); i += 64 * NW) {
         const int e = i / kNf4LutCopies;
         const float v0 = kNf4Values[e & 15], v1 = kNf4Values[e >> 4];
         const _Float16 h0 = static_cast<_Float16>(v0), h1 = static_cast<_Float16>(v1);
@@ -501,7 +523,9 @@ void nf4_planes_kernel(NBatch b) {
 
     const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
     const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
-    const rsrc_t ramax = make_rsrc(P.absmax, chunks * 64u * NBPC);
+    constexpr uint32_t kMetaRow = Q40 ? 8u : I4 ? 2u : 4u * NBPC;  // metadata bytes per row and chunk
+    const rsrc_t ramax = make_rsrc(P.absmax, chunks * 16u * kMetaRow);
+    const rsrc_t rzero = make_rsrc(P.zeros, I4 ? chunks * 8u : 0u);
     int lt = 0, lg = wave;
     while (lg >= G) {
         lg -= G;
@@ -510,13 +534,15 @@ void nf4_planes_kernel(NBatch b) {
     int pt = lt, pg = lg;
     // per-lane offsets, pushed out of range (OR kOob) for rows outside [rlo, rhi) and past the
     // workgroup's tiles; the absmax values multiply the MFMA result, whose rows lanes 0..15 hold
-    uint32_t vcode, vam;
+    // (INT4: every lane needs its row's zero point for the exact q - z decode)
+    uint32_t vcode, vam, vzero;
     auto lane_offsets = [&]() __attribute__((always_inline)) {
         const int row = (t0 + lt) * 16 + r16;
         const bool ok = lt < ntiles && row >= rlo && row < rhi;
         const uint32_t m = ok ? 0u : kOob;
         vcode = (static_cast<uint32_t>(lane) * 16u) | m;
-        vam = (static_cast<uint32_t>(r16) * (4u * NBPC)) | (lane < 16 ? m : kOob);
+        vam = (static_cast<uint32_t>(r16) * kMetaRow) | (lane < 16 ? m : kOob);
+        vzero = static_cast<uint32_t>(r16 >> 1) | m;
     };
     lane_offsets();
     auto load = [&](NStage &st) __attribute__((always_inline)) {
@@ -527,8 +553,15 @@ void nf4_planes_kernel(NBatch b) {
         st.w[1] = v.y;
         st.w[2] = v.z;
         st.w[3] = v.w;
-        const uint32_t ao = vam + chunk * (64u * NBPC);
-        if constexpr (NBPC == 1) {
+        const uint32_t ao = vam + chunk * (16u * kMetaRow);
+        if constexpr (I4) {  // the group's f16 scale (lanes 0..15) and zero-point byte (all lanes)
+            st.am[0] = __builtin_amdgcn_raw_buffer_load_b16(ramax, ao, 0, 0);
+            st.am[1] = __builtin_amdgcn_raw_buffer_load_b8(rzero, vzero + chunk * 8u, 0, 0);
+        } else if constexpr (Q40) {  // the 4 blocks' f16 d
+            const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ramax, ao, 0, 0));
+            st.am[0] = a.x;
+            st.am[1] = a.y;
+        } else if constexpr (NBPC == 1) {
             st.am[0] = __builtin_amdgcn_raw_buffer_load_b32(ramax, ao, 0, 0);
         } else if constexpr (NBPC == 2) {
             const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ramax, ao, 0, 0));
@@ -555,7 +588,7 @@ void nf4_planes_kernel(NBatch b) {
         load(st[i]);
         __builtin_amdgcn_sched_barrier(0);
     });
-    lds_barrier<2 * D>();  // this wave's copies of x have landed; the table is written
+    lds_barrier<(I4 ? 3 : 2) * D>();  // this wave's copies of x have landed; the table is written
 
     // x to f16 in natural order, each chunk of 128 scaled by the power of two that brings its
     // largest |x| into [2^14, 2^15) (every finite bf16 is then exact in f16 down to 2^-38 of
@@ -587,11 +620,15 @@ void nf4_planes_kernel(NBatch b) {
             sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
             const float pre = __uint_as_float(static_cast<uint32_t>(127 - sh) << 23);
             const float post = __uint_as_float(static_cast<uint32_t>(127 + sh) << 23);
+            // NF4: natural order; Q4_0: per 8 values the pairs (0, 4), (1, 5), (2, 6), (3, 7) of
+            // the INT4 decode
+            constexpr int kPerm[16] = {0, 4, 1, 5, 2, 6, 3, 7, 8, 12, 9, 13, 10, 14, 11, 15};
             uint32_t o[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const float f0 = __uint_as_float(wv[q] << 16) * pre;
-                const float f1 = __uint_as_float(wv[q] & 0xffff0000u) * pre;
+                const int s0 = Q40 || I4 ? kPerm[2 * q] : 2 * q, s1 = Q40 || I4 ? kPerm[2 * q + 1] : 2 * q + 1;
+                const float f0 = bf16_to_f32(static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)))) * pre;
+                const float f1 = bf16_to_f32(static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)))) * pre;
                 o[q] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f0))) |
                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f1))) << 16);
             }
@@ -604,6 +641,7 @@ void nf4_planes_kernel(NBatch b) {
     }
     lds_barrier<63>();
 
+    const uint32_t LO = vgpr_const(0x000F000Fu), HI = vgpr_const(0x00F000F0u), MG = vgpr_const(0x64006400u);
     const uint32_t lbase = static_cast<uint32_t>(lane & (kNf4LutCopies - 1)) * 8u;  // < 256
     // table entry of byte B of word v for this lane, at (byte * 32 + lane % 32) * 8: one byte
     // permute puts the byte at bits 8..15 and the lane's copy offset at bits 0..7
@@ -619,8 +657,9 @@ void nf4_planes_kernel(NBatch b) {
             const bool live = pt < ntiles;
             const NStage &s = st[i];
             const int g = live ? pg : 0;
-            // A fragment of MFMA q: x[128 g + 32 q + 8 p .. + 7]
-            const uint8_t *xa = lds + xoff + g * (kGroup * 2) + part * 16;
+            // A fragment of MFMA q: x[128 g + 32 q + 8 p .. + 7] (INT4: x[128 g + 32 p + 8 q ..])
+            const uint8_t *xa = lds + xoff + g * (kGroup * 2) + part * (I4 ? 64 : 16);
+            constexpr int xq = I4 ? 16 : 64;
             const float post = reinterpret_cast<const float *>(lds + soff)[g];
             // one accumulation chain per block of the chunk (two for a single block, to halve the
             // MFMA dependency latency)
@@ -630,18 +669,39 @@ void nf4_planes_kernel(NBatch b) {
             for (int j = 0; j < NC; ++j) c[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const half8_t a = *reinterpret_cast<const half8_t *>(xa + 64 * q);
+                const half8_t a = *reinterpret_cast<const half8_t *>(xa + xq * q);
                 const uint32_t wq = s.w[q];
-                const uint2 e0 = entry(wq, std::integral_constant<uint32_t, 0>{});
-                const uint2 e1 = entry(wq, std::integral_constant<uint32_t, 1>{});
-                const uint2 e2 = entry(wq, std::integral_constant<uint32_t, 2>{});
-                const uint2 e3 = entry(wq, std::integral_constant<uint32_t, 3>{});
                 const int j = NBPC == 1 ? (q & 1) : q * NBPC / 4;
-                c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pack8(e0.x, e1.x, e2.x, e3.x), c[j], 0, 0, 0);
-                c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pack8(e0.y, e1.y, e2.y, e3.y), c[j], 0, 0, 0);
+                if constexpr (Q40 || I4) {
+                    // (1024 + q) - (1024 + z) and (1024 + 16 q) / 16 - (64 + z): the exact
+                    // integers q - z (Q4_0: z = 8)
+                    const uint32_t zi = I4 ? (s.am[1] >> (4 * (r16 & 1))) & 15u : 8u;
+                    const half2_t zc1024 = as_h2((0xE400u + zi) * 0x00010001u);
+                    const half2_t zc64 = as_h2((0xD400u + (zi << 4)) * 0x00010001u);
+                    const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+                    const uint32_t w8 = wq >> 8;
+                    const half8_t bq = pack8(as_u(as_h2((wq & LO) | MG) + zc1024), as_u(as_h2((wq & HI) | MG) * sixteenth + zc64),
+                                             as_u(as_h2((w8 & LO) | MG) + zc1024), as_u(as_h2((w8 & HI) | MG) * sixteenth + zc64));
+                    c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, c[j], 0, 0, 0);
+                } else {
+                    const uint2 e0 = entry(wq, std::integral_constant<uint32_t, 0>{});
+                    const uint2 e1 = entry(wq, std::integral_constant<uint32_t, 1>{});
+                    const uint2 e2 = entry(wq, std::integral_constant<uint32_t, 2>{});
+                    const uint2 e3 = entry(wq, std::integral_constant<uint32_t, 3>{});
+                    c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pack8(e0.x, e1.x, e2.x, e3.x), c[j], 0, 0, 0);
+                    c[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pack8(e0.y, e1.y, e2.y, e3.y), c[j], 0, 0, 0);
+                }
             }
             float v;
-            if constexpr (NBPC == 1) {
+            if constexpr (I4) {
+                v = __fmul_rn(c[0][0] + c[1][0], f16_to_f32(static_cast<uint16_t>(s.am[0])) * post);
+            } else if constexpr (Q40) {
+                float t = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    t = __fadd_rn(t, __fmul_rn(c[j][0], f16_to_f32(static_cast<uint16_t>(s.am[j >> 1] >> (16 * (j & 1))))));
+                v = __fmul_rn(t, post);
+            } else if constexpr (NBPC == 1) {
                 v = __fmul_rn(__fmul_rn(c[0][0] + c[1][0], __uint_as_float(s.am[0])), post);
             } else {
                 float t = 0.0f;
@@ -776,6 +836,42 @@ __global__ void nf4_from_planes_kernel(const uint8_t *pc, const float *pa, int64
     }
 }
 
+// GGUF Q4_0 planes (codes u8 [N, K/2], 64-byte chunks of four 16-byte parts; d f16 [N, GP])
+// <-> Q4_0 GEMV planes: chunk (t, g) holds at byte 16 * (16 p + r) part p of chunk g of row
+// 16 t + r, and d [T][G][16][4] the four blocks' d of row 16 t + r.  One thread per piece.
+__global__ void q40_to_planes_kernel(const uint8_t *codes, const uint16_t *scales, int64_t n, int64_t k, uint8_t *pc,
+                                     uint16_t *pd) {
+    const int64_t G = k / kGroup, T = (n + 15) / 16, GP = (k / 32 + 7) / 8 * 8;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (u >= T * G * 64) return;
+    const int64_t chunk = u >> 6, l = u & 63;
+    const int64_t t = chunk / G, g = chunk % G, p = l >> 4, r = l & 15, row = t * 16 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (row < n) v = *reinterpret_cast<const uint4 *>(codes + row * (k / 2) + g * 64 + 16 * p);
+    *reinterpret_cast<uint4 *>(pc + u * 16) = v;
+    if (p == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pd[(chunk * 16 + r) * 4 + j] = row < n ? scales[row * GP + 4 * g + j] : 0;
+    }
+}
+
+__global__ void q40_from_planes_kernel(const uint8_t *pc, const uint16_t *pd, int64_t n, int64_t k, uint8_t *codes,
+                                       uint16_t *scales) {
+    const int64_t G = k / kGroup, GP = (k / 32 + 7) / 8 * 8;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // over n * G * 4
+    if (u >= n * G * 4) return;
+    const int64_t row = u / (G * 4), c = u % (G * 4), g = c / 4, p = c % 4, t = row / 16, r = row % 16;
+    const int64_t chunk = t * G + g;
+    *reinterpret_cast<uint4 *>(codes + row * (k / 2) + g * 64 + 16 * p) =
+        *reinterpret_cast<const uint4 *>(pc + (chunk * 64 + p * 16 + r) * 16);
+    if (p == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) scales[row * GP + 4 * g + j] = pd[(chunk * 16 + r) * 4 + j];
+        if (g == G - 1)
+            for (int64_t j = 4 * G; j < GP; ++j) scales[row * GP + j] = 0;  // pad slots
+    }
+}
+
 // ---- host ----------------------------------------------------------------------------------
 int cu_count() {
     static std::mutex mu;
@@ -847,6 +943,9 @@ int64_t planes_lds(int mr, int nw, const PProblem &P) {
     return (rs * P.m + 15) / 16 * 16 + (P.G * mr * 4 + 15) / 16 * 16 + tiles * nw * 64 * mr;
 }
 
+template <int NBPC, int KIND = kKindNf4>
+void launch_planes_m1(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st);
+
 // M = 1: one row of x per problem (16 waves); M = 2..4: up to 4 rows (16 waves); M = 5..8:
 // up to 8 rows (8 waves), a problem whose 8 rows of x do not fit LDS next to its partials
 // split into two problems of 4 rows that stream the same planes.  Beyond M = 8 the partials of
@@ -872,6 +971,41 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
                 "x and codes planes must be 16-byte aligned, scales and y 4-byte aligned");
         require(((q.n + 15) / 16) * (q.k / kGroup) * 1024 < (int64_t(1) << 31),
                 "GEMV planes of one matrix must stay below 2 GiB");
+    }
+    if (m == 1 && CFH_PLANES_M1_GENERIC) {
+        std::vector<int64_t> bytes, units;
+        for (int i = 0; i < count; ++i) {
+            bytes.push_back(((problems[i].n + 15) / 16) * (problems[i].k / kGroup) * 1024);
+            units.push_back((problems[i].n + 7) / 8);
+        }
+        const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+        NBatch nb{};
+        int64_t need_max = 0, ngrid = 0;
+        for (int j = 0; j < count; ++j) {
+            const cfh_w4a16_problem_t &q = problems[j];
+            NProblem &P = nb.p[j];
+            P.codes = reinterpret_cast<const uint8_t *>(q.codes);
+            P.absmax = reinterpret_cast<const float *>(q.scales_f16);  // f16 scale planes
+            P.zeros = reinterpret_cast<const uint8_t *>(q.zeros);
+            P.x = q.x;
+            P.y = q.y;
+            P.n = static_cast<int32_t>(q.n);
+            P.G = static_cast<int32_t>(q.k / kGroup);
+            P.units = static_cast<int32_t>(units[static_cast<size_t>(j)]);
+            P.wg0 = static_cast<int32_t>(ngrid);
+            P.wgs = wgs[static_cast<size_t>(j)];
+            require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
+            ngrid += P.wgs;
+            const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
+            need_max = std::max<int64_t>(need_max, int64_t(P.G) * 256 + (int64_t(P.G) * 4 + 15) / 16 * 16 +
+                                                       tiles * kWaves * 64);
+        }
+        nb.count = count;
+        nb.y_bf16 = y_dtype == CFH_DTYPE_BF16;
+        require(need_max <= kLdsMax / kWgPerCu, "a problem of the batch exceeds the GEMV planes kernel's LDS (m * k too "
+                                                "large or too many rows per workgroup)");
+        launch_planes_m1<1, kKindInt4>(nb, ngrid, std::max<int64_t>(need_max, kLdsFloor), st);
+        return;
     }
     // row groups: rows [r0, r0 + rows) of problem src
     struct Group {
@@ -934,8 +1068,9 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
     else launch_planes<CFH_PLANES_WAVES8, CFH_PLANES_DEPTH8, 8>(b, grid, req, st);
 }
 
-template <int NBPC>
-void launch_nf4_planes(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
+template <int NBPC, int KIND>
+void launch_planes_m1(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
+    constexpr int D = KIND == kKindInt4 ? kI4Depth : kNf4Depth;
     static std::mutex mu;
     static std::map<int, bool> attr_set;  // per device
     int dev = 0;
@@ -943,15 +1078,15 @@ void launch_nf4_planes(const NBatch &b, int64_t grid, int64_t lds, hipStream_t s
     {
         std::lock_guard<std::mutex> g(mu);
         if (!attr_set[dev]) {
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&nf4_planes_kernel<kWaves, kNf4Depth, NBPC>),
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_m1_kernel<kWaves, D, NBPC, KIND>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
                       "hipFuncSetAttribute");
             attr_set[dev] = true;
         }
     }
-    nf4_planes_kernel<kWaves, kNf4Depth, NBPC>
+    planes_m1_kernel<kWaves, D, NBPC, KIND>
         <<<dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), static_cast<size_t>(lds), st>>>(b);
-    check_launch("nf4_planes_kernel");
+    check_launch("planes_m1_kernel");
 }
 
 bool nf4_block_ok(int64_t block) { return block >= 32 && block <= (int64_t(1) << 20) && (block & (block - 1)) == 0; }
@@ -1006,9 +1141,67 @@ void nf4_planes_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_
     b.count = count;
     b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
     require(lds_max <= kLdsMax, "a problem of the batch exceeds the NF4 planes kernel's LDS (k too large)");
-    if (nbpc == 1) launch_nf4_planes<1>(b, grid, lds_max, st);
-    else if (nbpc == 2) launch_nf4_planes<2>(b, grid, lds_max, st);
-    else launch_nf4_planes<4>(b, grid, lds_max, st);
+    if (nbpc == 1) launch_planes_m1<1>(b, grid, lds_max, st);
+    else if (nbpc == 2) launch_planes_m1<2>(b, grid, lds_max, st);
+    else launch_planes_m1<4>(b, grid, lds_max, st);
+}
+
+// GGUF Q4_0 decode GEMV (M = 1) over Q4_0 GEMV planes: the NF4 planes kernel with the exact
+// (q - 8) decode and one f16 d per block of 32.
+void q40_planes_batched(const cfh_gguf_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
+                        hipStream_t st) {
+    require(count >= 1 && count <= CFH_MAX_BATCH, "count must be in 1..8");
+    require(problems != nullptr, "problems must not be NULL");
+    require(m == 1, "the Q4_0 planes kernel takes M = 1");
+    require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
+    const int W = cu_count();
+    std::vector<int64_t> bytes, units;
+    for (int i = 0; i < count; ++i) {
+        const cfh_gguf_problem_t &q = problems[i];
+        require(q.n >= 1 && q.k >= kGroup && q.k % kGroup == 0, "Q4_0 planes need n >= 1 and k % 128 == 0");
+        require(q.x && q.codes && q.scales_f16 && q.y, "x, planes and y must not be NULL");
+        require(aligned(q.x, 16) && aligned(q.codes, 16) && aligned(q.scales_f16, 8) && aligned(q.y, 4),
+                "x and codes planes must be 16-byte aligned, d planes 8-byte aligned, y 4-byte aligned");
+        require(((q.n + 15) / 16) * (q.k / kGroup) * 1024 < (int64_t(1) << 31),
+                "Q4_0 planes of one matrix must stay below 2 GiB");
+        bytes.push_back(((q.n + 15) / 16) * (q.k / kGroup) * (1024 + 128));
+        units.push_back((q.n + 7) / 8);
+    }
+    const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+    NBatch b{};
+    int64_t lds_max = 0, grid = 0;
+    for (int j = 0; j < count; ++j) {
+        const cfh_gguf_problem_t &q = problems[j];
+        NProblem &P = b.p[j];
+        P.codes = reinterpret_cast<const uint8_t *>(q.codes);
+        P.absmax = reinterpret_cast<const float *>(q.scales_f16);  // the d planes (8 bytes per row and chunk)
+        P.x = q.x;
+        P.y = q.y;
+        P.n = static_cast<int32_t>(q.n);
+        P.G = static_cast<int32_t>(q.k / kGroup);
+        P.units = static_cast<int32_t>(units[j]);
+        P.wg0 = static_cast<int32_t>(grid);
+        P.wgs = wgs[j];
+        require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
+        grid += P.wgs;
+        const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
+        const int64_t need = int64_t(P.G) * 256 + (int64_t(P.G) * 4 + 15) / 16 * 16 + tiles * kWaves * 64;
+        lds_max = std::max<int64_t>(lds_max, need);
+    }
+    b.count = count;
+    b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
+    require(lds_max <= kLdsMax, "a problem of the batch exceeds the Q4_0 planes kernel's LDS (k too large)");
+    launch_planes_m1<4, kKindQ40>(b, grid, std::max<int64_t>(lds_max, kLdsFloor), st);
+}
+
+void q40_planes_checks(const void *codes, const void *scales, int64_t rows, int64_t k, const void *pc, const void *pd) {
+    require(rows >= 0 && k >= 0 && k % kGroup == 0, "rows >= 0 and k % 128 == 0 are required");
+    if (rows > 0 && k > 0) {
+        require(codes && scales && pc && pd, "buffers must not be NULL");
+        require(aligned(codes, 16) && aligned(pc, 16), "codes and codes planes must be 16-byte aligned");
+        require(aligned(scales, 2) && aligned(pd, 8), "d must be 2-byte and d planes 8-byte aligned");
+        require(((rows + 15) / 16) * (k / kGroup) * 1024 < (int64_t(1) << 31), "planes must stay below 2 GiB");
+    }
 }
 
 void nf4_planes_checks(const void *codes, const void *absmax, int64_t rows, int64_t k, int64_t block, const void *pc,
@@ -1109,6 +1302,38 @@ int32_t castforge_hip_nf4_from_planes(const void *planes_codes, const float *pla
 int32_t castforge_hip_gemv_nf4_planes_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_t m,
                                               int32_t y_dtype, void *stream, char **out_error) {
     return guarded(out_error, [&] { nf4_planes_batched(problems, count, m, y_dtype, static_cast<hipStream_t>(stream)); });
+}
+
+int32_t castforge_hip_gguf_q4_0_to_gemv_planes(const void *codes, const uint16_t *scales_f16, int64_t rows, int64_t k,
+                                              void *planes_codes, uint16_t *planes_d, void *stream, char **out_error) {
+    return guarded(out_error, [&] {
+        q40_planes_checks(codes, scales_f16, rows, k, planes_codes, planes_d);
+        const int64_t units = ((rows + 15) / 16) * (k / kGroup) * 64;
+        if (units == 0) return;
+        q40_to_planes_kernel<<<dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0,
+                               static_cast<hipStream_t>(stream)>>>(static_cast<const uint8_t *>(codes), scales_f16, rows,
+                                                                   k, static_cast<uint8_t *>(planes_codes), planes_d);
+        check_launch("q40_to_planes_kernel");
+    });
+}
+
+int32_t castforge_hip_gguf_q4_0_from_gemv_planes(const void *planes_codes, const uint16_t *planes_d, int64_t rows,
+                                                int64_t k, void *codes, uint16_t *scales_f16, void *stream,
+                                                char **out_error) {
+    return guarded(out_error, [&] {
+        q40_planes_checks(codes, scales_f16, rows, k, planes_codes, planes_d);
+        const int64_t units = rows * (k / kGroup) * 4;
+        if (units == 0) return;
+        q40_from_planes_kernel<<<dim3(static_cast<unsigned>((units + 255) / 256)), dim3(256), 0,
+                                 static_cast<hipStream_t>(stream)>>>(static_cast<const uint8_t *>(planes_codes), planes_d,
+                                                                     rows, k, static_cast<uint8_t *>(codes), scales_f16);
+        check_launch("q40_from_planes_kernel");
+    });
+}
+
+int32_t castforge_hip_gemv_gguf_q4_0_planes_batched(const cfh_gguf_problem_t *problems, int32_t count, int64_t m,
+                                                   int32_t y_dtype, void *stream, char **out_error) {
+    return guarded(out_error, [&] { q40_planes_batched(problems, count, m, y_dtype, static_cast<hipStream_t>(stream)); });
 }
 
 }  // extern "C"

@@ -153,6 +153,9 @@ SIGNATURES = {
     "castforge_hip_dequantize_gguf": (c_int32, [c_int32, _P, _P, c_int64, c_int64, _P, _P, _E]),
     "castforge_hip_gemv_gguf": (c_int32, [c_int32, _P, c_int64, c_int64, c_int64, _P, _P, _P, c_int32, _P, _E]),
     "castforge_hip_gemv_gguf_batched": (c_int32, [c_int32, POINTER(GgufProblem), c_int32, c_int64, c_int32, _P, _E]),
+    "castforge_hip_gguf_q4_0_to_gemv_planes": (c_int32, [_P, _P, c_int64, c_int64, _P, _P, _P, _E]),
+    "castforge_hip_gguf_q4_0_from_gemv_planes": (c_int32, [_P, _P, c_int64, c_int64, _P, _P, _P, _E]),
+    "castforge_hip_gemv_gguf_q4_0_planes_batched": (c_int32, [POINTER(GgufProblem), c_int32, c_int64, c_int32, _P, _E]),
 }
 
 _lib = None

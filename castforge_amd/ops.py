@@ -671,6 +671,66 @@ def gemv_gguf_batched(xs: list[torch.Tensor], ps: list[GgufPacked], ys: list[tor
     ffi.call("castforge_hip_gemv_gguf_batched", t, arr, len(ps), m, yd, _stream(xs[0]))
 
 
+@dataclass
+class Q40Planes:
+    """GGUF Q4_0 weights in the Q4_0 GEMV planes layout (castforge_hip_gguf_q4_0_to_gemv_planes):
+    codes u8 [T * G * 1024], d f16 [T, G, 16, 4] with T = ceil(n/16), G = k/128."""
+    codes: torch.Tensor
+    scales: torch.Tensor
+    n: int
+    k: int
+
+    def nbytes(self) -> int:
+        return self.codes.numel() + self.scales.numel() * 2
+
+
+def gguf_q4_0_to_gemv_planes(p: GgufPacked) -> Q40Planes:
+    """The Q4_0 GEMV planes of GGUF Q4_0 planes (built once, at load time)."""
+    if p.ggml_type != ffi.GGML_Q4_0 or p.k % 128:
+        raise ValueError("Q4_0 GEMV planes hold GGUF Q4_0 matrices with k % 128 == 0")
+    t, g = (p.n + 15) // 16, p.k // 128
+    dev = p.codes.device
+    pl = Q40Planes(torch.empty(t * g * 1024, dtype=torch.uint8, device=dev),
+                   torch.empty((t, g, 16, 4), dtype=torch.float16, device=dev), p.n, p.k)
+    ffi.call("castforge_hip_gguf_q4_0_to_gemv_planes", _ptr(_dev(p.codes)), _ptr(_dev(p.scales)), p.n, p.k,
+             _ptr(pl.codes), _ptr(pl.scales), _stream(p.codes))
+    return pl
+
+
+def gguf_q4_0_from_gemv_planes(pl: Q40Planes) -> GgufPacked:
+    """GGUF Q4_0 planes back from Q4_0 GEMV planes (bit for bit)."""
+    n, k = pl.n, pl.k
+    dev = pl.codes.device
+    gp = (k // 32 + 7) // 8 * 8
+    p = GgufPacked(ffi.GGML_Q4_0, torch.empty((n, k // 2), dtype=torch.uint8, device=dev),
+                   torch.empty((n, gp), dtype=torch.float16, device=dev), n, k)
+    ffi.call("castforge_hip_gguf_q4_0_from_gemv_planes", _ptr(_dev(pl.codes)), _ptr(_dev(pl.scales)), n, k,
+             _ptr(p.codes), _ptr(p.scales), _stream(pl.codes))
+    return p
+
+
+def gemv_gguf_q4_0_planes_batched(xs: list[torch.Tensor], ps: list[Q40Planes], ys: list[torch.Tensor]) -> None:
+    """Q4_0 decode (x of one row) over Q4_0 GEMV planes, all problems in one launch (one
+    workgroup per CU)."""
+    if not (len(xs) == len(ps) == len(ys)) or not 1 <= len(ps) <= ffi.MAX_BATCH:
+        raise ValueError("xs, ps, ys must have the same length in 1..8")
+    m = xs[0].shape[0] if xs[0].dim() == 2 else 0
+    if m != 1:
+        raise ValueError("the Q4_0 planes kernel takes x of one row")
+    yd = _check_batch(xs, ys, m, [p.n for p in ps], [p.k for p in ps])
+    arr = (ffi.GgufProblem * len(ps))()
+    for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
+        arr[i] = ffi.GgufProblem(_ptr(x), _ptr(p.codes), _ptr(p.scales), _ptr(y), p.n, p.k)
+    ffi.call("castforge_hip_gemv_gguf_q4_0_planes_batched", arr, len(ps), m, yd, _stream(xs[0]))
+
+
+def gemv_gguf_q4_0_planes(x: torch.Tensor, p: Q40Planes, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """y [1, n] for x bf16 [1, k] over Q4_0 GEMV planes."""
+    y = torch.empty((1, p.n), dtype=out_dtype, device=x.device)
+    gemv_gguf_q4_0_planes_batched([x], [p], [y])
+    return y
+
+
 # ------------------------------------------------------------- static W8A8 (calibrate) ----
 def static_quantize(x: torch.Tensor, scale: float, bits: int = 8) -> torch.Tensor:
     """castforge.static_quantize (eval.rs:1369-1382): clamp(round(x / scale), +-qmax) * scale

@@ -469,6 +469,28 @@ int32_t castforge_hip_gemv_gguf(int32_t ggml_type, const uint16_t *x, int64_t m,
 int32_t castforge_hip_gemv_gguf_batched(int32_t ggml_type, const cfh_gguf_problem_t *problems, int32_t count,
                                         int64_t m, int32_t y_dtype, void *stream, char **out_error);
 
+/* Q4_0 GEMV planes: GGUF Q4_0 planes (castforge_hip_gguf_repack) of a [rows, k] matrix
+ * (k % 128 == 0) rewritten once, at load, for the M = 1 decode kernel below (no reference
+ * counterpart).  T = ceil(rows/16), G = k/128:
+ *   planes_codes: T x G chunks of 1024 bytes; chunk (t, g) holds, at byte 16 * (16 p + r), the
+ *                 16-byte part p of chunk g of row 16 t + r of the GGUF planes (elements
+ *                 8p..8p+7 of its four blocks);
+ *   planes_d    : f16 [T][G][16][4], the d of blocks 4g..4g+3 of row 16 t + r.
+ * Rows past `rows` are zero.  from_gemv_planes restores the GGUF planes (pad d slots 0) bit for
+ * bit.  codes and planes_codes 16-byte aligned, planes_d 8-byte aligned. */
+int32_t castforge_hip_gguf_q4_0_to_gemv_planes(const void *codes, const uint16_t *scales_f16, int64_t rows, int64_t k,
+                                              void *planes_codes, uint16_t *planes_d, void *stream, char **out_error);
+int32_t castforge_hip_gguf_q4_0_from_gemv_planes(const void *planes_codes, const uint16_t *planes_d, int64_t rows,
+                                                int64_t k, void *codes, uint16_t *scales_f16, void *stream,
+                                                char **out_error);
+/* castforge_hip_gemv_gguf_batched for Q4_0 at M = 1 over Q4_0 GEMV planes (codes / scales_f16
+ * of each problem point at its planes; x [1, k] 16-byte aligned): y = x * decode(W)^T as the
+ * reference decodes Q4_0 (gguf.rs:513-550) and evaluates the matmul (codegen/eval.rs:1465-1507),
+ * in one launch of one workgroup per CU.  Each block's products are exact ((q - 8) in f16, x
+ * with a power-of-two pre-scale per 128 activations) and its f32 sum is scaled by its d. */
+int32_t castforge_hip_gemv_gguf_q4_0_planes_batched(const cfh_gguf_problem_t *problems, int32_t count, int64_t m,
+                                                   int32_t y_dtype, void *stream, char **out_error);
+
 /* *out = max |src[i]| over the non-NaN elements (0 for n == 0), written on the device: the
  * constant ranges of calibrate-quantize's calibrate_value_ranges (formats.rs:135-150). */
 int32_t castforge_hip_absmax_f32(const float *src, int64_t n, float *out, void *stream, char **out_error);
