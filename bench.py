@@ -486,6 +486,30 @@ def main():
                          f"evaluator semantics (dequantize to f32, then the m,n,k f32 loop of "
                          f"eval.rs:1465-1507), single thread, {t_cpu:.1f} s"}
         log(f"[bench] cpu baseline {cpu['value']} GB/s over {passes} passes ({t_cpu:.1f}s)")
+        # CPU-C, the best-effort host figure (blocked, SIMD, all visible cores; oracle/cpu_best.c):
+        # reported beside the port, which stays the baseline
+        import ctypes
+        cpub = ctypes.CDLL(str(ROOT / "oracle" / "_build" / "libcf_cpubest.so"))
+        cp = ctypes.c_void_p
+        cpub.cpub_gemv_w4a16.argtypes = [cp, ctypes.c_int64, ctypes.c_int64, cp, cp, cp, cp, ctypes.c_int]
+        ncpu = len(os.sched_getaffinity(0))
+        xf = [np.ascontiguousarray(O.bf16_bits_to_f32(x).reshape(-1), dtype=np.float32) for x in xh]
+        yf = [np.zeros(n, np.float32) for (_, n, k) in synth.LLAMA7B_BLOCK]
+        ptr = lambda a: a.ctypes.data_as(cp)
+        passes_c, t_c = 0, 0.0
+        while t_c < 2.0 and passes_c < 200:
+            t1 = time.perf_counter()
+            for (c, s_, z, n, k), x, y in zip(host, xf, yf):
+                cpub.cpub_gemv_w4a16(ptr(x), n, k, ptr(c), ptr(s_), ptr(z), ptr(y), ncpu)
+            t_c += time.perf_counter() - t1
+            passes_c += 1
+        cpu["best_effort"] = {"value": round(w4_bytes(1) * passes_c / t_c / 1e9, 2), "unit": "GB/s",
+                              "cores": ncpu, "kind": "CPU-C best-effort (oracle/cpu_best.c)",
+                              "sample": f"{passes_c} passes of the full block W4A16 GEMV at M=1, OpenMP over "
+                                        f"{ncpu} threads, AVX2/FMA, group products in f32 lanes with the "
+                                        f"zero point folded out, {t_c:.1f} s"}
+        log(f"[bench] cpu best-effort {cpu['best_effort']['value']} GB/s on {ncpu} threads "
+            f"over {passes_c} passes ({t_c:.1f}s)")
 
     traffic = None
     tfile = ROOT / "profiles" / "traffic_w4a16_planes_gemv_m1.json"
