@@ -496,16 +496,21 @@ def main():
         xf = [np.ascontiguousarray(O.bf16_bits_to_f32(x).reshape(-1), dtype=np.float32) for x in xh]
         yf = [np.zeros(n, np.float32) for (_, n, k) in synth.LLAMA7B_BLOCK]
         ptr = lambda a: a.ctypes.data_as(cp)
+        # 6 rotating copies of the block (630 MB), more than a host's last-level cache, as the GPU
+        # side rotates copies past the MALL
+        hosts = [host] + [[(c.copy(), s_.copy(), z.copy(), n, k) for (c, s_, z, n, k) in host] for _ in range(5)]
         passes_c, t_c = 0, 0.0
-        while t_c < 2.0 and passes_c < 200:
+        while t_c < 2.0 and passes_c < 5000:
             t1 = time.perf_counter()
-            for (c, s_, z, n, k), x, y in zip(host, xf, yf):
+            for (c, s_, z, n, k), x, y in zip(hosts[passes_c % len(hosts)], xf, yf):
                 cpub.cpub_gemv_w4a16(ptr(x), n, k, ptr(c), ptr(s_), ptr(z), ptr(y), ncpu)
             t_c += time.perf_counter() - t1
             passes_c += 1
+        del hosts
         cpu["best_effort"] = {"value": round(w4_bytes(1) * passes_c / t_c / 1e9, 2), "unit": "GB/s",
                               "cores": ncpu, "kind": "CPU-C best-effort (oracle/cpu_best.c)",
-                              "sample": f"{passes_c} passes of the full block W4A16 GEMV at M=1, OpenMP over "
+                              "sample": f"{passes_c} passes of the full block W4A16 GEMV at M=1 over 6 rotating "
+                                        f"copies (630 MB), OpenMP over "
                                         f"{ncpu} threads, AVX2/FMA, group products in f32 lanes with the "
                                         f"zero point folded out, {t_c:.1f} s"}
         log(f"[bench] cpu best-effort {cpu['best_effort']['value']} GB/s on {ncpu} threads "
