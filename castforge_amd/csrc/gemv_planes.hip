@@ -1,5 +1,7 @@
-// W4A16 decode GEMV (M = 1..8) over INT4 g128 weights in the GEMV planes layout, and the NF4
-// decode GEMV (M = 1) over NF4 planes (at the end of the device code), gfx950.
+// W4A16 decode GEMV (M = 1..8) over INT4 g128 weights in the GEMV planes layout, and the M = 1
+// decode GEMV over NF4 planes and GGUF Q4_0 GEMV planes, gfx950.  planes_kernel serves INT4 at
+// M = 2..8; planes_m1_kernel (after it) serves M = 1 for the three formats, INT4 with the same
+// arithmetic as planes_kernel at M = 1.
 //
 // Replaces the evaluation of `castforge.fused_qmatmul` at decode (eval.rs:1145-1179 with
 // eval_matmul_2d, eval.rs:1465-1507; packed_rhs [N, K] weights, fold.rs:549-554) for the
@@ -405,7 +407,10 @@ void planes_kernel(PBatch b) {
     }
 }
 
-// ---- NF4 over GEMV planes (M = 1) -----------------------------------------------------------
+// ---- M = 1: INT4 g128, NF4 and GGUF Q4_0 planes ------------------------------------------------
+// planes_m1_kernel: the design above specialised to one row of x (a scalar partial per lane, a
+// 64-byte problem record, 8 problems per launch), with the decode and metadata of its KIND.
+//
 // NF4 planes.  Codes: the same T x G chunks of 1024 bytes, but the piece of lane (p, r) holds
 // canonical words 16 g + p, 16 g + 4 + p, 16 g + 8 + p, 16 g + 12 + p of row 16 t + r, so that
 // the q-th words of the four parts, which one MFMA takes, are codes 32 q .. 32 q + 31 of the
@@ -463,6 +468,9 @@ struct NStage {
 
 // LDS: [decode table, 64 KB (NF4 only)][x as f16, G * 256 B][per chunk 2^sh, G * 4 B (16-byte
 // padded)][partials: tiles x NW x 16 f32]
+// Q4_0 GEMV planes (castforge_hip_gguf_q4_0_to_gemv_planes): chunk (t, g) holds at byte
+// 16 * (16 p + r) the 16-byte part p of chunk g of row 16 t + r of the GGUF planes (elements
+// 8p..8p+7 of its four blocks, so MFMA q takes block q), d f16 [T][G][16][4].
 // Q40: the GGUF Q4_0 form over Q4_0 GEMV planes (below): codes decoded to the exact f16
 // q - 8 like INT4, one f16 d per block of 32 (NBPC = 4 blocks per chunk), x in the INT4
 // decode's order.
