@@ -1149,9 +1149,11 @@ void nf4_planes_batched(const cfh_nf4_problem_t *problems, int32_t count, int64_
     b.count = count;
     b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
     require(lds_max <= kLdsMax, "a problem of the batch exceeds the NF4 planes kernel's LDS (k too large)");
-    if (nbpc == 1) launch_planes_m1<1>(b, grid, lds_max, st);
-    else if (nbpc == 2) launch_planes_m1<2>(b, grid, lds_max, st);
-    else launch_planes_m1<4>(b, grid, lds_max, st);
+    // at least kLdsFloor, so that one workgroup per CU holds for small k too
+    const int64_t req = std::max<int64_t>(lds_max, kLdsFloor);
+    if (nbpc == 1) launch_planes_m1<1>(b, grid, req, st);
+    else if (nbpc == 2) launch_planes_m1<2>(b, grid, req, st);
+    else launch_planes_m1<4>(b, grid, req, st);
 }
 
 // GGUF Q4_0 decode GEMV (M = 1) over Q4_0 GEMV planes: the NF4 planes kernel with the exact
