@@ -61,7 +61,12 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 constexpr int kGroup = 128;
 constexpr uint32_t kOob = 0x80000000u;  // past every descriptor's range: reads 0, no traffic
-constexpr int kMaxP = 4 * CFH_MAX_BATCH;  // problems of a launch after splitting rows of x
+// problems of a launch: one per matrix at M <= 4; at M = 5..8 a matrix whose 8 rows of x do
+// not fit LDS splits into two problems of 4 rows.  Each kernel instance's argument holds only
+// as many problems as it can get (a smaller argument shortens the prologue's reads of it).
+constexpr int kMaxP = 2 * CFH_MAX_BATCH;
+template <int MR>
+__host__ __device__ constexpr int max_problems() { return MR == 8 ? kMaxP : CFH_MAX_BATCH; }
 
 #ifndef CFH_PLANES_WAVES
 #define CFH_PLANES_WAVES 16
@@ -103,8 +108,9 @@ struct PProblem {
     int32_t m;          // rows of x (and y) of this problem
 };
 
+template <int NP>
 struct PBatch {
-    PProblem p[kMaxP];
+    PProblem p[NP];
     int32_t count, y_bf16;
 };
 
@@ -156,7 +162,7 @@ __host__ __device__ constexpr uint32_t x_row_stride(uint32_t G) { return MR == 1
 // MR = 8: A row i is x row min(i mod 8, M - 1); D rows 0..7 are lanes 0..31 (4 rows each).
 template <int NW, int D, int MR>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW * kWgPerCu / 4)))
-void planes_kernel(PBatch b) {
+void planes_kernel(PBatch<max_problems<MR>()> b) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = uni(tid >> 6);
@@ -167,7 +173,7 @@ void planes_kernel(PBatch b) {
     // workgroups (host-checked: wgs * units < 2^31)
     int pi = 0;
 #pragma unroll
-    for (int i = 1; i < kMaxP; ++i)
+    for (int i = 1; i < max_problems<MR>(); ++i)
         if (i < b.count && w >= b.p[i].wg0) pi = i;
     const PProblem &P = b.p[pi];
     const int G = P.G, local = w - P.wg0;
@@ -924,7 +930,12 @@ std::vector<int> workgroups_per_problem(const std::vector<int64_t> &bytes, const
 }
 
 template <int NW, int D, int MR>
-void launch_planes(const PBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
+void launch_planes(const PBatch<kMaxP> &all, int64_t grid, int64_t lds, hipStream_t st) {
+    require(all.count >= 1 && all.count <= max_problems<MR>(), "too many problems for one launch");
+    PBatch<max_problems<MR>()> b{};
+    for (int i = 0; i < all.count; ++i) b.p[i] = all.p[i];
+    b.count = all.count;
+    b.y_bf16 = all.y_bf16;
     static std::mutex mu;
     static std::map<int, bool> attr_set;  // per device
     int dev = 0;
@@ -1020,7 +1031,7 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
         int src, r0, rows;
     };
     std::vector<int> split4(static_cast<size_t>(count), 0);  // problems whose groups hold 4 rows
-    PBatch b{};
+    PBatch<kMaxP> b{};
     int64_t lds_max = 0, grid = 0;
     for (int attempt = 0; attempt <= count; ++attempt) {  // each retry splits at least one more problem
         std::vector<Group> groups;
@@ -1036,7 +1047,7 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
             units.push_back((q.n + 7) / 8);
         }
         const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
-        b = PBatch{};
+        b = PBatch<kMaxP>{};
         lds_max = 0;
         grid = 0;
         bool retry = false;
