@@ -15,11 +15,13 @@
 //   Q8_0  q * d (19 bits) and NF4 f32(T[q] * absmax) (24 bits): three terms.
 //   A non-finite scale gives a non-finite weight (the remainder terms are 0) and so, as in the
 //   evaluator, non-finite outputs on its row.
-//   (A one-term INT4 form that applies the group scale to the accumulator -- multiplying it by
-//   s_prev / s_cur at every group start -- was measured: 1.15x faster at 128 x 128 tiles, but
-//   the rounding of the running sum at each group start put near-zero outputs of
-//   cancellation-heavy rows further from the exact value than the evaluator's own f32 sum, and
-//   VALU work on the accumulators keeps them out of the AGPRs, which spills the large tiles.)
+//   INT4 whose groups are whole 128-wide K blocks has a second kernel, prefill_i4_kernel below:
+//   one MFMA per product on the exact integer (q - z), a fresh f32 partial per K block, and the
+//   block's group scale applied to the partial by one fma into the running total.
+//   (A one-term INT4 form that instead multiplied the running accumulator by s_prev / s_cur
+//   at every group start was measured and dropped: the rounding of the running sum put
+//   near-zero outputs of cancellation-heavy rows further from the exact value than the
+//   evaluator's own f32 sum.)
 //
 // Design:
 //   * workgroup tile BN (n) x BM (m) with 4 waves; W is the MFMA row operand, so each lane
@@ -34,6 +36,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
@@ -455,6 +459,298 @@ void prefill_qgemm_kernel(PfArgs a) {
     });
 }
 
+// ---- INT4 with groups of a multiple of 128: one MFMA per product ----
+//
+// `prefill_i4_kernel<BM, D>` feeds the MFMA the exact integer (q - z) as bf16 (|q - z| <= 15)
+// and x as the bf16 it is.  Per 128-wide K block the MFMAs sum x (q - z) into a fresh f32
+// partial, and one fma per accumulator applies the block's f16 group scale:
+// y = sum_b s_b * P_b, the GEMV's per-group partial scheme.  Each partial rounds 8 times
+// (one per 16-wide MFMA step) over 128 products and the total once per block, against the
+// evaluator's one rounding per product (eval.rs:1465-1507).
+//   * Tile 256 (n) x BM (m), 4 waves.  Wave w owns n rows [64 w, 64 w + 64) (2 MFMA blocks of
+//     32) and all BM rows of x (BM / 32 blocks).  W is the MFMA B operand, so a lane's
+//     accumulators hold 16 m of one n and one scale multiplies them all.
+//   * W never touches LDS: each lane loads its row's 32 code bytes of the block (k = 64 h ..
+//     64 h + 63 of the block, h = lane / 32) and decodes word kk for MFMA step kk.  The f16
+//     pairs 1024 + q (even nibbles, at mantissa bits 0..3) and 64 + q (odd nibbles, at bits
+//     4..7) come from one v_and_or_b32 each; v_fma_mix_f32 subtracts 1024 + z or 64 + z from
+//     a half, giving q - z in f32 exactly; v_perm packs the bf16 halves.  17 VALU
+//     instructions per 8 weights.
+//   * x goes global -> LDS (buffer loads, rows past M read zero) in a ring of D + 1 stages of
+//     BM rows x 256 bytes; 16-byte chunk c of row r sits at c ^ (r & 15), so the 16 rows that
+//     one read phase touches hit 16 distinct chunks.  MFMA step kk reads chunk 8 h + kk, the
+//     k range the W lane decoded.
+//   * One barrier per block; block b + D's loads are issued right after it.
+#ifndef CFH_PF_I4_DEPTH
+#define CFH_PF_I4_DEPTH 2
+#endif
+// 1: block b - 1's partials are folded pair by pair in block b's first MFMA step; 0: at the
+// end of block b - 1
+#ifndef CFH_PF_I4_FOLD_FIRST
+#define CFH_PF_I4_FOLD_FIRST 0
+#endif
+constexpr int kI4BN = 256;
+constexpr int kI4KB = 128;
+
+template <int BM, int D>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_i4_kernel(PfArgs a) {
+    constexpr int J = BM / 32;
+    constexpr int S = D + 1;
+    constexpr int kStage = BM * kI4KB * 2;
+    constexpr int kDma = BM / 16;            // 1 KB buffer -> LDS loads per wave and block
+    constexpr int kLoads = kDma + 2 * 2 + 2 * 2;  // vector-memory loads per wave and block
+    static_assert(BM % 64 == 0 && S * kStage <= 160 * 1024, "tile / LDS budget");
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    const int M = a.M, N = a.N, K = a.K;
+    int pid = blockIdx.x;
+    const int ntiles = a.tiles_m * a.tiles_n;
+    {
+        const int per_xcd = ntiles / kXcds, full = per_xcd * kXcds;
+        if (pid < full) pid = (pid % kXcds) * per_xcd + pid / kXcds;
+    }
+    const int group_span = kGroupM * a.tiles_n;
+    const int first_m = (pid / group_span) * kGroupM;
+    const int gsize = (a.tiles_m - first_m) < kGroupM ? (a.tiles_m - first_m) : kGroupM;
+    const int m0 = (first_m + (pid % group_span) % gsize) * BM;
+    const int n0 = ((pid % group_span) / gsize) * kI4BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int fr = lane & 31, h = lane >> 5;
+    const int KB = K / kI4KB;
+    const int G = K / a.group, ZW = (G + 7) / 8, GP = ZW * 8;
+    const int bpg = a.group / kI4KB;  // K blocks per group
+
+    const rsrc_t rx = make_rsrc(a.x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(min(BM, M - m0)) * K * 2);
+    // descriptors over the tile's rows [n0, n0 + n_valid) (rows past N read zero); a lane's
+    // row is 64 wave + 32 i + fr of the tile
+    const int nw0 = n0 + 64 * wave;
+    const uint32_t n_valid = static_cast<uint32_t>(min(kI4BN, N - n0));
+    const rsrc_t rw = make_rsrc(static_cast<const uint8_t *>(a.codes) + static_cast<int64_t>(n0) * (K / 2), n_valid * (K / 2));
+    const rsrc_t rs = make_rsrc(static_cast<const uint16_t *>(a.scales) + static_cast<int64_t>(n0) * GP, n_valid * GP * 2);
+    const rsrc_t rz = make_rsrc(a.zeros + static_cast<int64_t>(n0) * ZW, n_valid * ZW * 4);
+    uint32_t vw[2], vs[2], vz[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t row = static_cast<uint32_t>(64 * wave + 32 * i + fr);
+        vw[i] = row * static_cast<uint32_t>(K / 2) + 32u * h;
+        vs[i] = row * static_cast<uint32_t>(GP) * 2u;
+        vz[i] = row * static_cast<uint32_t>(ZW) * 4u;
+    }
+    // lane offsets of the x loads: load t writes rows 4 t .. 4 t + 3 of the wave's BM / 4;
+    // lane -> row 4 t + lane / 16, physical chunk lane % 16 (logical chunk ^ (row & 15))
+    uint32_t lv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int r = 4 * u + (lane >> 4);
+        lv[u] = static_cast<uint32_t>((lane >> 4) * K * 2 + (((lane & 15) ^ (r & 15)) * 16));
+    }
+
+    struct WSet {
+        uint4 w[2][2];  // [row block i][k half]: words 0..3, 4..7 of the lane's 32 code bytes
+        uint32_t s[2], z[2];
+    };
+    auto issue = [&](int b, uint8_t *stage, WSet &r) __attribute__((always_inline)) {
+        uint8_t *dst = stage + (BM / 4) * wave * (kI4KB * 2);
+#pragma unroll
+        for (int t = 0; t < kDma; ++t)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rx, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(dst + t * 1024)),
+                16, lv[t & 3], ((BM / 4) * wave + 4 * t) * K * 2 + b * (kI4KB * 2), 0, 0);
+        const int g = b / bpg;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            r.w[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64, 0, 0));
+            r.w[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64 + 16, 0, 0));
+            r.s[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, vs[i] + (g & ~1) * 2, 0, 0);
+            r.z[i] = __builtin_amdgcn_raw_buffer_load_b32(rz, vz[i] + (g >> 3) * 4, 0, 0);
+        }
+    };
+
+    floatx16 tot[2][J];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) tot[i][j][e] = 0.f;
+
+    // opaque constants: kept in registers so the masks fold into v_and_or_b32 and the unit
+    // multiplier of v_fma_mix_f32 is not simplified away
+    auto opaque = [](uint32_t v) __attribute__((always_inline)) {
+        asm("" : "+v"(v));
+        return v;
+    };
+    const uint32_t kM0 = opaque(0x000F000Fu), kM1 = opaque(0x00F000F0u);
+    const uint32_t kC0 = opaque(0x64006400u), kC1 = opaque(0x54005400u);  // f16 1024, 64
+    const float kOne = __uint_as_float(opaque(0x3F800000u));
+    // 8 codes (k order) -> 4 bf16 pairs of exact q - z; ce = -(1024 + z), co = -(64 + z)
+    auto decode = [&](uint32_t w, float ce, float co) __attribute__((always_inline)) {
+        typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+        const uint32_t w8 = w >> 8;
+        const h2_t p0 = __builtin_bit_cast(h2_t, (w & kM0) | kC0), p1 = __builtin_bit_cast(h2_t, (w & kM1) | kC1);
+        const h2_t p2 = __builtin_bit_cast(h2_t, (w8 & kM0) | kC0), p3 = __builtin_bit_cast(h2_t, (w8 & kM1) | kC1);
+        const float q0 = __builtin_fmaf(static_cast<float>(p0.x), kOne, ce), q4 = __builtin_fmaf(static_cast<float>(p0.y), kOne, ce);
+        const float q1 = __builtin_fmaf(static_cast<float>(p1.x), kOne, co), q5 = __builtin_fmaf(static_cast<float>(p1.y), kOne, co);
+        const float q2 = __builtin_fmaf(static_cast<float>(p2.x), kOne, ce), q6 = __builtin_fmaf(static_cast<float>(p2.y), kOne, ce);
+        const float q3 = __builtin_fmaf(static_cast<float>(p3.x), kOne, co), q7 = __builtin_fmaf(static_cast<float>(p3.y), kOne, co);
+        return __builtin_bit_cast(bf16x8_t, make_uint4(pack_hi16(q0, q1), pack_hi16(q2, q3), pack_hi16(q4, q5), pack_hi16(q6, q7)));
+    };
+
+    // One set of partials.  Block b's first MFMA step overwrites pair (i, j) only right after
+    // block b - 1's partials of that pair are scaled into the total, so the VALU work of the
+    // fold runs beside the MFMAs of the other pairs.  Block 0's "previous" partials are zero
+    // with scale zero.
+    floatx16 part[2][J];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) part[i][j][e] = 0.f;
+    float sc_prev[2] = {0.f, 0.f};
+    auto fold = [&](int i, int j) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tot[i][j][e] = __builtin_fmaf(sc_prev[i], part[i][j][e], tot[i][j][e]);
+    };
+
+    auto compute = [&](int b, const uint8_t *__restrict__ stage, const WSet &r) __attribute__((always_inline)) {
+        const int g = b / bpg;
+        float ce[2], co[2], sc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float z = static_cast<float>((r.z[i] >> (4 * (g & 7))) & 15u);
+            ce[i] = -(1024.0f + z);
+            co[i] = -(64.0f + z);
+            sc[i] = f16_to_f32(static_cast<uint16_t>((g & 1) ? (r.s[i] >> 16) : (r.s[i] & 0xFFFFu)));
+        }
+        static_for<8>([&](auto KK) {
+            constexpr int kk = decltype(KK)::value;
+            bf16x8_t xf[J], wf[2];
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                xf[j] = *reinterpret_cast<const bf16x8_t *>(stage + (32 * j + fr) * (kI4KB * 2) + (((8 * h + kk) ^ (fr & 15)) * 16));
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint4 q = r.w[i][kk >> 2];
+                const uint32_t word = (kk & 3) == 0 ? q.x : (kk & 3) == 1 ? q.y : (kk & 3) == 2 ? q.z : q.w;
+                wf[i] = decode(word, ce[i], co[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    if constexpr (kk == 0) {
+                        // the pair's fold, then its first MFMA; nothing moves across the
+                        // barrier, so the reads of the fold stay next to the MFMA that needs
+                        // their registers
+                        if (CFH_PF_I4_FOLD_FIRST) fold(i, j);
+                        floatx16 z{};
+                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[j], wf[i], z, 0, 0, 0);
+                        if (CFH_PF_I4_FOLD_FIRST) __builtin_amdgcn_sched_barrier(0);
+                    } else {
+                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[j], wf[i], part[i][j], 0, 0, 0);
+                    }
+                }
+        });
+        sc_prev[0] = sc[0];
+        sc_prev[1] = sc[1];
+        if (!CFH_PF_I4_FOLD_FIRST) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < J; ++j) fold(i, j);
+        }
+    };
+
+    // Block b: wait for its loads (those of blocks b + 1 .. b + D - 1 may still be in
+    // flight), barrier (every wave's LDS writes of block b landed, every wave is done with
+    // block b - 1's stage), issue block b + D into the stage and register set block b - 1
+    // used, compute block b.  Steps are unrolled S-fold so every register set index is a
+    // constant.
+    constexpr int U = S;
+    WSet ws[S];
+    static_for<D>([&](auto II) {
+        constexpr int i = decltype(II)::value;
+        if (i < KB) issue(i, lds + i * kStage, ws[i]);
+    });
+    // Steady steps (every block of the unrolled group issues its block b + D) are branch-free,
+    // so the compiler's own vmcnt waits cover only the loads being consumed; the last steps
+    // wait for whatever is left.
+    auto step = [&](auto steady, auto SI, int b) __attribute__((always_inline)) {
+        constexpr bool kSteady = decltype(steady)::value;
+        constexpr int si = decltype(SI)::value;
+        if (kSteady || b + D - 1 < KB) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((D - 1) * kLoads) & ~(15 << 8));
+        } else if (D > 2 && b + 1 < KB) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoads) & ~(15 << 8));
+        } else {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));
+        }
+        __builtin_amdgcn_s_barrier();
+        if (kSteady || b + D < KB) issue(b + D, lds + ((si + D) % S) * kStage, ws[(si + D) % S]);
+        compute(b, lds + si * kStage, ws[si]);
+    };
+    int b0 = 0;
+    for (; b0 + U - 1 + D < KB; b0 += U)
+        static_for<U>([&](auto SI) { step(std::true_type{}, SI, b0 + decltype(SI)::value); });
+    for (; b0 < KB; b0 += U)
+        static_for<U>([&](auto SI) {
+            if (b0 + decltype(SI)::value < KB) step(std::false_type{}, SI, b0 + decltype(SI)::value);
+        });
+    // the last block's partials
+    if (CFH_PF_I4_FOLD_FIRST) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < J; ++j) fold(i, j);
+    }
+
+    // ---- epilogue: tot[i][j] reg 4 g + q holds m = m0 + 32 j + 8 g + 4 h + q, n = nw0 + 32 i + fr ----
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int n = nw0 + 32 * i + fr;
+        if (n >= N) continue;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + 32 * j + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (m < M) {
+                    const int64_t o = static_cast<int64_t>(m) * N + n;
+                    if (a.y_bf16) static_cast<uint16_t *>(a.y)[o] = f32_to_bf16_rne(tot[i][j][e]);
+                    else static_cast<float *>(a.y)[o] = tot[i][j][e];
+                }
+            }
+    }
+}
+
+template <int BM, int D>
+void launch_i4(PfArgs a, hipStream_t st) {
+    constexpr int lds = (D + 1) * BM * kI4KB * 2;
+    static std::mutex mu;
+    static std::map<int, bool> attr_set;  // per device
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    {
+        std::lock_guard<std::mutex> g(mu);
+        if (!attr_set[dev]) {
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_i4_kernel<BM, D>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+                      "hipFuncSetAttribute(prefill_i4_kernel)");
+            attr_set[dev] = true;
+        }
+    }
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + kI4BN - 1) / kI4BN;
+    const int64_t tiles = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
+    require(tiles <= 0x7fffffff, "too many tiles");
+    prefill_i4_kernel<BM, D><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), lds, st>>>(a);
+    check_launch("prefill_i4_kernel");
+}
+
 template <int FMT, int BM, int BN, int WN, int R>
 void launch_cfg(PfArgs a, hipStream_t st) {
     constexpr int lds = 2 * stage_bytes<FMT, BM, BN>();
@@ -523,6 +819,25 @@ void launch_fmt(const PfArgs &a, hipStream_t st) {
     }
 }
 
+// INT4 whose groups are whole 128-wide K blocks takes the one-MFMA kernel when its 256 x 128
+// tiles give every CU a workgroup.  CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the
+// generic kernel, =1 sends every one whose groups allow it to the one-MFMA kernel.
+bool i4_eligible(const PfArgs &a) {
+    if (a.group % kI4KB != 0 || a.K % a.group != 0) return false;
+    if (static_cast<int64_t>(128) * a.K * 2 >= (int64_t{1} << 31)) return false;
+    if (const char *e = std::getenv("CASTFORGE_PREFILL_I4")) {
+        if (std::strcmp(e, "0") == 0) return false;
+        if (std::strcmp(e, "1") == 0) return true;
+    }
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    }
+    const int64_t tiles = ((a.M + 127) / 128) * static_cast<int64_t>((a.N + kI4BN - 1) / kI4BN);
+    return tiles >= cus;
+}
+
 }  // namespace
 
 // Routes one problem to the prefill MFMA kernel when its shape allows it.
@@ -537,7 +852,8 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
     if (!aligned(x, 16) || !aligned(codes, 16)) return false;
     PfArgs a{x, codes, scales, zeros, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
-    if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
+    if (fmt == FMT_INT4 && i4_eligible(a)) launch_i4<128, CFH_PF_I4_DEPTH>(a, st);
+    else if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
     else if (fmt == FMT_NF4) launch_fmt<FMT_NF4>(a, st);
     else if (fmt == FMT_Q4G) launch_fmt<FMT_Q4G>(a, st);
     else if (fmt == FMT_Q8G) launch_fmt<FMT_Q8G>(a, st);

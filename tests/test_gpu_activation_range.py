@@ -17,7 +17,11 @@ and per kernel (M = 1 split-K, M = 3 and 16 skinny, M = 40 and 300 prefill):
     weight term: (3 K / 16 + 8) 2^-24 sum |x w|) of 0, and the residuals' RMS no larger than
     the evaluator's;
   * a non-finite x gives non-finite rows.
+INT4 g128 runs a second time with the one-MFMA prefill kernel forced (int4_g128_one): exact
+(q - z) operands, one f32 partial per 128-wide K block scaled into the total.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -61,13 +65,16 @@ class Case:
     def __init__(self, fmt, n, k, dev, seed=11, halves=False):
         self.fmt, self.n, self.k = fmt, n, k
         if fmt.startswith("int4"):
-            g = int(fmt[6:])
+            g = int(fmt.split("_")[1][1:])
             w = _weight(seed, n, k, halves)
             c, s, z = O.quantize_int4g(w, g)
             self.p = ops.Int4Packed(torch.from_numpy(c.view(np.int32)).to(dev),
                                     torch.from_numpy(s.view(np.float16)).to(dev),
                                     torch.from_numpy(z.view(np.int32)).to(dev), n, k, g)
-            self.run = lambda x, out: ops.gemm_w4a16(x, self.p, out)
+            if fmt.endswith("_one"):  # the one-MFMA prefill kernel, forced at every M > 64
+                self.run = lambda x, out: _one_mfma(lambda: ops.gemm_w4a16(x, self.p, out))
+            else:
+                self.run = lambda x, out: ops.gemm_w4a16(x, self.p, out)
             self.oracle = lambda xb: O.gemm_w4a16(xb, c, s, z, n, k, g)
             self.deq = O.dequantize_int4g(c, s, z, n, k, g)
         elif fmt == "int8":
@@ -95,7 +102,21 @@ class Case:
         self.deq = np.asarray(self.deq, np.float64).reshape(n, k)
 
 
-FORMATS = ["int4_g128", "int4_g64", "int4_g32", "int8", "nf4", "q4_0", "q8_0"]
+def _one_mfma(call):
+    """Runs call with CASTFORGE_PREFILL_I4=1: INT4 prefill problems whose groups are whole
+    128-wide K blocks take the one-MFMA kernel whatever their tile count."""
+    old = os.environ.get("CASTFORGE_PREFILL_I4")
+    os.environ["CASTFORGE_PREFILL_I4"] = "1"
+    try:
+        return call()
+    finally:
+        if old is None:
+            del os.environ["CASTFORGE_PREFILL_I4"]
+        else:
+            os.environ["CASTFORGE_PREFILL_I4"] = old
+
+
+FORMATS = ["int4_g128", "int4_g128_one", "int4_g64", "int4_g32", "int8", "nf4", "q4_0", "q8_0"]
 MS = [1, 3, 16, 40, 300]
 
 
@@ -170,7 +191,7 @@ def test_exact_cancellation(cuda, fmt, m):
     assert rms <= rms_ref + ATOL, (rms, rms_ref)
 
 
-@pytest.mark.parametrize("m", [1, 5, 40])
+@pytest.mark.parametrize("m", [1, 5, 40, 100])
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_nonfinite_x_gives_nonfinite_rows(cuda, fmt, m):
     n, k = 32, 1024

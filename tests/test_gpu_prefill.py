@@ -37,11 +37,26 @@ def _int4(w, group, dev):
     return p, (codes, scales, zeros)
 
 
+# INT4 prefill kernel: "auto" picks by shape (the one-MFMA kernel once its tiles fill the chip),
+# "0" keeps the generic two-term kernel, "1" forces the one-MFMA kernel wherever the groups
+# are whole 128-wide K blocks (CASTFORGE_PREFILL_I4).
+I4_KERNELS = ["auto", "0", "1"]
+
+
+def _i4_kernel(monkeypatch, kernel):
+    if kernel == "auto":
+        monkeypatch.delenv("CASTFORGE_PREFILL_I4", raising=False)
+    else:
+        monkeypatch.setenv("CASTFORGE_PREFILL_I4", kernel)
+
+
+@pytest.mark.parametrize("kernel", I4_KERNELS)
 @pytest.mark.parametrize("m", [17, 64, 130, 256, 300])
 @pytest.mark.parametrize("n,k", [(256, 1024), (300, 512), (520, 2048)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
-def test_w4a16_prefill(cuda, m, n, k, out):
-    print(f"[prefill w4a16] m={m} n={n} k={k} out={out}", flush=True)
+def test_w4a16_prefill(cuda, monkeypatch, kernel, m, n, k, out):
+    _i4_kernel(monkeypatch, kernel)
+    print(f"[prefill w4a16] kernel={kernel} m={m} n={n} k={k} out={out}", flush=True)
     w = synth.weight(81, 1, n, k)
     p, (c, s, z) = _int4(w, 128, cuda)
     xb, x = _x(82, m, k, cuda)
@@ -50,10 +65,12 @@ def test_w4a16_prefill(cuda, m, n, k, out):
     _close(y, O.gemm_w4a16(xb, c, s, z, n, k, 128), "w4a16")
 
 
+@pytest.mark.parametrize("kernel", I4_KERNELS)
 @pytest.mark.parametrize("group", [32, 64, 256, 1024])
-def test_w4a16_prefill_groups(cuda, group):
+def test_w4a16_prefill_groups(cuda, monkeypatch, kernel, group):
+    _i4_kernel(monkeypatch, kernel)
     m, n, k = 96, 264, 2048
-    print(f"[prefill w4a16 group] group={group}", flush=True)
+    print(f"[prefill w4a16 group] kernel={kernel} group={group}", flush=True)
     w = synth.weight(83, 1, n, k)
     p, (c, s, z) = _int4(w, group, cuda)
     xb, x = _x(84, m, k, cuda)
@@ -117,8 +134,10 @@ def test_w8a16_prefill(cuda, m, gran):
     _close(y, O.gemm_w8a16(xb, q.cpu().numpy(), sc), "w8a16")
 
 
-def test_prefill_unaligned_output(cuda):
+@pytest.mark.parametrize("kernel", I4_KERNELS)
+def test_prefill_unaligned_output(cuda, monkeypatch, kernel):
     """N % 4 != 0 and an output view that is not 16-byte aligned take the checked stores."""
+    _i4_kernel(monkeypatch, kernel)
     m, n, k = 70, 262, 512
     w = synth.weight(89, 1, n, k)
     p, (c, s, z) = _int4(w, 128, cuda)
@@ -132,6 +151,29 @@ def test_prefill_unaligned_output(cuda):
     torch.cuda.synchronize()
     _close(y, ref, "unaligned")
     assert buf[0].item() == -7.0, "wrote before the output"
+
+
+@pytest.mark.parametrize("kernel", ["0", "1"])
+def test_w4a16_prefill_special_scales(cuda, monkeypatch, kernel):
+    """Group scales that are f16 subnormals, zero and the largest finite f16 give the
+    oracle's outputs (each is exact in f32 and multiplies an exact partial); a row with one
+    +Inf scale gives non-finite outputs in its column, as the evaluator's Inf weights do."""
+    _i4_kernel(monkeypatch, kernel)
+    m, n, k = 150, 300, 1024
+    w = synth.weight(95, 1, n, k)
+    codes, scales, zeros = O.quantize_int4g(w, 128)
+    sv = scales.view(np.uint16).copy()
+    sv[3, :4] = [0x0001, 0x03FF, 0x0000, 0x7BFF]  # subnormals, zero, 65504
+    sv[7, 2] = 0x7C00                               # +Inf
+    p = ops.Int4Packed(torch.from_numpy(codes.view(np.int32)).to(cuda), torch.from_numpy(sv.view(np.float16)).to(cuda),
+                       torch.from_numpy(zeros.view(np.int32)).to(cuda), n, k, 128)
+    xb, x = _x(96, m, k, cuda)
+    y = ops.gemm_w4a16(x, p, torch.float32).cpu().numpy()
+    assert not np.isfinite(y[:, 7]).any()
+    ok = np.ones(n, bool)
+    ok[7] = False
+    ref = O.gemm_w4a16(xb, codes, sv, zeros, n, k, 128)
+    _close(y[:, ok], ref[:, ok], "special scales")
 
 
 def test_prefill_k_not_multiple_of_32_uses_exact_fallback(cuda):
