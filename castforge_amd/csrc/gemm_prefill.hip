@@ -467,9 +467,11 @@ void prefill_qgemm_kernel(PfArgs a) {
 // y = sum_b s_b * P_b, the GEMV's per-group partial scheme.  Each partial rounds 8 times
 // (one per 16-wide MFMA step) over 128 products and the total once per block, against the
 // evaluator's one rounding per product (eval.rs:1465-1507).
-//   * Tile 256 (n) x BM (m), 4 waves.  Wave w owns n rows [64 w, 64 w + 64) (2 MFMA blocks of
-//     32) and all BM rows of x (BM / 32 blocks).  W is the MFMA B operand, so a lane's
-//     accumulators hold 16 m of one n and one scale multiplies them all.
+//   * Tile 256 (n) x BM (m), NW waves.  Wave w owns n rows [256 / NW * w, 256 / NW * (w + 1))
+//     (I = 8 / NW MFMA blocks of 32) and all BM rows of x (BM / 32 blocks).  W is the MFMA B
+//     operand, so a lane's accumulators hold 16 m of one n and one scale multiplies them all.
+//     At NW = 8 two waves share a SIMD: each holds half the accumulators, and one wave's
+//     decode and fold run while the other's MFMAs do.
 //   * W never touches LDS: each lane loads its row's 32 code bytes of the block (k = 64 h ..
 //     64 h + 63 of the block, h = lane / 32) and decodes word kk for MFMA step kk.  The f16
 //     pairs 1024 + q (even nibbles, at mantissa bits 0..3) and 64 + q (odd nibbles, at bits
@@ -489,18 +491,26 @@ void prefill_qgemm_kernel(PfArgs a) {
 #ifndef CFH_PF_I4_FOLD_FIRST
 #define CFH_PF_I4_FOLD_FIRST 0
 #endif
+// waves per workgroup: 8 (two per SIMD, 32 W rows each; measured 1.13-1.17x faster at
+// M = 4096) or 4 (one per SIMD, 64 rows each)
+#ifndef CFH_PF_I4_WAVES
+#define CFH_PF_I4_WAVES 8
+#endif
 constexpr int kI4BN = 256;
 constexpr int kI4KB = 128;
 
-template <int BM, int D>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <int BM, int D, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void prefill_i4_kernel(PfArgs a) {
     constexpr int J = BM / 32;
+    constexpr int I = kI4BN / 32 / NW;  // MFMA row blocks of W per wave
+    constexpr int kRowsW = kI4BN / NW;  // W rows per wave
     constexpr int S = D + 1;
     constexpr int kStage = BM * kI4KB * 2;
-    constexpr int kDma = BM / 16;            // 1 KB buffer -> LDS loads per wave and block
-    constexpr int kLoads = kDma + 2 * 2 + 2 * 2;  // vector-memory loads per wave and block
-    static_assert(BM % 64 == 0 && S * kStage <= 160 * 1024, "tile / LDS budget");
+    constexpr int kRowsX = BM / NW;          // x rows each wave loads
+    constexpr int kDma = kRowsX / 4;         // 1 KB buffer -> LDS loads per wave and block
+    constexpr int kLoads = kDma + I * 4;     // vector-memory loads per wave and block
+    static_assert(I >= 1 && kRowsX % 16 == 0 && S * kStage <= 160 * 1024, "tile / LDS budget");
     extern __shared__ __align__(16) uint8_t lds[];
 
     const int M = a.M, N = a.N, K = a.K;
@@ -526,15 +536,15 @@ void prefill_i4_kernel(PfArgs a) {
     const rsrc_t rx = make_rsrc(a.x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(min(BM, M - m0)) * K * 2);
     // descriptors over the tile's rows [n0, n0 + n_valid) (rows past N read zero); a lane's
     // row is 64 wave + 32 i + fr of the tile
-    const int nw0 = n0 + 64 * wave;
+    const int nw0 = n0 + kRowsW * wave;
     const uint32_t n_valid = static_cast<uint32_t>(min(kI4BN, N - n0));
     const rsrc_t rw = make_rsrc(static_cast<const uint8_t *>(a.codes) + static_cast<int64_t>(n0) * (K / 2), n_valid * (K / 2));
     const rsrc_t rs = make_rsrc(static_cast<const uint16_t *>(a.scales) + static_cast<int64_t>(n0) * GP, n_valid * GP * 2);
     const rsrc_t rz = make_rsrc(a.zeros + static_cast<int64_t>(n0) * ZW, n_valid * ZW * 4);
-    uint32_t vw[2], vs[2], vz[2];
+    uint32_t vw[I], vs[I], vz[I];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t row = static_cast<uint32_t>(64 * wave + 32 * i + fr);
+    for (int i = 0; i < I; ++i) {
+        const uint32_t row = static_cast<uint32_t>(kRowsW * wave + 32 * i + fr);
         vw[i] = row * static_cast<uint32_t>(K / 2) + 32u * h;
         vs[i] = row * static_cast<uint32_t>(GP) * 2u;
         vz[i] = row * static_cast<uint32_t>(ZW) * 4u;
@@ -549,19 +559,19 @@ void prefill_i4_kernel(PfArgs a) {
     }
 
     struct WSet {
-        uint4 w[2][2];  // [row block i][k half]: words 0..3, 4..7 of the lane's 32 code bytes
-        uint32_t s[2], z[2];
+        uint4 w[I][2];  // [row block i][k half]: words 0..3, 4..7 of the lane's 32 code bytes
+        uint32_t s[I], z[I];
     };
     auto issue = [&](int b, uint8_t *stage, WSet &r) __attribute__((always_inline)) {
-        uint8_t *dst = stage + (BM / 4) * wave * (kI4KB * 2);
+        uint8_t *dst = stage + kRowsX * wave * (kI4KB * 2);
 #pragma unroll
         for (int t = 0; t < kDma; ++t)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rx, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(dst + t * 1024)),
-                16, lv[t & 3], ((BM / 4) * wave + 4 * t) * K * 2 + b * (kI4KB * 2), 0, 0);
+                16, lv[t & 3], (kRowsX * wave + 4 * t) * K * 2 + b * (kI4KB * 2), 0, 0);
         const int g = b / bpg;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < I; ++i) {
             r.w[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64, 0, 0));
             r.w[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64 + 16, 0, 0));
             r.s[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, vs[i] + (g & ~1) * 2, 0, 0);
@@ -569,9 +579,9 @@ void prefill_i4_kernel(PfArgs a) {
         }
     };
 
-    floatx16 tot[2][J];
+    floatx16 tot[I][J];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < I; ++i)
 #pragma unroll
         for (int j = 0; j < J; ++j)
 #pragma unroll
@@ -603,14 +613,14 @@ void prefill_i4_kernel(PfArgs a) {
     // block b - 1's partials of that pair are scaled into the total, so the VALU work of the
     // fold runs beside the MFMAs of the other pairs.  Block 0's "previous" partials are zero
     // with scale zero.
-    floatx16 part[2][J];
+    floatx16 part[I][J];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < I; ++i)
 #pragma unroll
         for (int j = 0; j < J; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) part[i][j][e] = 0.f;
-    float sc_prev[2] = {0.f, 0.f};
+    float sc_prev[I] = {};
     auto fold = [&](int i, int j) __attribute__((always_inline)) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) tot[i][j][e] = __builtin_fmaf(sc_prev[i], part[i][j][e], tot[i][j][e]);
@@ -618,9 +628,9 @@ void prefill_i4_kernel(PfArgs a) {
 
     auto compute = [&](int b, const uint8_t *__restrict__ stage, const WSet &r) __attribute__((always_inline)) {
         const int g = b / bpg;
-        float ce[2], co[2], sc[2];
+        float ce[I], co[I], sc[I];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < I; ++i) {
             const float z = static_cast<float>((r.z[i] >> (4 * (g & 7))) & 15u);
             ce[i] = -(1024.0f + z);
             co[i] = -(64.0f + z);
@@ -628,18 +638,18 @@ void prefill_i4_kernel(PfArgs a) {
         }
         static_for<8>([&](auto KK) {
             constexpr int kk = decltype(KK)::value;
-            bf16x8_t xf[J], wf[2];
+            bf16x8_t xf[J], wf[I];
 #pragma unroll
             for (int j = 0; j < J; ++j)
                 xf[j] = *reinterpret_cast<const bf16x8_t *>(stage + (32 * j + fr) * (kI4KB * 2) + (((8 * h + kk) ^ (fr & 15)) * 16));
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < I; ++i) {
                 const uint4 q = r.w[i][kk >> 2];
                 const uint32_t word = (kk & 3) == 0 ? q.x : (kk & 3) == 1 ? q.y : (kk & 3) == 2 ? q.z : q.w;
                 wf[i] = decode(word, ce[i], co[i]);
             }
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < I; ++i)
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     if constexpr (kk == 0) {
@@ -655,11 +665,11 @@ void prefill_i4_kernel(PfArgs a) {
                     }
                 }
         });
-        sc_prev[0] = sc[0];
-        sc_prev[1] = sc[1];
+#pragma unroll
+        for (int i = 0; i < I; ++i) sc_prev[i] = sc[i];
         if (!CFH_PF_I4_FOLD_FIRST) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < I; ++i)
 #pragma unroll
                 for (int j = 0; j < J; ++j) fold(i, j);
         }
@@ -703,14 +713,14 @@ void prefill_i4_kernel(PfArgs a) {
     // the last block's partials
     if (CFH_PF_I4_FOLD_FIRST) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < I; ++i)
 #pragma unroll
             for (int j = 0; j < J; ++j) fold(i, j);
     }
 
     // ---- epilogue: tot[i][j] reg 4 g + q holds m = m0 + 32 j + 8 g + 4 h + q, n = nw0 + 32 i + fr ----
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < I; ++i) {
         const int n = nw0 + 32 * i + fr;
         if (n >= N) continue;
 #pragma unroll
@@ -727,7 +737,7 @@ void prefill_i4_kernel(PfArgs a) {
     }
 }
 
-template <int BM, int D>
+template <int BM, int D, int NW>
 void launch_i4(PfArgs a, hipStream_t st) {
     constexpr int lds = (D + 1) * BM * kI4KB * 2;
     static std::mutex mu;
@@ -737,7 +747,7 @@ void launch_i4(PfArgs a, hipStream_t st) {
     {
         std::lock_guard<std::mutex> g(mu);
         if (!attr_set[dev]) {
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_i4_kernel<BM, D>),
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_i4_kernel<BM, D, NW>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds),
                       "hipFuncSetAttribute(prefill_i4_kernel)");
             attr_set[dev] = true;
@@ -747,7 +757,7 @@ void launch_i4(PfArgs a, hipStream_t st) {
     a.tiles_n = (a.N + kI4BN - 1) / kI4BN;
     const int64_t tiles = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
     require(tiles <= 0x7fffffff, "too many tiles");
-    prefill_i4_kernel<BM, D><<<dim3(static_cast<unsigned>(tiles)), dim3(kThreads), lds, st>>>(a);
+    prefill_i4_kernel<BM, D, NW><<<dim3(static_cast<unsigned>(tiles)), dim3(64 * NW), lds, st>>>(a);
     check_launch("prefill_i4_kernel");
 }
 
@@ -852,7 +862,7 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
     if (!aligned(x, 16) || !aligned(codes, 16)) return false;
     PfArgs a{x, codes, scales, zeros, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
-    if (fmt == FMT_INT4 && i4_eligible(a)) launch_i4<128, CFH_PF_I4_DEPTH>(a, st);
+    if (fmt == FMT_INT4 && i4_eligible(a)) launch_i4<128, CFH_PF_I4_DEPTH, CFH_PF_I4_WAVES>(a, st);
     else if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
     else if (fmt == FMT_NF4) launch_fmt<FMT_NF4>(a, st);
     else if (fmt == FMT_Q4G) launch_fmt<FMT_Q4G>(a, st);
