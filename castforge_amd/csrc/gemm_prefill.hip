@@ -487,9 +487,13 @@ void prefill_qgemm_kernel(PfArgs a) {
 #define CFH_PF_I4_DEPTH 2
 #endif
 // 1: block b - 1's partials are folded pair by pair in block b's first MFMA step; 0: at the
-// end of block b - 1
+// end of block b - 1 (with 8 waves the first is 1-2 % faster)
 #ifndef CFH_PF_I4_FOLD_FIRST
-#define CFH_PF_I4_FOLD_FIRST 0
+#define CFH_PF_I4_FOLD_FIRST 1
+#endif
+// 1: a step's x fragments are read during the previous step's MFMAs
+#ifndef CFH_PF_I4_XPREFETCH
+#define CFH_PF_I4_XPREFETCH 1
 #endif
 // waves per workgroup: 8 (two per SIMD, 32 W rows each; measured 1.13-1.17x faster at
 // M = 4096) or 4 (one per SIMD, 64 rows each)
@@ -636,12 +640,20 @@ void prefill_i4_kernel(PfArgs a) {
             co[i] = -(64.0f + z);
             sc[i] = f16_to_f32(static_cast<uint16_t>((g & 1) ? (r.s[i] >> 16) : (r.s[i] & 0xFFFFu)));
         }
-        static_for<8>([&](auto KK) {
-            constexpr int kk = decltype(KK)::value;
-            bf16x8_t xf[J], wf[I];
+        // x fragments of step kk + 1 are read while step kk's MFMAs run (two sets)
+        bf16x8_t xf[2][J];
+        auto read_x = [&](int kk, bf16x8_t (&dst)[J]) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < J; ++j)
-                xf[j] = *reinterpret_cast<const bf16x8_t *>(stage + (32 * j + fr) * (kI4KB * 2) + (((8 * h + kk) ^ (fr & 15)) * 16));
+                dst[j] = *reinterpret_cast<const bf16x8_t *>(stage + (32 * j + fr) * (kI4KB * 2) + (((8 * h + kk) ^ (fr & 15)) * 16));
+        };
+        if (CFH_PF_I4_XPREFETCH) read_x(0, xf[0]);
+        static_for<8>([&](auto KK) {
+            constexpr int kk = decltype(KK)::value;
+            constexpr int xs = CFH_PF_I4_XPREFETCH ? (kk & 1) : 0;
+            bf16x8_t wf[I];
+            if (!CFH_PF_I4_XPREFETCH) read_x(kk, xf[0]);
+            else if (kk + 1 < 8) read_x(kk + 1, xf[xs ^ 1]);
 #pragma unroll
             for (int i = 0; i < I; ++i) {
                 const uint4 q = r.w[i][kk >> 2];
@@ -658,10 +670,10 @@ void prefill_i4_kernel(PfArgs a) {
                         // their registers
                         if (CFH_PF_I4_FOLD_FIRST) fold(i, j);
                         floatx16 z{};
-                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[j], wf[i], z, 0, 0, 0);
+                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[xs][j], wf[i], z, 0, 0, 0);
                         if (CFH_PF_I4_FOLD_FIRST) __builtin_amdgcn_sched_barrier(0);
                     } else {
-                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[j], wf[i], part[i][j], 0, 0, 0);
+                        part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[xs][j], wf[i], part[i][j], 0, 0, 0);
                     }
                 }
         });
