@@ -841,9 +841,12 @@ void launch_fmt(const PfArgs &a, hipStream_t st) {
     }
 }
 
-// INT4 whose groups are whole 128-wide K blocks takes the one-MFMA kernel when its 256 x 128
-// tiles give every CU a workgroup.  CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the
-// generic kernel, =1 sends every one whose groups allow it to the one-MFMA kernel.
+// INT4 whose groups are whole 128-wide K blocks takes the one-MFMA kernel once it has at least
+// one 256 x 128 tile per 6 CUs (43 on 256 CUs).  Measured against the generic kernel's smaller
+// tiles: 11008 x 4096 (43 n-tiles) at M = 96 / 512 / 1024: 57 / 61 / 125 us against 65 / 128 /
+// 290; 4096 x 11008 (16 n-tiles) at M = 256 / 512: 143 / 143 us against 121 / 199.
+// CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the generic kernel, =1 sends every one
+// whose groups allow it to the one-MFMA kernel.
 bool i4_eligible(const PfArgs &a) {
     if (a.group % kI4KB != 0 || a.K % a.group != 0) return false;
     if (static_cast<int64_t>(128) * a.K * 2 >= (int64_t{1} << 31)) return false;
@@ -857,7 +860,7 @@ bool i4_eligible(const PfArgs &a) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
     }
     const int64_t tiles = ((a.M + 127) / 128) * static_cast<int64_t>((a.N + kI4BN - 1) / kI4BN);
-    return tiles >= cus;
+    return 6 * tiles >= cus;
 }
 
 }  // namespace
