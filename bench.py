@@ -395,7 +395,7 @@ def main():
             xp = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
             pp = packed0[4 if name == "w_gate" else 6]
             yp = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-            st = time_steps(lambda i: ops.gemm_w4a16(xp, pp, torch.bfloat16), 10, 2)
+            st = time_steps(lambda i: ops.gemm_w4a16(xp, pp, torch.bfloat16), 10, 2, min_ms=30.0, replays=3)
             components[f"w4a16_prefill_m{m}_n{n}_k{k}_TFLOPs"] = round(2.0 * m * n * k / (st * 1e-3) / 1e12, 1)
             log(f"[bench] W4A16 prefill M={m} {name}: {st * 1e3:.1f} us, "
                 f"{components[f'w4a16_prefill_m{m}_n{n}_k{k}_TFLOPs']} TFLOP/s")
