@@ -15,9 +15,10 @@
 //   Q8_0  q * d (19 bits) and NF4 f32(T[q] * absmax) (24 bits): three terms.
 //   A non-finite scale gives a non-finite weight (the remainder terms are 0) and so, as in the
 //   evaluator, non-finite outputs on its row.
-//   INT4 whose groups are whole 128-wide K blocks has a second kernel, prefill_i4_kernel below:
-//   one MFMA per product on the exact integer (q - z), a fresh f32 partial per K block, and the
-//   block's group scale applied to the partial by one fma into the running total.
+//   INT4 whose groups are whole 128-wide K blocks, and GGUF Q4_0 planes, have a second
+//   kernel, prefill_i4_kernel below: one MFMA per product on the exact integer (q - z), a
+//   fresh f32 partial per group (Q4_0: per 32-wide block), and the group's scale applied to
+//   the partial by one fma into the running total.
 //   (A one-term INT4 form that instead multiplied the running accumulator by s_prev / s_cur
 //   at every group start was measured and dropped: the rounding of the running sum put
 //   near-zero outputs of cancellation-heavy rows further from the exact value than the
@@ -459,8 +460,10 @@ void prefill_qgemm_kernel(PfArgs a) {
     });
 }
 
-// ---- INT4 with groups of a multiple of 128: one MFMA per product ----
+// ---- INT4 with groups of a multiple of 128, and GGUF Q4_0 planes: one MFMA per product ----
 //
+// (Q4_0: z = 8 and a d per 32-wide block, so a fold every two MFMA steps; the words of the
+// planes map to k as described at WSet below.)
 // `prefill_i4_kernel<BM, D>` feeds the MFMA the exact integer (q - z) as bf16 (|q - z| <= 15)
 // and x as the bf16 it is.  Per 128-wide K block the MFMAs sum x (q - z) into a fresh f32
 // partial, and one fma per accumulator applies the block's f16 group scale:
@@ -491,6 +494,10 @@ void prefill_qgemm_kernel(PfArgs a) {
 #ifndef CFH_PF_I4_FOLD_FIRST
 #define CFH_PF_I4_FOLD_FIRST 1
 #endif
+// prefetch depth of the Q4_0 planes form
+#ifndef CFH_PF_Q4_DEPTH
+#define CFH_PF_Q4_DEPTH 2
+#endif
 // 1: a step's x fragments are read during the previous step's MFMAs
 #ifndef CFH_PF_I4_XPREFETCH
 #define CFH_PF_I4_XPREFETCH 1
@@ -503,9 +510,12 @@ void prefill_qgemm_kernel(PfArgs a) {
 constexpr int kI4BN = 256;
 constexpr int kI4KB = 128;
 
-template <int BM, int D, int NW>
+template <int BM, int D, int NW, int FMT>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void prefill_i4_kernel(PfArgs a) {
+    static_assert(FMT == FMT_INT4 || FMT == FMT_Q4G, "INT4 or GGUF Q4_0 planes");
+    constexpr bool kQ4 = FMT == FMT_Q4G;
+    static_assert(!kQ4 || CFH_PF_I4_FOLD_FIRST, "Q4_0 folds at the start of each 32-wide block");
     constexpr int J = BM / 32;
     constexpr int I = kI4BN / 32 / NW;  // MFMA row blocks of W per wave
     constexpr int kRowsW = kI4BN / NW;  // W rows per wave
@@ -513,7 +523,7 @@ void prefill_i4_kernel(PfArgs a) {
     constexpr int kStage = BM * kI4KB * 2;
     constexpr int kRowsX = BM / NW;          // x rows each wave loads
     constexpr int kDma = kRowsX / 4;         // 1 KB buffer -> LDS loads per wave and block
-    constexpr int kLoads = kDma + I * 4;     // vector-memory loads per wave and block
+    constexpr int kLoads = kDma + I * (kQ4 ? 3 : 4);  // vector-memory loads per wave and block
     static_assert(I >= 1 && kRowsX % 16 == 0 && S * kStage <= 160 * 1024, "tile / LDS budget");
     extern __shared__ __align__(16) uint8_t lds[];
 
@@ -562,9 +572,12 @@ void prefill_i4_kernel(PfArgs a) {
         lv[u] = static_cast<uint32_t>((lane >> 4) * K * 2 + (((lane & 15) ^ (r & 15)) * 16));
     }
 
+    // INT4: word t of the lane's 32 code bytes holds k = 64 h + 8 t .. + 7 of the block.
+    // Q4_0 planes: 8-element piece p of 32-wide block bb sits at byte 16 p + 4 bb of the row's
+    // 64-byte chunk, so word 4 pp + bb (pp = p - 2 h) holds k = 32 bb + 16 h + 8 pp .. + 7.
     struct WSet {
-        uint4 w[I][2];  // [row block i][k half]: words 0..3, 4..7 of the lane's 32 code bytes
-        uint32_t s[I], z[I];
+        uint4 w[I][2];  // [row block i][half]: words 0..3, 4..7 of the lane's 32 code bytes
+        uint32_t s[I][2], z[I];  // INT4: s[i][0] = the f16 scale pair; Q4_0: the block's 4 d
     };
     auto issue = [&](int b, uint8_t *stage, WSet &r) __attribute__((always_inline)) {
         uint8_t *dst = stage + kRowsX * wave * (kI4KB * 2);
@@ -578,8 +591,14 @@ void prefill_i4_kernel(PfArgs a) {
         for (int i = 0; i < I; ++i) {
             r.w[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64, 0, 0));
             r.w[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64 + 16, 0, 0));
-            r.s[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, vs[i] + (g & ~1) * 2, 0, 0);
-            r.z[i] = __builtin_amdgcn_raw_buffer_load_b32(rz, vz[i] + (g >> 3) * 4, 0, 0);
+            if constexpr (kQ4) {
+                const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs[i] + b * 8, 0, 0));
+                r.s[i][0] = d.x;
+                r.s[i][1] = d.y;
+            } else {
+                r.s[i][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, vs[i] + (g & ~1) * 2, 0, 0);
+                r.z[i] = __builtin_amdgcn_raw_buffer_load_b32(rz, vz[i] + (g >> 3) * 4, 0, 0);
+            }
         }
     };
 
@@ -635,50 +654,72 @@ void prefill_i4_kernel(PfArgs a) {
         float ce[I], co[I], sc[I];
 #pragma unroll
         for (int i = 0; i < I; ++i) {
-            const float z = static_cast<float>((r.z[i] >> (4 * (g & 7))) & 15u);
+            const float z = kQ4 ? 8.0f : static_cast<float>((r.z[i] >> (4 * (g & 7))) & 15u);
             ce[i] = -(1024.0f + z);
             co[i] = -(64.0f + z);
-            sc[i] = f16_to_f32(static_cast<uint16_t>((g & 1) ? (r.s[i] >> 16) : (r.s[i] & 0xFFFFu)));
+            sc[i] = f16_to_f32(static_cast<uint16_t>((g & 1) ? (r.s[i][0] >> 16) : (r.s[i][0] & 0xFFFFu)));
         }
-        // x fragments of step kk + 1 are read while step kk's MFMAs run (two sets)
+        // x fragments of step kk + 1 are read while step kk's MFMAs run (two sets); step kk
+        // reads the 16-byte chunk holding the k range its W word covers
         bf16x8_t xf[2][J];
         auto read_x = [&](int kk, bf16x8_t (&dst)[J]) __attribute__((always_inline)) {
+            const int c = kQ4 ? 4 * (kk >> 1) + 2 * h + (kk & 1) : 8 * h + kk;
 #pragma unroll
             for (int j = 0; j < J; ++j)
-                dst[j] = *reinterpret_cast<const bf16x8_t *>(stage + (32 * j + fr) * (kI4KB * 2) + (((8 * h + kk) ^ (fr & 15)) * 16));
+                dst[j] = *reinterpret_cast<const bf16x8_t *>(stage + (32 * j + fr) * (kI4KB * 2) + ((c ^ (fr & 15)) * 16));
         };
-        if (CFH_PF_I4_XPREFETCH) read_x(0, xf[0]);
+        // (Q4_0 reads each step's fragments in the step: its extra folds leave no registers
+        // for a second set)
+        constexpr bool kXPre = CFH_PF_I4_XPREFETCH && !kQ4;
+        if (kXPre) read_x(0, xf[0]);
         static_for<8>([&](auto KK) {
             constexpr int kk = decltype(KK)::value;
-            constexpr int xs = CFH_PF_I4_XPREFETCH ? (kk & 1) : 0;
+            constexpr int xs = kXPre ? (kk & 1) : 0;
             bf16x8_t wf[I];
-            if (!CFH_PF_I4_XPREFETCH) read_x(kk, xf[0]);
+            if (!kXPre) read_x(kk, xf[0]);
             else if (kk + 1 < 8) read_x(kk + 1, xf[xs ^ 1]);
+            // INT4: word kk; Q4_0: word 4 (kk & 1) + kk / 2 (block kk / 2, half kk & 1)
+            constexpr int half = kQ4 ? (kk & 1) : (kk >> 2), comp = kQ4 ? (kk >> 1) : (kk & 3);
+            // Q4_0: nothing moves across a 32-wide block start (the compiler would otherwise
+            // hoist later blocks' decodes above the folds and run out of registers)
+            if constexpr (kQ4 && (kk & 1) == 0 && kk > 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < I; ++i) {
-                const uint4 q = r.w[i][kk >> 2];
-                const uint32_t word = (kk & 3) == 0 ? q.x : (kk & 3) == 1 ? q.y : (kk & 3) == 2 ? q.z : q.w;
+                const uint4 q = r.w[i][half];
+                const uint32_t word = comp == 0 ? q.x : comp == 1 ? q.y : comp == 2 ? q.z : q.w;
                 wf[i] = decode(word, ce[i], co[i]);
             }
+            // Q4_0: a new 32-wide block (and scale) every two steps
+            constexpr bool kStart = kQ4 ? (kk & 1) == 0 : kk == 0;
 #pragma unroll
             for (int i = 0; i < I; ++i)
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
-                    if constexpr (kk == 0) {
+                    if constexpr (kStart) {
                         // the pair's fold, then its first MFMA; nothing moves across the
                         // barrier, so the reads of the fold stay next to the MFMA that needs
                         // their registers
                         if (CFH_PF_I4_FOLD_FIRST) fold(i, j);
                         floatx16 z{};
                         part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[xs][j], wf[i], z, 0, 0, 0);
-                        if (CFH_PF_I4_FOLD_FIRST) __builtin_amdgcn_sched_barrier(0);
+                        if (CFH_PF_I4_FOLD_FIRST && !kQ4) __builtin_amdgcn_sched_barrier(0);
                     } else {
                         part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[xs][j], wf[i], part[i][j], 0, 0, 0);
                     }
                 }
-        });
+            if constexpr (kQ4 && kStart) {
+                // block kk / 2's d scales the partial that the next block start folds
 #pragma unroll
-        for (int i = 0; i < I; ++i) sc_prev[i] = sc[i];
+                for (int i = 0; i < I; ++i) {
+                    const uint32_t dw = r.s[i][kk >> 2];
+                    sc_prev[i] = f16_to_f32(static_cast<uint16_t>((kk & 2) ? (dw >> 16) : (dw & 0xFFFFu)));
+                }
+            }
+        });
+        if constexpr (!kQ4) {
+#pragma unroll
+            for (int i = 0; i < I; ++i) sc_prev[i] = sc[i];
+        }
         if (!CFH_PF_I4_FOLD_FIRST) {
 #pragma unroll
             for (int i = 0; i < I; ++i)
@@ -749,7 +790,7 @@ void prefill_i4_kernel(PfArgs a) {
     }
 }
 
-template <int BM, int D, int NW>
+template <int BM, int D, int NW, int FMT>
 void launch_i4(PfArgs a, hipStream_t st) {
     constexpr int lds = (D + 1) * BM * kI4KB * 2;
     static std::mutex mu;
@@ -759,7 +800,7 @@ void launch_i4(PfArgs a, hipStream_t st) {
     {
         std::lock_guard<std::mutex> g(mu);
         if (!attr_set[dev]) {
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_i4_kernel<BM, D, NW>),
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_i4_kernel<BM, D, NW, FMT>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds),
                       "hipFuncSetAttribute(prefill_i4_kernel)");
             attr_set[dev] = true;
@@ -769,7 +810,7 @@ void launch_i4(PfArgs a, hipStream_t st) {
     a.tiles_n = (a.N + kI4BN - 1) / kI4BN;
     const int64_t tiles = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
     require(tiles <= 0x7fffffff, "too many tiles");
-    prefill_i4_kernel<BM, D, NW><<<dim3(static_cast<unsigned>(tiles)), dim3(64 * NW), lds, st>>>(a);
+    prefill_i4_kernel<BM, D, NW, FMT><<<dim3(static_cast<unsigned>(tiles)), dim3(64 * NW), lds, st>>>(a);
     check_launch("prefill_i4_kernel");
 }
 
@@ -847,8 +888,8 @@ void launch_fmt(const PfArgs &a, hipStream_t st) {
 // 290; 4096 x 11008 (16 n-tiles) at M = 256 / 512: 143 / 143 us against 121 / 199.
 // CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the generic kernel, =1 sends every one
 // whose groups allow it to the one-MFMA kernel.
-bool i4_eligible(const PfArgs &a) {
-    if (a.group % kI4KB != 0 || a.K % a.group != 0) return false;
+bool i4_eligible(const PfArgs &a, int fmt) {
+    if (fmt == FMT_Q4G ? a.K % kI4KB != 0 : (a.group % kI4KB != 0 || a.K % a.group != 0)) return false;
     if (static_cast<int64_t>(128) * a.K * 2 >= (int64_t{1} << 31)) return false;
     if (const char *e = std::getenv("CASTFORGE_PREFILL_I4")) {
         if (std::strcmp(e, "0") == 0) return false;
@@ -877,7 +918,8 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
     if (!aligned(x, 16) || !aligned(codes, 16)) return false;
     PfArgs a{x, codes, scales, zeros, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
-    if (fmt == FMT_INT4 && i4_eligible(a)) launch_i4<128, CFH_PF_I4_DEPTH, CFH_PF_I4_WAVES>(a, st);
+    if (fmt == FMT_INT4 && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_I4_DEPTH, CFH_PF_I4_WAVES, FMT_INT4>(a, st);
+    else if (fmt == FMT_Q4G && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q4_DEPTH, CFH_PF_I4_WAVES, FMT_Q4G>(a, st);
     else if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
     else if (fmt == FMT_NF4) launch_fmt<FMT_NF4>(a, st);
     else if (fmt == FMT_Q4G) launch_fmt<FMT_Q4G>(a, st);

@@ -17,8 +17,9 @@ and per kernel (M = 1 split-K, M = 3 and 16 skinny, M = 40 and 300 prefill):
     weight term: (3 K / 16 + 8) 2^-24 sum |x w|) of 0, and the residuals' RMS no larger than
     the evaluator's;
   * a non-finite x gives non-finite rows.
-INT4 g128 runs a second time with the one-MFMA prefill kernel forced (int4_g128_one): exact
-(q - z) operands, one f32 partial per 128-wide K block scaled into the total.
+INT4 g128 and GGUF Q4_0 run a second time with the one-MFMA prefill kernel forced
+(int4_g128_one, q4_0_one): exact (q - z) operands, one f32 partial per 128-wide K block (Q4_0:
+per 32-wide block) scaled into the total.
 """
 import os
 
@@ -92,10 +93,13 @@ class Case:
             self.oracle = lambda xb: O.gemm_nf4(xb, c, am, n, k, 64)
             self.deq = O.dequantize_nf4(c, am, n, k, 64)
         else:
-            ty = Q4_0 if fmt == "q4_0" else Q8_0
+            ty = Q4_0 if fmt.startswith("q4_0") else Q8_0
             raw = _gguf_raw(ty, seed, n, k, halves)
             self.p = ops.gguf_repack(ty, torch.from_numpy(raw).to(dev), n, k)
-            self.run = lambda x, out: ops.gemm_gguf(x, self.p, out)
+            if fmt.endswith("_one"):  # the one-MFMA prefill kernel, forced at every M > 64
+                self.run = lambda x, out: _one_mfma(lambda: ops.gemm_gguf(x, self.p, out))
+            else:
+                self.run = lambda x, out: ops.gemm_gguf(x, self.p, out)
             wd = O.gguf_decode(ty, raw, n * k).reshape(n, k)
             self.oracle = lambda xb: O.matmul_2d(O.bf16_bits_to_f32(xb), wd, packed_rhs=True)
             self.deq = wd
@@ -116,7 +120,7 @@ def _one_mfma(call):
             os.environ["CASTFORGE_PREFILL_I4"] = old
 
 
-FORMATS = ["int4_g128", "int4_g128_one", "int4_g64", "int4_g32", "int8", "nf4", "q4_0", "q8_0"]
+FORMATS = ["int4_g128", "int4_g128_one", "int4_g64", "int4_g32", "int8", "nf4", "q4_0", "q4_0_one", "q8_0"]
 MS = [1, 3, 16, 40, 300]
 
 

@@ -193,12 +193,20 @@ def test_gemv_matches_oracle(cuda, ty, m, n, k, out):
     _close(y, ref)
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 96, 1024), (300, 256, 4096), (17, 48, 256)])
-def test_q4_0_prefill_and_int4g_form(cuda, m, n, k):
+@pytest.mark.parametrize("kernel", ["auto", "0", "1"])
+@pytest.mark.parametrize("special", [False, True])
+@pytest.mark.parametrize("m,n,k", [(64, 96, 1024), (300, 256, 4096), (17, 48, 256), (130, 1000, 2048), (129, 257, 640)])
+def test_q4_0_prefill_and_int4g_form(cuda, monkeypatch, kernel, special, m, n, k):
     """Q4_0 at M > 16: the prefill MFMA kernel reading the planes matches the oracle's
     decode-then-matmul, and the INT4g form of the planes dequantizes to the same values bit
-    for bit."""
-    raw = _blocks(Q4_0, n * k // 32, 700 + m)
+    for bit.  kernel: CASTFORGE_PREFILL_I4 ("1" forces the one-MFMA kernel, exact q - 8 with
+    one f32 partial per 32-wide block scaled by its d; "0" the two-term kernel); special: d
+    values that are subnormal, zero, -0, negative and the largest finite f16."""
+    if kernel == "auto":
+        monkeypatch.delenv("CASTFORGE_PREFILL_I4", raising=False)
+    else:
+        monkeypatch.setenv("CASTFORGE_PREFILL_I4", kernel)
+    raw = _blocks(Q4_0, n * k // 32, 700 + m, special)
     p = ops.gguf_repack(Q4_0, _dev_u8(raw, cuda), n, k)
     i4 = ops.gguf_q4_0_to_int4g(p)
     _same(ops.dequantize_int4g(i4).cpu().numpy().reshape(-1), O.gguf_decode(Q4_0, raw, n * k))
