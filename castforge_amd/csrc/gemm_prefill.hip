@@ -838,9 +838,9 @@ void launch_cfg(PfArgs a, hipStream_t st) {
     check_launch("prefill_qgemm");
 }
 
-// Tile shapes, largest first.  The largest one that still gives every CU a workgroup is used;
-// small M or N falls through to smaller tiles rather than leaving CUs idle (NF4 at M = 64 over
-// an 11008 x 4096 matrix: 227 us with 256 x 256 tiles, 45 us with 64 x 64).
+// Tile shapes, largest first.  The largest square one that still gives every CU a workgroup
+// is used; small M or N falls through to smaller tiles rather than leaving CUs idle (NF4 at
+// M = 64 over an 11008 x 4096 matrix: 227 us with 256 x 256 tiles, 45 us with 64 x 64).
 // CASTFORGE_PREFILL_TILE (e.g. "64x128") forces a shape.
 // register sets in flight per tile shape (slices loaded ahead of their LDS write)
 #ifndef CFH_PF_R_256
@@ -876,7 +876,11 @@ int pick_tile(int64_t M, int64_t N) {
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
     }
-    for (int t = 0; t < PF_NTILES; ++t) {
+    // 128 x 256 and 64 x 128 are left to the override: at every shape measured they lost to
+    // the next smaller square tile (W_gate / W_down of the 7B block at M = 512 / 1024 / 4096,
+    // NF4 / Q8_0 / INT8: e.g. Q8_0 11008 x 4096 at M = 1024 406 against 278 us on 128 x 128,
+    // NF4 4096 x 11008 at M = 512 254 on 64 x 128 against 196 us on 64 x 64)
+    for (int t : {PF_256x256, PF_128x128, PF_64x64}) {
         const int64_t tiles = ((M + kPfTileM[t] - 1) / kPfTileM[t]) * ((N + kPfTileN[t] - 1) / kPfTileN[t]);
         if (M > kPfTileM[t] / 2 && tiles >= static_cast<int64_t>(cus)) return t;
     }
