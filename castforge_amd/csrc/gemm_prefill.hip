@@ -15,10 +15,10 @@
 //   Q8_0  q * d (19 bits) and NF4 f32(T[q] * absmax) (24 bits): three terms.
 //   A non-finite scale gives a non-finite weight (the remainder terms are 0) and so, as in the
 //   evaluator, non-finite outputs on its row.
-//   INT4 whose groups are whole 128-wide K blocks, and GGUF Q4_0 planes, have a second
-//   kernel, prefill_i4_kernel below: one MFMA per product on the exact integer (q - z), a
-//   fresh f32 partial per group (Q4_0: per 32-wide block), and the group's scale applied to
-//   the partial by one fma into the running total.
+//   INT4 whose groups are whole 128-wide K blocks, and GGUF Q4_0 / Q8_0 planes, have a second
+//   kernel, prefill_i4_kernel below: one MFMA per product on the exact integer (q - z, q - 8
+//   or q), a fresh f32 partial per group (GGUF: per 32-wide block), and the group's scale
+//   applied to the partial by one fma into the running total.
 //   (A one-term INT4 form that instead multiplied the running accumulator by s_prev / s_cur
 //   at every group start was measured and dropped: the rounding of the running sum put
 //   near-zero outputs of cancellation-heavy rows further from the exact value than the
@@ -460,10 +460,10 @@ void prefill_qgemm_kernel(PfArgs a) {
     });
 }
 
-// ---- INT4 with groups of a multiple of 128, and GGUF Q4_0 planes: one MFMA per product ----
+// ---- INT4 with groups of a multiple of 128, and GGUF Q4_0 / Q8_0 planes: one MFMA per product ----
 //
-// (Q4_0: z = 8 and a d per 32-wide block, so a fold every two MFMA steps; the words of the
-// planes map to k as described at WSet below.)
+// (GGUF: a d per 32-wide block, so a fold every two MFMA steps; Q4_0 decodes q - 8, Q8_0 the
+// signed byte q; the words of the planes map to k as described at WSet below.)
 // `prefill_i4_kernel<BM, D>` feeds the MFMA the exact integer (q - z) as bf16 (|q - z| <= 15)
 // and x as the bf16 it is.  Per 128-wide K block the MFMAs sum x (q - z) into a fresh f32
 // partial, and one fma per accumulator applies the block's f16 group scale:
@@ -501,6 +501,14 @@ void prefill_qgemm_kernel(PfArgs a) {
 #ifndef CFH_PF_Q4_XPREFETCH
 #define CFH_PF_Q4_XPREFETCH 0
 #endif
+// prefetch depths of the Q8_0 planes form: x blocks and W blocks in flight (its 16 code words
+// per row block and lane leave registers for two W sets only)
+#ifndef CFH_PF_Q8_DEPTH
+#define CFH_PF_Q8_DEPTH 2
+#endif
+#ifndef CFH_PF_Q8_WDEPTH
+#define CFH_PF_Q8_WDEPTH 1
+#endif
 // 1: a step's x fragments are read during the previous step's MFMAs
 #ifndef CFH_PF_I4_XPREFETCH
 #define CFH_PF_I4_XPREFETCH 1
@@ -513,12 +521,13 @@ void prefill_qgemm_kernel(PfArgs a) {
 constexpr int kI4BN = 256;
 constexpr int kI4KB = 128;
 
-template <int BM, int D, int NW, int FMT>
+template <int BM, int D, int NW, int FMT, int DW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void prefill_i4_kernel(PfArgs a) {
-    static_assert(FMT == FMT_INT4 || FMT == FMT_Q4G, "INT4 or GGUF Q4_0 planes");
-    constexpr bool kQ4 = FMT == FMT_Q4G;
-    static_assert(!kQ4 || CFH_PF_I4_FOLD_FIRST, "Q4_0 folds at the start of each 32-wide block");
+    static_assert(FMT == FMT_INT4 || FMT == FMT_Q4G || FMT == FMT_Q8G, "INT4 or GGUF Q4_0 / Q8_0 planes");
+    constexpr bool kQ8 = FMT == FMT_Q8G;
+    constexpr bool kQ4 = FMT == FMT_Q4G || kQ8;  // a d per 32-wide block (the GGUF forms)
+    static_assert(!kQ4 || CFH_PF_I4_FOLD_FIRST, "GGUF forms fold at the start of each 32-wide block");
     constexpr int J = BM / 32;
     constexpr int I = kI4BN / 32 / NW;  // MFMA row blocks of W per wave
     constexpr int kRowsW = kI4BN / NW;  // W rows per wave
@@ -526,7 +535,7 @@ void prefill_i4_kernel(PfArgs a) {
     constexpr int kStage = BM * kI4KB * 2;
     constexpr int kRowsX = BM / NW;          // x rows each wave loads
     constexpr int kDma = kRowsX / 4;         // 1 KB buffer -> LDS loads per wave and block
-    constexpr int kLoads = kDma + I * (kQ4 ? 3 : 4);  // vector-memory loads per wave and block
+    constexpr int kLoads = kDma + I * (kQ8 ? 9 : kQ4 ? 3 : 4);  // vector-memory loads per wave and block
     static_assert(I >= 1 && kRowsX % 16 == 0 && S * kStage <= 160 * 1024, "tile / LDS budget");
     extern __shared__ __align__(16) uint8_t lds[];
 
@@ -555,14 +564,16 @@ void prefill_i4_kernel(PfArgs a) {
     // row is 64 wave + 32 i + fr of the tile
     const int nw0 = n0 + kRowsW * wave;
     const uint32_t n_valid = static_cast<uint32_t>(min(kI4BN, N - n0));
-    const rsrc_t rw = make_rsrc(static_cast<const uint8_t *>(a.codes) + static_cast<int64_t>(n0) * (K / 2), n_valid * (K / 2));
+    const int row_bytes = kQ8 ? K : K / 2;
+    const rsrc_t rw = make_rsrc(static_cast<const uint8_t *>(a.codes) + static_cast<int64_t>(n0) * row_bytes,
+                                n_valid * static_cast<uint32_t>(row_bytes));
     const rsrc_t rs = make_rsrc(static_cast<const uint16_t *>(a.scales) + static_cast<int64_t>(n0) * GP, n_valid * GP * 2);
     const rsrc_t rz = make_rsrc(a.zeros + static_cast<int64_t>(n0) * ZW, n_valid * ZW * 4);
     uint32_t vw[I], vs[I], vz[I];
 #pragma unroll
     for (int i = 0; i < I; ++i) {
         const uint32_t row = static_cast<uint32_t>(kRowsW * wave + 32 * i + fr);
-        vw[i] = row * static_cast<uint32_t>(K / 2) + 32u * h;
+        vw[i] = row * static_cast<uint32_t>(row_bytes) + 32u * h;
         vs[i] = row * static_cast<uint32_t>(GP) * 2u;
         vz[i] = row * static_cast<uint32_t>(ZW) * 4u;
     }
@@ -578,22 +589,38 @@ void prefill_i4_kernel(PfArgs a) {
     // INT4: word t of the lane's 32 code bytes holds k = 64 h + 8 t .. + 7 of the block.
     // Q4_0 planes: 8-element piece p of 32-wide block bb sits at byte 16 p + 4 bb of the row's
     // 64-byte chunk, so word 4 pp + bb (pp = p - 2 h) holds k = 32 bb + 16 h + 8 pp .. + 7.
+    // Q8_0 planes: 8-byte piece p of 32-wide block B sits at byte 16 p + 8 (B & 1) of the
+    // row's 64-byte chunk B / 2; lane half h loads pieces 2 h and 2 h + 1 of each block
+    // (w[i][B]: words 0-1 piece 2 h, 2-3 piece 2 h + 1), k = 32 B + 16 h + 8 pp .. + 7.
     struct WSet {
-        uint4 w[I][2];  // [row block i][half]: words 0..3, 4..7 of the lane's 32 code bytes
-        uint32_t s[I][2], z[I];  // INT4: s[i][0] = the f16 scale pair; Q4_0: the block's 4 d
+        uint4 w[I][kQ8 ? 4 : 2];  // INT4 / Q4_0 [half]: words 0..3, 4..7 of the lane's 32 code bytes
+        uint32_t s[I][2], z[I];   // INT4: s[i][0] = the f16 scale pair; GGUF: the block's 4 d
     };
-    auto issue = [&](int b, uint8_t *stage, WSet &r) __attribute__((always_inline)) {
+    auto issue_x = [&](int b, uint8_t *stage) __attribute__((always_inline)) {
         uint8_t *dst = stage + kRowsX * wave * (kI4KB * 2);
 #pragma unroll
         for (int t = 0; t < kDma; ++t)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rx, reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(dst + t * 1024)),
                 16, lv[t & 3], (kRowsX * wave + 4 * t) * K * 2 + b * (kI4KB * 2), 0, 0);
+    };
+    auto issue_w = [&](int b, WSet &r) __attribute__((always_inline)) {
         const int g = b / bpg;
 #pragma unroll
         for (int i = 0; i < I; ++i) {
-            r.w[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64, 0, 0));
-            r.w[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64 + 16, 0, 0));
+            if constexpr (kQ8) {
+                // vw = row * K + 32 h; piece 2 h + pp of block B at 64 (B / 2) + 8 (B & 1) + 16 pp
+#pragma unroll
+                for (int B = 0; B < 4; ++B) {
+                    const uint32_t o = vw[i] + b * 128 + 64 * (B >> 1) + 8 * (B & 1);
+                    const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, 0));
+                    const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, o + 16, 0, 0));
+                    r.w[i][B] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                }
+            } else {
+                r.w[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64, 0, 0));
+                r.w[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64 + 16, 0, 0));
+            }
             if constexpr (kQ4) {
                 const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs[i] + b * 8, 0, 0));
                 r.s[i][0] = d.x;
@@ -632,6 +659,20 @@ void prefill_i4_kernel(PfArgs a) {
         const float q1 = __builtin_fmaf(static_cast<float>(p1.x), kOne, co), q5 = __builtin_fmaf(static_cast<float>(p1.y), kOne, co);
         const float q2 = __builtin_fmaf(static_cast<float>(p2.x), kOne, ce), q6 = __builtin_fmaf(static_cast<float>(p2.y), kOne, ce);
         const float q3 = __builtin_fmaf(static_cast<float>(p3.x), kOne, co), q7 = __builtin_fmaf(static_cast<float>(p3.y), kOne, co);
+        return __builtin_bit_cast(bf16x8_t, make_uint4(pack_hi16(q0, q1), pack_hi16(q2, q3), pack_hi16(q4, q5), pack_hi16(q6, q7)));
+    };
+    // Q8_0: 8 signed codes (two words, k order) -> 4 bf16 pairs of exact q: (w & 0x00FF00FF) ^
+    // 0x64806480 is the f16 pair 1024 + (q + 128), and v_fma_mix_f32 subtracts 1152
+    const uint32_t kM8 = opaque(0x00FF00FFu), kC8 = opaque(0x64806480u);
+    auto decode8 = [&](uint32_t w0, uint32_t w1) __attribute__((always_inline)) {
+        typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+        const float c = -1152.0f;
+        const h2_t a0 = __builtin_bit_cast(h2_t, (w0 & kM8) ^ kC8), a1 = __builtin_bit_cast(h2_t, ((w0 >> 8) & kM8) ^ kC8);
+        const h2_t b0 = __builtin_bit_cast(h2_t, (w1 & kM8) ^ kC8), b1 = __builtin_bit_cast(h2_t, ((w1 >> 8) & kM8) ^ kC8);
+        const float q0 = __builtin_fmaf(static_cast<float>(a0.x), kOne, c), q2 = __builtin_fmaf(static_cast<float>(a0.y), kOne, c);
+        const float q1 = __builtin_fmaf(static_cast<float>(a1.x), kOne, c), q3 = __builtin_fmaf(static_cast<float>(a1.y), kOne, c);
+        const float q4 = __builtin_fmaf(static_cast<float>(b0.x), kOne, c), q6 = __builtin_fmaf(static_cast<float>(b0.y), kOne, c);
+        const float q5 = __builtin_fmaf(static_cast<float>(b1.x), kOne, c), q7 = __builtin_fmaf(static_cast<float>(b1.y), kOne, c);
         return __builtin_bit_cast(bf16x8_t, make_uint4(pack_hi16(q0, q1), pack_hi16(q2, q3), pack_hi16(q4, q5), pack_hi16(q6, q7)));
     };
 
@@ -697,9 +738,14 @@ void prefill_i4_kernel(PfArgs a) {
             if constexpr (kQ4 && (kk & 1) == 0 && kk > 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < I; ++i) {
-                const uint4 q = r.w[i][half];
-                const uint32_t word = comp == 0 ? q.x : comp == 1 ? q.y : comp == 2 ? q.z : q.w;
-                wf[i] = decode(word, ce[i], co[i]);
+                if constexpr (kQ8) {
+                    const uint4 q = r.w[i][kk >> 1];  // block kk / 2, piece 2 h + (kk & 1)
+                    wf[i] = (kk & 1) ? decode8(q.z, q.w) : decode8(q.x, q.y);
+                } else {
+                    const uint4 q = r.w[i][half];
+                    const uint32_t word = comp == 0 ? q.x : comp == 1 ? q.y : comp == 2 ? q.z : q.w;
+                    wf[i] = decode(word, ce[i], co[i]);
+                }
             }
             // Q4_0: a new 32-wide block (and scale) every two steps
             constexpr bool kStart = kQ4 ? (kk & 1) == 0 : kk == 0;
@@ -740,33 +786,42 @@ void prefill_i4_kernel(PfArgs a) {
         }
     };
 
-    // Block b: wait for its loads (those of blocks b + 1 .. b + D - 1 may still be in
-    // flight), barrier (every wave's LDS writes of block b landed, every wave is done with
-    // block b - 1's stage), issue block b + D into the stage and register set block b - 1
-    // used, compute block b.  Steps are unrolled S-fold so every register set index is a
-    // constant.
-    constexpr int U = S;
-    WSet ws[S];
+    // Block b: wait for its loads, barrier (every wave's LDS writes of block b landed, every
+    // wave is done with block b - 1's stage), issue W of block b + DW into the register set
+    // block b - 1 used and x of block b + D into the stage block b - 1 used, compute block b.
+    // With DW < D a step issues W before x, so block b's W and x are both in when at most the
+    // loads issued after W(b) are outstanding (x of b + 1 .. b + D - DW, then whole steps).
+    // Steps are unrolled U-fold (a multiple of both ring sizes) so every index is a constant.
+    constexpr int SW = DW + 1;
+    constexpr int U = S % SW == 0 ? S : SW % S == 0 ? SW : S * SW;
+    constexpr int kAhead = kDma * (D - DW) + (DW - 1) * kLoads;  // loads issued after W(b), steady
+    static_assert(DW >= 1 && DW <= D, "W depth within the x depth");
+    WSet ws[SW];
+    // (with DW == D the order within a step does not change the count; x first there keeps
+    // the INT4 form's schedule, which spilled with W first)
+    constexpr bool kWFirst = DW < D;
     static_for<D>([&](auto II) {
         constexpr int i = decltype(II)::value;
-        if (i < KB) issue(i, lds + i * kStage, ws[i]);
+        if (!kWFirst && i < KB) issue_x(i, lds + i * kStage);
+        if (i < DW && i < KB) issue_w(i, ws[i]);
+        if (kWFirst && i < KB) issue_x(i, lds + i * kStage);
     });
-    // Steady steps (every block of the unrolled group issues its block b + D) are branch-free,
-    // so the compiler's own vmcnt waits cover only the loads being consumed; the last steps
-    // wait for whatever is left.
+    // Steady steps (every block of the unrolled group issues its loads) are branch-free, so
+    // the compiler's own vmcnt waits cover only the loads being consumed; the last steps wait
+    // for everything.
     auto step = [&](auto steady, auto SI, int b) __attribute__((always_inline)) {
         constexpr bool kSteady = decltype(steady)::value;
-        constexpr int si = decltype(SI)::value;
-        if (kSteady || b + D - 1 < KB) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm((D - 1) * kLoads) & ~(15 << 8));
-        } else if (D > 2 && b + 1 < KB) {
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kLoads) & ~(15 << 8));
+        constexpr int sx = decltype(SI)::value % S, sw = decltype(SI)::value % SW;
+        if (kSteady) {
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kAhead) & ~(15 << 8));
         } else {
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));
         }
         __builtin_amdgcn_s_barrier();
-        if (kSteady || b + D < KB) issue(b + D, lds + ((si + D) % S) * kStage, ws[(si + D) % S]);
-        compute(b, lds + si * kStage, ws[si]);
+        if (!kWFirst && (kSteady || b + D < KB)) issue_x(b + D, lds + ((sx + D) % S) * kStage);
+        if (kSteady || b + DW < KB) issue_w(b + DW, ws[(sw + DW) % SW]);
+        if (kWFirst && (kSteady || b + D < KB)) issue_x(b + D, lds + ((sx + D) % S) * kStage);
+        compute(b, lds + sx * kStage, ws[sw]);
     };
     int b0 = 0;
     for (; b0 + U - 1 + D < KB; b0 += U)
@@ -802,7 +857,7 @@ void prefill_i4_kernel(PfArgs a) {
     }
 }
 
-template <int BM, int D, int NW, int FMT>
+template <int BM, int D, int NW, int FMT, int DW = D>
 void launch_i4(PfArgs a, hipStream_t st) {
     constexpr int lds = (D + 1) * BM * kI4KB * 2;
     static std::mutex mu;
@@ -812,7 +867,7 @@ void launch_i4(PfArgs a, hipStream_t st) {
     {
         std::lock_guard<std::mutex> g(mu);
         if (!attr_set[dev]) {
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_i4_kernel<BM, D, NW, FMT>),
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&prefill_i4_kernel<BM, D, NW, FMT, DW>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds),
                       "hipFuncSetAttribute(prefill_i4_kernel)");
             attr_set[dev] = true;
@@ -822,7 +877,7 @@ void launch_i4(PfArgs a, hipStream_t st) {
     a.tiles_n = (a.N + kI4BN - 1) / kI4BN;
     const int64_t tiles = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
     require(tiles <= 0x7fffffff, "too many tiles");
-    prefill_i4_kernel<BM, D, NW, FMT><<<dim3(static_cast<unsigned>(tiles)), dim3(64 * NW), lds, st>>>(a);
+    prefill_i4_kernel<BM, D, NW, FMT, DW><<<dim3(static_cast<unsigned>(tiles)), dim3(64 * NW), lds, st>>>(a);
     check_launch("prefill_i4_kernel");
 }
 
@@ -905,7 +960,7 @@ void launch_fmt(const PfArgs &a, hipStream_t st) {
 // CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the generic kernel, =1 sends every one
 // whose groups allow it to the one-MFMA kernel.
 bool i4_eligible(const PfArgs &a, int fmt) {
-    if (fmt == FMT_Q4G ? a.K % kI4KB != 0 : (a.group % kI4KB != 0 || a.K % a.group != 0)) return false;
+    if (fmt == FMT_Q4G || fmt == FMT_Q8G ? a.K % kI4KB != 0 : (a.group % kI4KB != 0 || a.K % a.group != 0)) return false;
     if (static_cast<int64_t>(128) * a.K * 2 >= (int64_t{1} << 31)) return false;
     if (const char *e = std::getenv("CASTFORGE_PREFILL_I4")) {
         if (std::strcmp(e, "0") == 0) return false;
@@ -936,6 +991,7 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
     if (fmt == FMT_INT4 && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_I4_DEPTH, CFH_PF_I4_WAVES, FMT_INT4>(a, st);
     else if (fmt == FMT_Q4G && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q4_DEPTH, CFH_PF_I4_WAVES, FMT_Q4G>(a, st);
+    else if (fmt == FMT_Q8G && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q8_DEPTH, CFH_PF_I4_WAVES, FMT_Q8G, CFH_PF_Q8_WDEPTH>(a, st);
     else if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);
     else if (fmt == FMT_NF4) launch_fmt<FMT_NF4>(a, st);
     else if (fmt == FMT_Q4G) launch_fmt<FMT_Q4G>(a, st);

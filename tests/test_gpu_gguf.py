@@ -217,12 +217,20 @@ def test_q4_0_prefill_and_int4g_form(cuda, monkeypatch, kernel, special, m, n, k
     _close(y, O.matmul_2d(O.bf16_bits_to_f32(xb.reshape(m, k)), w, packed_rhs=True))
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 96, 1024), (300, 256, 4096), (17, 48, 256), (130, 1000, 2048)])
+@pytest.mark.parametrize("kernel", ["auto", "0", "1"])
+@pytest.mark.parametrize("special", [False, True])
+@pytest.mark.parametrize("m,n,k", [(64, 96, 1024), (300, 256, 4096), (17, 48, 256), (130, 1000, 2048), (129, 257, 640)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
-def test_q8_0_prefill_reads_planes(cuda, m, n, k, out):
-    """Q8_0 at M > 16: the prefill MFMA kernel reads the planes directly (one block per
-    32-element slice) and matches the oracle's decode-then-matmul."""
-    raw = _blocks(Q8_0, n * k // 32, 800 + m)
+def test_q8_0_prefill_reads_planes(cuda, monkeypatch, kernel, special, m, n, k, out):
+    """Q8_0 at M > 16: the prefill MFMA kernels read the planes directly and match the
+    oracle's decode-then-matmul.  kernel: CASTFORGE_PREFILL_I4 ("1" forces the one-MFMA kernel,
+    exact q with one f32 partial per 32-wide block scaled by its d, at K % 128 == 0; "0" the
+    three-term kernel); special: subnormal, zero, -0, negative and largest finite d."""
+    if kernel == "auto":
+        monkeypatch.delenv("CASTFORGE_PREFILL_I4", raising=False)
+    else:
+        monkeypatch.setenv("CASTFORGE_PREFILL_I4", kernel)
+    raw = _blocks(Q8_0, n * k // 32, 800 + m, special)
     p = ops.gguf_repack(Q8_0, _dev_u8(raw, cuda), n, k)
     xb, x = _x(801, m, k, cuda)
     y = ops.gemm_gguf(x, p, out)
