@@ -15,10 +15,10 @@
 //   Q8_0  q * d (19 bits) and NF4 f32(T[q] * absmax) (24 bits): three terms.
 //   A non-finite scale gives a non-finite weight (the remainder terms are 0) and so, as in the
 //   evaluator, non-finite outputs on its row.
-//   INT4 whose groups are whole 128-wide K blocks, and GGUF Q4_0 / Q8_0 planes, have a second
-//   kernel, prefill_i4_kernel below: one MFMA per product on the exact integer (q - z, q - 8
-//   or q), a fresh f32 partial per group (GGUF: per 32-wide block), and the group's scale
-//   applied to the partial by one fma into the running total.
+//   INT4 whose groups are whole 128-wide K blocks, INT8 and GGUF Q4_0 / Q8_0 planes have a
+//   second kernel, prefill_i4_kernel below: one MFMA per product on the exact integer (q - z,
+//   q - 8 or q) decoded in registers, a fresh f32 partial per group (GGUF: per 32-wide block;
+//   INT8: one sum), and the group's scale applied to the partial by one fma into the total.
 //   (A one-term INT4 form that instead multiplied the running accumulator by s_prev / s_cur
 //   at every group start was measured and dropped: the rounding of the running sum put
 //   near-zero outputs of cancellation-heavy rows further from the exact value than the
@@ -460,7 +460,7 @@ void prefill_qgemm_kernel(PfArgs a) {
     });
 }
 
-// ---- INT4 with groups of a multiple of 128, and GGUF Q4_0 / Q8_0 planes: one MFMA per product ----
+// ---- INT4 with groups of a multiple of 128, INT8, GGUF Q4_0 / Q8_0 planes: one MFMA per product ----
 //
 // (GGUF: a d per 32-wide block, so a fold every two MFMA steps; Q4_0 decodes q - 8, Q8_0 the
 // signed byte q; the words of the planes map to k as described at WSet below.)
@@ -524,7 +524,9 @@ constexpr int kI4KB = 128;
 template <int BM, int D, int NW, int FMT, int DW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void prefill_i4_kernel(PfArgs a) {
-    static_assert(FMT == FMT_INT4 || FMT == FMT_Q4G || FMT == FMT_Q8G, "INT4 or GGUF Q4_0 / Q8_0 planes");
+    static_assert(FMT == FMT_INT4 || FMT == FMT_Q4G || FMT == FMT_Q8G || FMT == FMT_INT8,
+                  "INT4, INT8 or GGUF Q4_0 / Q8_0 planes");
+    constexpr bool kI8 = FMT == FMT_INT8;  // one scale per row (or tensor): no per-block fold
     constexpr bool kQ8 = FMT == FMT_Q8G;
     constexpr bool kQ4 = FMT == FMT_Q4G || kQ8;  // a d per 32-wide block (the GGUF forms)
     static_assert(!kQ4 || CFH_PF_I4_FOLD_FIRST, "GGUF forms fold at the start of each 32-wide block");
@@ -536,6 +538,7 @@ void prefill_i4_kernel(PfArgs a) {
     constexpr int kRowsX = BM / NW;          // x rows each wave loads
     constexpr int kDma = kRowsX / 4;         // 1 KB buffer -> LDS loads per wave and block
     constexpr int kLoads = kDma + I * (kQ8 ? 9 : kQ4 ? 3 : 4);  // vector-memory loads per wave and block
+    static_assert(!kI8 || I * 4 == kLoads - kDma, "INT8: 4 code loads per row block");
     static_assert(I >= 1 && kRowsX % 16 == 0 && S * kStage <= 160 * 1024, "tile / LDS budget");
     extern __shared__ __align__(16) uint8_t lds[];
 
@@ -557,14 +560,14 @@ void prefill_i4_kernel(PfArgs a) {
     const int fr = lane & 31, h = lane >> 5;
     const int KB = K / kI4KB;
     const int G = K / a.group, ZW = (G + 7) / 8, GP = ZW * 8;
-    const int bpg = a.group / kI4KB;  // K blocks per group
+    const int bpg = max(1, a.group / kI4KB);  // K blocks per group (INT4; unused by the others)
 
     const rsrc_t rx = make_rsrc(a.x + static_cast<int64_t>(m0) * K, static_cast<uint32_t>(min(BM, M - m0)) * K * 2);
     // descriptors over the tile's rows [n0, n0 + n_valid) (rows past N read zero); a lane's
     // row is 64 wave + 32 i + fr of the tile
     const int nw0 = n0 + kRowsW * wave;
     const uint32_t n_valid = static_cast<uint32_t>(min(kI4BN, N - n0));
-    const int row_bytes = kQ8 ? K : K / 2;
+    const int row_bytes = kQ8 || kI8 ? K : K / 2;
     const rsrc_t rw = make_rsrc(static_cast<const uint8_t *>(a.codes) + static_cast<int64_t>(n0) * row_bytes,
                                 n_valid * static_cast<uint32_t>(row_bytes));
     const rsrc_t rs = make_rsrc(static_cast<const uint16_t *>(a.scales) + static_cast<int64_t>(n0) * GP, n_valid * GP * 2);
@@ -573,7 +576,7 @@ void prefill_i4_kernel(PfArgs a) {
 #pragma unroll
     for (int i = 0; i < I; ++i) {
         const uint32_t row = static_cast<uint32_t>(kRowsW * wave + 32 * i + fr);
-        vw[i] = row * static_cast<uint32_t>(row_bytes) + 32u * h;
+        vw[i] = row * static_cast<uint32_t>(row_bytes) + (kI8 ? 64u : 32u) * h;
         vs[i] = row * static_cast<uint32_t>(GP) * 2u;
         vz[i] = row * static_cast<uint32_t>(ZW) * 4u;
     }
@@ -593,7 +596,8 @@ void prefill_i4_kernel(PfArgs a) {
     // row's 64-byte chunk B / 2; lane half h loads pieces 2 h and 2 h + 1 of each block
     // (w[i][B]: words 0-1 piece 2 h, 2-3 piece 2 h + 1), k = 32 B + 16 h + 8 pp .. + 7.
     struct WSet {
-        uint4 w[I][kQ8 ? 4 : 2];  // INT4 / Q4_0 [half]: words 0..3, 4..7 of the lane's 32 code bytes
+        uint4 w[I][kQ8 || kI8 ? 4 : 2];  // INT4 / Q4_0 [half]: words 0..3, 4..7 of the lane's 32 code bytes;
+                                         // INT8: the lane's 64 code bytes (k = 64 h .. 64 h + 63)
         uint32_t s[I][2], z[I];   // INT4: s[i][0] = the f16 scale pair; GGUF: the block's 4 d
     };
     auto issue_x = [&](int b, uint8_t *stage) __attribute__((always_inline)) {
@@ -608,7 +612,11 @@ void prefill_i4_kernel(PfArgs a) {
         const int g = b / bpg;
 #pragma unroll
         for (int i = 0; i < I; ++i) {
-            if constexpr (kQ8) {
+            if constexpr (kI8) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    r.w[i][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 128 + 16 * c, 0, 0));
+            } else if constexpr (kQ8) {
                 // vw = row * K + 32 h; piece 2 h + pp of block B at 64 (B / 2) + 8 (B & 1) + 16 pp
 #pragma unroll
                 for (int B = 0; B < 4; ++B) {
@@ -621,7 +629,8 @@ void prefill_i4_kernel(PfArgs a) {
                 r.w[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64, 0, 0));
                 r.w[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64 + 16, 0, 0));
             }
-            if constexpr (kQ4) {
+            if constexpr (kI8) {
+            } else if constexpr (kQ4) {
                 const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs[i] + b * 8, 0, 0));
                 r.s[i][0] = d.x;
                 r.s[i][1] = d.y;
@@ -688,6 +697,15 @@ void prefill_i4_kernel(PfArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) part[i][j][e] = 0.f;
     float sc_prev[I] = {};
+    if constexpr (kI8) {
+        // per-channel: scales[n] (0 past N); per tensor: scales[0]
+        const float *sp = static_cast<const float *>(a.scales);
+#pragma unroll
+        for (int i = 0; i < I; ++i) {
+            const int n = nw0 + 32 * i + fr;
+            sc_prev[i] = n < N ? sp[a.per_row ? n : 0] : 0.f;
+        }
+    }
     auto fold = [&](int i, int j) __attribute__((always_inline)) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) tot[i][j][e] = __builtin_fmaf(sc_prev[i], part[i][j][e], tot[i][j][e]);
@@ -698,10 +716,10 @@ void prefill_i4_kernel(PfArgs a) {
         float ce[I], co[I], sc[I];
 #pragma unroll
         for (int i = 0; i < I; ++i) {
-            const float z = kQ4 ? 8.0f : static_cast<float>((r.z[i] >> (4 * (g & 7))) & 15u);
+            const float z = kQ4 || kI8 ? 8.0f : static_cast<float>((r.z[i] >> (4 * (g & 7))) & 15u);
             ce[i] = -(1024.0f + z);
             co[i] = -(64.0f + z);
-            sc[i] = f16_to_f32(static_cast<uint16_t>((g & 1) ? (r.s[i][0] >> 16) : (r.s[i][0] & 0xFFFFu)));
+            sc[i] = kI8 ? 0.f : f16_to_f32(static_cast<uint16_t>((g & 1) ? (r.s[i][0] >> 16) : (r.s[i][0] & 0xFFFFu)));
         }
         // x fragments of step kk + 1 are read while step kk's MFMAs run (two sets); step kk
         // reads the 16-byte chunk holding the k range its W word covers
@@ -738,8 +756,9 @@ void prefill_i4_kernel(PfArgs a) {
             if constexpr (kQ4 && (kk & 1) == 0 && kk > 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < I; ++i) {
-                if constexpr (kQ8) {
-                    const uint4 q = r.w[i][kk >> 1];  // block kk / 2, piece 2 h + (kk & 1)
+                if constexpr (kQ8 || kI8) {
+                    // Q8_0: block kk / 2, piece 2 h + (kk & 1); INT8: words 2 kk, 2 kk + 1
+                    const uint4 q = r.w[i][kk >> 1];
                     wf[i] = (kk & 1) ? decode8(q.z, q.w) : decode8(q.x, q.y);
                 } else {
                     const uint4 q = r.w[i][half];
@@ -748,7 +767,7 @@ void prefill_i4_kernel(PfArgs a) {
                 }
             }
             // Q4_0: a new 32-wide block (and scale) every two steps
-            constexpr bool kStart = kQ4 ? (kk & 1) == 0 : kk == 0;
+            constexpr bool kStart = kI8 ? false : kQ4 ? (kk & 1) == 0 : kk == 0;
 #pragma unroll
             for (int i = 0; i < I; ++i)
 #pragma unroll
@@ -774,7 +793,7 @@ void prefill_i4_kernel(PfArgs a) {
                 }
             }
         });
-        if constexpr (!kQ4) {
+        if constexpr (!kQ4 && !kI8) {
 #pragma unroll
             for (int i = 0; i < I; ++i) sc_prev[i] = sc[i];
         }
@@ -960,7 +979,9 @@ void launch_fmt(const PfArgs &a, hipStream_t st) {
 // CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the generic kernel, =1 sends every one
 // whose groups allow it to the one-MFMA kernel.
 bool i4_eligible(const PfArgs &a, int fmt) {
-    if (fmt == FMT_Q4G || fmt == FMT_Q8G ? a.K % kI4KB != 0 : (a.group % kI4KB != 0 || a.K % a.group != 0)) return false;
+    if (fmt == FMT_Q4G || fmt == FMT_Q8G || fmt == FMT_INT8 ? a.K % kI4KB != 0
+                                                             : (a.group % kI4KB != 0 || a.K % a.group != 0))
+        return false;
     if (static_cast<int64_t>(128) * a.K * 2 >= (int64_t{1} << 31)) return false;
     if (const char *e = std::getenv("CASTFORGE_PREFILL_I4")) {
         if (std::strcmp(e, "0") == 0) return false;
@@ -990,6 +1011,7 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
     PfArgs a{x, codes, scales, zeros, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
     if (fmt == FMT_INT4 && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_I4_DEPTH, CFH_PF_I4_WAVES, FMT_INT4>(a, st);
+    else if (fmt == FMT_INT8 && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q8_DEPTH, CFH_PF_I4_WAVES, FMT_INT8, CFH_PF_Q8_WDEPTH>(a, st);
     else if (fmt == FMT_Q4G && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q4_DEPTH, CFH_PF_I4_WAVES, FMT_Q4G>(a, st);
     else if (fmt == FMT_Q8G && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q8_DEPTH, CFH_PF_I4_WAVES, FMT_Q8G, CFH_PF_Q8_WDEPTH>(a, st);
     else if (fmt == FMT_INT4) launch_fmt<FMT_INT4>(a, st);

@@ -17,9 +17,10 @@ and per kernel (M = 1 split-K, M = 3 and 16 skinny, M = 40 and 300 prefill):
     weight term: (3 K / 16 + 8) 2^-24 sum |x w|) of 0, and the residuals' RMS no larger than
     the evaluator's;
   * a non-finite x gives non-finite rows.
-INT4 g128 and GGUF Q4_0 / Q8_0 run a second time with the one-MFMA prefill kernel forced
-(int4_g128_one, q4_0_one, q8_0_one): exact (q - z) / q operands, one f32 partial per 128-wide K
-block (GGUF: per 32-wide block) scaled into the total.
+INT4 g128, INT8 and GGUF Q4_0 / Q8_0 run a second time with the one-MFMA prefill kernel forced
+(int4_g128_one, int8_one, q4_0_one, q8_0_one): exact (q - z) / q operands, one f32 partial per
+128-wide K block (GGUF: per 32-wide block; INT8: one sum, its row scale applied once) scaled
+into the total.
 """
 import os
 
@@ -78,11 +79,14 @@ class Case:
                 self.run = lambda x, out: ops.gemm_w4a16(x, self.p, out)
             self.oracle = lambda xb: O.gemm_w4a16(xb, c, s, z, n, k, g)
             self.deq = O.dequantize_int4g(c, s, z, n, k, g)
-        elif fmt == "int8":
+        elif fmt.startswith("int8"):
             w = _weight(seed, n, k, halves)
             c, s = O.quantize_int8_rows(w)
             cd, sd = torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev)
-            self.run = lambda x, out: ops.gemm_w8a16(x, cd, sd, "channel", out)
+            if fmt.endswith("_one"):  # the one-MFMA prefill kernel, forced at every M > 64
+                self.run = lambda x, out: _one_mfma(lambda: ops.gemm_w8a16(x, cd, sd, "channel", out))
+            else:
+                self.run = lambda x, out: ops.gemm_w8a16(x, cd, sd, "channel", out)
             self.oracle = lambda xb: O.gemm_w8a16(xb, c, s)
             self.deq = c.astype(np.float32) * s[:, None]
         elif fmt == "nf4":
@@ -120,7 +124,8 @@ def _one_mfma(call):
             os.environ["CASTFORGE_PREFILL_I4"] = old
 
 
-FORMATS = ["int4_g128", "int4_g128_one", "int4_g64", "int4_g32", "int8", "nf4", "q4_0", "q4_0_one", "q8_0", "q8_0_one"]
+FORMATS = ["int4_g128", "int4_g128_one", "int4_g64", "int4_g32", "int8", "int8_one", "nf4", "q4_0", "q4_0_one", "q8_0",
+           "q8_0_one"]
 MS = [1, 3, 16, 40, 300]
 
 

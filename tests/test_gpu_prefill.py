@@ -119,11 +119,14 @@ def test_prefill_every_tile_shape(cuda, monkeypatch, tile, fmt):
     _close(y, ref, f"{fmt} {tile}")
 
 
-@pytest.mark.parametrize("m", [17, 200])
+@pytest.mark.parametrize("kernel", I4_KERNELS)
+@pytest.mark.parametrize("m,n,k", [(17, 300, 1024), (200, 300, 1024), (300, 520, 2048), (129, 257, 640)])
 @pytest.mark.parametrize("gran", ["channel", "tensor"])
-def test_w8a16_prefill(cuda, m, gran):
-    n, k = 300, 1024
-    print(f"[prefill w8a16] m={m} gran={gran}", flush=True)
+def test_w8a16_prefill(cuda, monkeypatch, kernel, m, n, k, gran):
+    """INT8 at M > 16; kernel "1" forces the one-MFMA kernel (K % 128 == 0: exact q, the row or
+    tensor scale applied once to the f32 sum), "0" the generic kernel."""
+    _i4_kernel(monkeypatch, kernel)
+    print(f"[prefill w8a16] kernel={kernel} m={m} n={n} k={k} gran={gran}", flush=True)
     w = synth.weight(87, 1, n, k)
     xb, x = _x(88, m, k, cuda)
     q, s = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, gran, "half_even")
