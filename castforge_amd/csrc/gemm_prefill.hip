@@ -973,7 +973,8 @@ void launch_fmt(const PfArgs &a, hipStream_t st) {
 }
 
 // INT4 whose groups are whole 128-wide K blocks takes the one-MFMA kernel once it has at least
-// one 256 x 128 tile per 6 CUs (43 on 256 CUs).  Measured against the generic kernel's smaller
+// one 256 x 128 tile per 6 CUs (43 on 256 CUs; other formats below).  Measured against the
+// generic kernel's smaller
 // tiles: 11008 x 4096 (43 n-tiles) at M = 96 / 512 / 1024: 57 / 61 / 125 us against 65 / 128 /
 // 290; 4096 x 11008 (16 n-tiles) at M = 256 / 512: 143 / 143 us against 121 / 199.
 // CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the generic kernel, =1 sends every one
@@ -993,6 +994,13 @@ bool i4_eligible(const PfArgs &a, int fmt) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
     }
     const int64_t tiles = ((a.M + 127) / 128) * static_cast<int64_t>((a.N + kI4BN - 1) / kI4BN);
+    // INT4: one tile per 6 CUs.  The GGUF forms fold every two MFMA steps and INT8's generic
+    // kernel is already one term, so they switch later (measured on 256 CUs, us generic / one-
+    // MFMA): Q4_0 / Q8_0 11008 x 4096 at M = 128 (43 tiles) 65 / 76 and 75 / 92, at M = 256
+    // (86) 102 / 77 and 116 / 92; INT8 4096 x 11008 and 4096 x 4096 at M = 1024 (128 tiles)
+    // 124 / 136 and 51 / 55, 11008 x 4096 at M = 512 (172) 73 / 56.
+    if (fmt == FMT_INT8) return 8 * tiles >= 5 * static_cast<int64_t>(cus);
+    if (fmt == FMT_Q4G || fmt == FMT_Q8G) return 3 * tiles >= cus;
     return 6 * tiles >= cus;
 }
 
