@@ -10,7 +10,7 @@ Also reported (`components`): quantize GB/s (INT4 g128 and INT8 per-channel over
 block), W4A16 GEMV at M=4/8 over the GEMV planes and at M=8/16 over the canonical layout,
 W8A16 GEMV at M=1 (config 1), NF4 GEMV at M=1 and NF4 GEMM at M=64/512 (config 3), W4A16 prefill GEMM at M=4096 (config 5), FP8 W8A8 GEMM (config 4), and
 the 32-layer AWQ-style INT4 model (config 5): quantize, decode GEMV and prefill GEMM over all
-layers.
+layers; also W8A16 and GGUF Q4_0 / Q8_0 prefill at M=4096 on the W_gate / W_down shapes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -336,6 +336,18 @@ def main():
         st = time_steps(w8_step, 50, 5)
         w8_bytes = nel + nrows * 4 + sum(2 * k + 2 * n for (_, n, k) in synth.LLAMA7B_BLOCK)
         components["w8a16_gemv_m1_GBps"] = round(w8_bytes / (st * 1e-3) / 1e9, 1)
+        # INT8 prefill at M = 4096 on W_gate / W_down (one-MFMA kernel at these shapes)
+        for idx in (4, 6):
+            _, n, k = synth.LLAMA7B_BLOCK[idx]
+            m = 4096
+            xp = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+            qi, si = q8[idx]
+            st = time_steps(lambda i: ops.gemm_w8a16(xp, qi, si, "channel", torch.bfloat16), 10, 2, min_ms=30.0,
+                            replays=3)
+            components[f"w8a16_prefill_m{m}_n{n}_k{k}_TFLOPs"] = round(2.0 * m * n * k / (st * 1e-3) / 1e12, 1)
+            log(f"[bench] W8A16 prefill M={m} n={n} k={k}: {st * 1e3:.1f} us, "
+                f"{components[f'w8a16_prefill_m{m}_n{n}_k{k}_TFLOPs']} TFLOP/s")
+            del xp
         del q8, q8c
 
         # NF4 b64 GEMV M=1 over W_gate/W_up/W_down (config 3)
@@ -386,6 +398,17 @@ def main():
                 log(f"[bench] GGUF q4_0 GEMV M=1 over Q4_0 GEMV planes: {st * 1e3:.1f} us, "
                     f"{components['gguf_q4_0_planes_gemv_m1_GBps']} GB/s")
                 del gpl
+            # prefill at M = 4096 on W_gate / W_down over the same planes
+            for idx in (4, 6):
+                _, n, k = synth.LLAMA7B_BLOCK[idx]
+                m = 4096
+                xp = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+                pg = gc[0][idx]
+                st = time_steps(lambda i: ops.gemm_gguf(xp, pg, torch.bfloat16), 10, 2, min_ms=30.0, replays=3)
+                components[f"gguf_{tag}_prefill_m{m}_n{n}_k{k}_TFLOPs"] = round(2.0 * m * n * k / (st * 1e-3) / 1e12, 1)
+                log(f"[bench] GGUF {tag} prefill M={m} n={n} k={k}: {st * 1e3:.1f} us, "
+                    f"{components[f'gguf_{tag}_prefill_m{m}_n{n}_k{k}_TFLOPs']} TFLOP/s")
+                del xp
             del gc, ysg
 
         # prefill GEMMs on MFMA: W4A16 INT4 g128 at M=4096 (config 5 follow-on) and NF4 b64 at
