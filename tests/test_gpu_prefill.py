@@ -157,6 +157,40 @@ def test_prefill_unaligned_output(cuda, monkeypatch, kernel):
 
 
 @pytest.mark.parametrize("kernel", ["0", "1"])
+@pytest.mark.parametrize("fmt", ["int4", "int8", "q4_0", "q8_0"])
+@pytest.mark.parametrize("m,n,k", [(130, 300, 128), (129, 64, 28672)])
+def test_prefill_k_extremes(cuda, monkeypatch, kernel, fmt, m, n, k):
+    """K of one 128-wide block (every step of the one-MFMA kernel is a tail step) and K =
+    28672 (224 blocks: many unrolled steady groups, then the tail), INT4 g128 / INT8 / GGUF
+    Q4_0 / Q8_0 on both prefill kernels, against the oracle at the north-star bound."""
+    _i4_kernel(monkeypatch, kernel)
+    print(f"[prefill k extremes] kernel={kernel} {fmt} m={m} n={n} k={k}", flush=True)
+    xb, x = _x(97, m, k, cuda)
+    xf = O.bf16_bits_to_f32(xb.reshape(m, k))
+    if fmt == "int4":
+        w = synth.weight(98, 1, n, k)
+        p, (c, s, z) = _int4(w, 128, cuda)
+        y = ops.gemm_w4a16(x, p, torch.float32)
+        ref = O.gemm_w4a16(xb, c, s, z, n, k, 128)
+    elif fmt == "int8":
+        w = synth.weight(98, 1, n, k)
+        q, sc = ops.quantize_int8(torch.from_numpy(w).to(cuda), 8, "channel", "half_even")
+        y = ops.gemm_w8a16(x, q, sc, "channel", torch.float32)
+        ref = O.gemm_w8a16(xb, q.cpu().numpy(), sc.cpu().numpy())
+    else:
+        ty, bb = (2, 18) if fmt == "q4_0" else (8, 34)
+        rng = np.random.default_rng(99)
+        raw = rng.integers(0, 256, (n * k // 32, bb), dtype=np.uint8)
+        raw[:, 0:2] = (rng.standard_normal(n * k // 32) * 0.003).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        raw = raw.reshape(-1)
+        p = ops.gguf_repack(ty, torch.from_numpy(raw).to(cuda), n, k)
+        y = ops.gemm_gguf(x, p, torch.float32)
+        ref = O.matmul_2d(xf, O.gguf_decode(ty, raw, n * k).reshape(n, k), packed_rhs=True)
+    torch.cuda.synchronize()
+    _close(y, ref, f"{fmt} k={k}")
+
+
+@pytest.mark.parametrize("kernel", ["0", "1"])
 def test_w4a16_prefill_special_scales(cuda, monkeypatch, kernel):
     """Group scales that are f16 subnormals, zero and the largest finite f16 give the
     oracle's outputs (each is exact in f32 and multiplies an exact partial); a row with one
