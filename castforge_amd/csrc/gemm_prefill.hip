@@ -52,7 +52,9 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 // FMT_Q4G / FMT_Q8G: GGUF Q4_0 / Q8_0 planes (codes, one f16 d per 32; the same numbers as the
 // GEMV's FMT_Q4_0 / FMT_Q8_0)
-enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2, FMT_Q4G = 3, FMT_Q8G = 4 };
+enum Fmt { FMT_INT4 = 0, FMT_INT8 = 1, FMT_NF4 = 2, FMT_Q4G = 3, FMT_Q8G = 4,
+           // INT4 with groups of 32 / 64: instances of the one-MFMA kernel only
+           FMT_I4G32 = 5, FMT_I4G64 = 6 };
 
 // bf16 weight planes per format
 template <int FMT> constexpr int planes() {
@@ -460,7 +462,7 @@ void prefill_qgemm_kernel(PfArgs a) {
     });
 }
 
-// ---- INT4 with groups of a multiple of 128, INT8, GGUF Q4_0 / Q8_0 planes: one MFMA per product ----
+// ---- INT4 (groups of 32, 64 or a multiple of 128), INT8, GGUF Q4_0 / Q8_0 planes: one MFMA per product ----
 //
 // (GGUF: a d per 32-wide block, so a fold every two MFMA steps; Q4_0 decodes q - 8, Q8_0 the
 // signed byte q; the words of the planes map to k as described at WSet below.)
@@ -524,12 +526,17 @@ constexpr int kI4KB = 128;
 template <int BM, int D, int NW, int FMT, int DW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void prefill_i4_kernel(PfArgs a) {
-    static_assert(FMT == FMT_INT4 || FMT == FMT_Q4G || FMT == FMT_Q8G || FMT == FMT_INT8,
+    static_assert(FMT == FMT_INT4 || FMT == FMT_Q4G || FMT == FMT_Q8G || FMT == FMT_INT8 || FMT == FMT_I4G32 ||
+                      FMT == FMT_I4G64,
                   "INT4, INT8 or GGUF Q4_0 / Q8_0 planes");
     constexpr bool kI8 = FMT == FMT_INT8;  // one scale per row (or tensor): no per-block fold
     constexpr bool kQ8 = FMT == FMT_Q8G;
     constexpr bool kQ4 = FMT == FMT_Q4G || kQ8;  // a d per 32-wide block (the GGUF forms)
-    static_assert(!kQ4 || CFH_PF_I4_FOLD_FIRST, "GGUF forms fold at the start of each 32-wide block");
+    // INT4 with groups of 32 / 64: canonical codes read in the GGUF forms' step -> k map (a
+    // step never straddles a group), a zero point and a scale per group
+    constexpr int kSG = FMT == FMT_I4G32 ? 32 : FMT == FMT_I4G64 ? 64 : 0;
+    constexpr bool kQmap = kQ4 || kSG;
+    static_assert(!kQmap || CFH_PF_I4_FOLD_FIRST, "small groups fold at the start of each group");
     constexpr int J = BM / 32;
     constexpr int I = kI4BN / 32 / NW;  // MFMA row blocks of W per wave
     constexpr int kRowsW = kI4BN / NW;  // W rows per wave
@@ -537,7 +544,7 @@ void prefill_i4_kernel(PfArgs a) {
     constexpr int kStage = BM * kI4KB * 2;
     constexpr int kRowsX = BM / NW;          // x rows each wave loads
     constexpr int kDma = kRowsX / 4;         // 1 KB buffer -> LDS loads per wave and block
-    constexpr int kLoads = kDma + I * (kQ8 ? 9 : kQ4 ? 3 : 4);  // vector-memory loads per wave and block
+    constexpr int kLoads = kDma + I * (kQ8 ? 9 : kQ4 ? 3 : kSG ? 6 : 4);  // vector-memory loads per wave and block
     static_assert(!kI8 || I * 4 == kLoads - kDma, "INT8: 4 code loads per row block");
     static_assert(I >= 1 && kRowsX % 16 == 0 && S * kStage <= 160 * 1024, "tile / LDS budget");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -576,7 +583,7 @@ void prefill_i4_kernel(PfArgs a) {
 #pragma unroll
     for (int i = 0; i < I; ++i) {
         const uint32_t row = static_cast<uint32_t>(kRowsW * wave + 32 * i + fr);
-        vw[i] = row * static_cast<uint32_t>(row_bytes) + (kI8 ? 64u : 32u) * h;
+        vw[i] = row * static_cast<uint32_t>(row_bytes) + (kI8 ? 64u : kSG ? 8u : 32u) * h;
         vs[i] = row * static_cast<uint32_t>(GP) * 2u;
         vz[i] = row * static_cast<uint32_t>(ZW) * 4u;
     }
@@ -625,11 +632,30 @@ void prefill_i4_kernel(PfArgs a) {
                     const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, o + 16, 0, 0));
                     r.w[i][B] = make_uint4(lo.x, lo.y, hi.x, hi.y);
                 }
+            } else if constexpr (kSG) {
+                // words 4 B + 2 h, 4 B + 2 h + 1 of the row's 16 (vw = row * K / 2 + 8 h): k = 32 B +
+                // 16 h .. + 15, kept in step order
+#pragma unroll
+                for (int B2 = 0; B2 < 2; ++B2) {
+                    const uint2 e = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, vw[i] + b * 64 + 32 * B2, 0, 0));
+                    const uint2 o = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, vw[i] + b * 64 + 32 * B2 + 16, 0, 0));
+                    r.w[i][B2] = make_uint4(e.x, e.y, o.x, o.y);
+                }
             } else {
                 r.w[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64, 0, 0));
                 r.w[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vw[i] + b * 64 + 16, 0, 0));
             }
             if constexpr (kI8) {
+            } else if constexpr (kSG) {
+                // the block's 4 (g32) or 2 (g64) scales and the zero-point word holding theirs
+                if constexpr (kSG == 32) {
+                    const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs[i] + b * 8, 0, 0));
+                    r.s[i][0] = d.x;
+                    r.s[i][1] = d.y;
+                } else {
+                    r.s[i][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, vs[i] + b * 4, 0, 0);
+                }
+                r.z[i] = __builtin_amdgcn_raw_buffer_load_b32(rz, vz[i] + (kSG == 32 ? (b >> 1) : (b >> 2)) * 4, 0, 0);
             } else if constexpr (kQ4) {
                 const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs[i] + b * 8, 0, 0));
                 r.s[i][0] = d.x;
@@ -729,11 +755,11 @@ void prefill_i4_kernel(PfArgs a) {
         // step constant, and the lane offset is hidden from the compiler, which would otherwise
         // keep one precomputed address per step and stage live and spill them (10 % faster);
         // INT4 keeps the precomputed addresses (1.5 % faster there).
-        const uint32_t xlane = static_cast<uint32_t>(fr * (kI4KB * 2) + (((fr & 15) ^ (kQ4 ? 2 * h : 8 * h)) * 16));
+        const uint32_t xlane = static_cast<uint32_t>(fr * (kI4KB * 2) + (((fr & 15) ^ (kQmap ? 2 * h : 8 * h)) * 16));
         auto read_x = [&](int kk, bf16x8_t (&dst)[J]) __attribute__((always_inline)) {
-            const uint32_t cst = kQ4 ? 4 * (kk >> 1) + (kk & 1) : kk;
+            const uint32_t cst = kQmap ? 4 * (kk >> 1) + (kk & 1) : kk;
             uint32_t xo = xlane;
-            if constexpr (kQ4) asm volatile("" : "+v"(xo));
+            if constexpr (kQmap) asm volatile("" : "+v"(xo));
             const uint8_t *row = stage + (xo ^ (cst << 4));
 #pragma unroll
             for (int j = 0; j < J; ++j)
@@ -741,7 +767,7 @@ void prefill_i4_kernel(PfArgs a) {
         };
         // (Q4_0 reads each step's fragments in the step by default: with its extra folds a
         // second set spills)
-        constexpr bool kXPre = CFH_PF_I4_XPREFETCH && (!kQ4 || CFH_PF_Q4_XPREFETCH);
+        constexpr bool kXPre = CFH_PF_I4_XPREFETCH && (!kQmap || CFH_PF_Q4_XPREFETCH);
         if (kXPre) read_x(0, xf[0]);
         static_for<8>([&](auto KK) {
             constexpr int kk = decltype(KK)::value;
@@ -753,7 +779,17 @@ void prefill_i4_kernel(PfArgs a) {
             constexpr int half = kQ4 ? (kk & 1) : (kk >> 2), comp = kQ4 ? (kk >> 1) : (kk & 3);
             // Q4_0: nothing moves across a 32-wide block start (the compiler would otherwise
             // hoist later blocks' decodes above the folds and run out of registers)
-            if constexpr (kQ4 && (kk & 1) == 0 && kk > 0) __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kQmap && (kk & 1) == 0 && kk > 0) __builtin_amdgcn_sched_barrier(0);
+            // small groups: the zero point of the group this step starts
+            if constexpr (kSG && (kk % (kSG / 16)) == 0) {
+                const int nib = kSG == 32 ? 4 * (b & 1) + (kk >> 1) : 2 * (b & 3) + (kk >> 2);
+#pragma unroll
+                for (int i = 0; i < I; ++i) {
+                    const float z = static_cast<float>((r.z[i] >> (4 * nib)) & 15u);
+                    ce[i] = -(1024.0f + z);
+                    co[i] = -(64.0f + z);
+                }
+            }
 #pragma unroll
             for (int i = 0; i < I; ++i) {
                 if constexpr (kQ8 || kI8) {
@@ -767,7 +803,7 @@ void prefill_i4_kernel(PfArgs a) {
                 }
             }
             // Q4_0: a new 32-wide block (and scale) every two steps
-            constexpr bool kStart = kI8 ? false : kQ4 ? (kk & 1) == 0 : kk == 0;
+            constexpr bool kStart = kI8 ? false : kQ4 ? (kk & 1) == 0 : kSG ? (kk % (kSG / 16)) == 0 : kk == 0;
 #pragma unroll
             for (int i = 0; i < I; ++i)
 #pragma unroll
@@ -779,11 +815,20 @@ void prefill_i4_kernel(PfArgs a) {
                         if (CFH_PF_I4_FOLD_FIRST) fold(i, j);
                         floatx16 z{};
                         part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[xs][j], wf[i], z, 0, 0, 0);
-                        if (CFH_PF_I4_FOLD_FIRST && !kQ4) __builtin_amdgcn_sched_barrier(0);
+                        if (CFH_PF_I4_FOLD_FIRST && !kQmap) __builtin_amdgcn_sched_barrier(0);
                     } else {
                         part[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf[xs][j], wf[i], part[i][j], 0, 0, 0);
                     }
                 }
+            if constexpr (kSG && kStart) {
+                // this group's scale multiplies the partial that the next group start folds
+#pragma unroll
+                for (int i = 0; i < I; ++i) {
+                    const uint32_t dw = kSG == 32 ? r.s[i][kk >> 2] : r.s[i][0];
+                    const bool hi = kSG == 32 ? (kk & 2) != 0 : (kk & 4) != 0;
+                    sc_prev[i] = f16_to_f32(static_cast<uint16_t>(hi ? (dw >> 16) : (dw & 0xFFFFu)));
+                }
+            }
             if constexpr (kQ4 && kStart) {
                 // block kk / 2's d scales the partial that the next block start folds
 #pragma unroll
@@ -793,7 +838,7 @@ void prefill_i4_kernel(PfArgs a) {
                 }
             }
         });
-        if constexpr (!kQ4 && !kI8) {
+        if constexpr (!kQmap && !kI8) {
 #pragma unroll
             for (int i = 0; i < I; ++i) sc_prev[i] = sc[i];
         }
@@ -980,9 +1025,12 @@ void launch_fmt(const PfArgs &a, hipStream_t st) {
 // CASTFORGE_PREFILL_I4=0 keeps every INT4 problem on the generic kernel, =1 sends every one
 // whose groups allow it to the one-MFMA kernel.
 bool i4_eligible(const PfArgs &a, int fmt) {
-    if (fmt == FMT_Q4G || fmt == FMT_Q8G || fmt == FMT_INT8 ? a.K % kI4KB != 0
-                                                             : (a.group % kI4KB != 0 || a.K % a.group != 0))
+    if (fmt == FMT_I4G32 || fmt == FMT_I4G64) {
+        if (a.K % kI4KB != 0) return false;
+    } else if (fmt == FMT_Q4G || fmt == FMT_Q8G || fmt == FMT_INT8 ? a.K % kI4KB != 0
+                                                                    : (a.group % kI4KB != 0 || a.K % a.group != 0)) {
         return false;
+    }
     if (static_cast<int64_t>(128) * a.K * 2 >= (int64_t{1} << 31)) return false;
     if (const char *e = std::getenv("CASTFORGE_PREFILL_I4")) {
         if (std::strcmp(e, "0") == 0) return false;
@@ -1000,7 +1048,7 @@ bool i4_eligible(const PfArgs &a, int fmt) {
     // (86) 102 / 77 and 116 / 92; INT8 4096 x 11008 and 4096 x 4096 at M = 1024 (128 tiles)
     // 124 / 136 and 51 / 55, 11008 x 4096 at M = 512 (172) 73 / 56.
     if (fmt == FMT_INT8) return 8 * tiles >= 5 * static_cast<int64_t>(cus);
-    if (fmt == FMT_Q4G || fmt == FMT_Q8G) return 3 * tiles >= cus;
+    if (fmt == FMT_Q4G || fmt == FMT_Q8G || fmt == FMT_I4G32 || fmt == FMT_I4G64) return 3 * tiles >= cus;
     return 6 * tiles >= cus;
 }
 
@@ -1019,6 +1067,10 @@ bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, in
     PfArgs a{x, codes, scales, zeros, y, static_cast<int>(m), static_cast<int>(n), static_cast<int>(k),
              static_cast<int>(fmt == FMT_INT8 ? BK : group), per_row, y_bf16, (n % 4 == 0 && aligned(y, 16)) ? 1 : 0, 0, 0};
     if (fmt == FMT_INT4 && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_I4_DEPTH, CFH_PF_I4_WAVES, FMT_INT4>(a, st);
+    else if (fmt == FMT_INT4 && a.group == 32 && i4_eligible(a, FMT_I4G32))
+        launch_i4<128, CFH_PF_Q4_DEPTH, CFH_PF_I4_WAVES, FMT_I4G32, 1>(a, st);  // two W sets: three spill
+    else if (fmt == FMT_INT4 && a.group == 64 && i4_eligible(a, FMT_I4G64))
+        launch_i4<128, CFH_PF_Q4_DEPTH, CFH_PF_I4_WAVES, FMT_I4G64>(a, st);
     else if (fmt == FMT_INT8 && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q8_DEPTH, CFH_PF_I4_WAVES, FMT_INT8, CFH_PF_Q8_WDEPTH>(a, st);
     else if (fmt == FMT_Q4G && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q4_DEPTH, CFH_PF_I4_WAVES, FMT_Q4G>(a, st);
     else if (fmt == FMT_Q8G && i4_eligible(a, fmt)) launch_i4<128, CFH_PF_Q8_DEPTH, CFH_PF_I4_WAVES, FMT_Q8G, CFH_PF_Q8_WDEPTH>(a, st);

@@ -17,10 +17,9 @@ and per kernel (M = 1 split-K, M = 3 and 16 skinny, M = 40 and 300 prefill):
     weight term: (3 K / 16 + 8) 2^-24 sum |x w|) of 0, and the residuals' RMS no larger than
     the evaluator's;
   * a non-finite x gives non-finite rows.
-INT4 g128, INT8 and GGUF Q4_0 / Q8_0 run a second time with the one-MFMA prefill kernel forced
-(int4_g128_one, int8_one, q4_0_one, q8_0_one): exact (q - z) / q operands, one f32 partial per
-128-wide K block (GGUF: per 32-wide block; INT8: one sum, its row scale applied once) scaled
-into the total.
+INT4 g128 / g64 / g32, INT8 and GGUF Q4_0 / Q8_0 run a second time with the one-MFMA prefill
+kernel forced (the *_one formats): exact (q - z) / q operands, one f32 partial per group
+(GGUF: per 32-wide block; INT8: one sum, its row scale applied once) scaled into the total.
 """
 import os
 
@@ -124,8 +123,8 @@ def _one_mfma(call):
             os.environ["CASTFORGE_PREFILL_I4"] = old
 
 
-FORMATS = ["int4_g128", "int4_g128_one", "int4_g64", "int4_g32", "int8", "int8_one", "nf4", "q4_0", "q4_0_one", "q8_0",
-           "q8_0_one"]
+FORMATS = ["int4_g128", "int4_g128_one", "int4_g64", "int4_g64_one", "int4_g32", "int4_g32_one", "int8", "int8_one",
+           "nf4", "q4_0", "q4_0_one", "q8_0", "q8_0_one"]
 MS = [1, 3, 16, 40, 300]
 
 
