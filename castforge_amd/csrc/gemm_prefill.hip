@@ -464,10 +464,8 @@ void prefill_qgemm_kernel(PfArgs a) {
 
 // ---- INT4 (groups of 32, 64 or a multiple of 128), INT8, GGUF Q4_0 / Q8_0 planes: one MFMA per product ----
 //
-// (GGUF: a d per 32-wide block, so a fold every two MFMA steps; Q4_0 decodes q - 8, Q8_0 the
-// signed byte q; the words of the planes map to k as described at WSet below.)
-// `prefill_i4_kernel<BM, D>` feeds the MFMA the exact integer (q - z) as bf16 (|q - z| <= 15)
-// and x as the bf16 it is.  Per 128-wide K block the MFMAs sum x (q - z) into a fresh f32
+// `prefill_i4_kernel<BM, D, NW, FMT, DW>` feeds the MFMA the exact integer (q - z) as bf16
+// (|q - z| <= 15) and x as the bf16 it is.  Per 128-wide K block the MFMAs sum x (q - z) into a fresh f32
 // partial, and one fma per accumulator applies the block's f16 group scale:
 // y = sum_b s_b * P_b, the GEMV's per-group partial scheme.  Each partial rounds 8 times
 // (one per 16-wide MFMA step) over 128 products and the total once per block, against the
@@ -487,7 +485,11 @@ void prefill_qgemm_kernel(PfArgs a) {
 //     BM rows x 256 bytes; 16-byte chunk c of row r sits at c ^ (r & 15), so the 16 rows that
 //     one read phase touches hit 16 distinct chunks.  MFMA step kk reads chunk 8 h + kk, the
 //     k range the W lane decoded.
-//   * One barrier per block; block b + D's loads are issued right after it.
+//   * One barrier per block; x of block b + D and W of block b + DW are issued right after it.
+//   * The other forms (instances by FMT): GGUF Q4_0 / Q8_0 (a d per 32-wide block, so a fold
+//     every two MFMA steps; q - 8 or the signed byte q) and INT4 with groups of 32 / 64 read
+//     their words in a step -> k map where no step straddles a group (WSet below); INT8 keeps
+//     one f32 sum and applies its row scale once.
 #ifndef CFH_PF_I4_DEPTH
 #define CFH_PF_I4_DEPTH 2
 #endif
