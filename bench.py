@@ -509,16 +509,36 @@ def main():
                          f"evaluator semantics (dequantize to f32, then the m,n,k f32 loop of "
                          f"eval.rs:1465-1507), single thread, {t_cpu:.1f} s"}
         log(f"[bench] cpu baseline {cpu['value']} GB/s over {passes} passes ({t_cpu:.1f}s)")
-        # CPU-C, the best-effort host figure (blocked, SIMD, all visible cores; oracle/cpu_best.c):
-        # reported beside the port, which stays the baseline
         import ctypes
-        cpub = ctypes.CDLL(str(ROOT / "oracle" / "_build" / "libcf_cpubest.so"))
         cp = ctypes.c_void_p
-        cpub.cpub_gemv_w4a16.argtypes = [cp, ctypes.c_int64, ctypes.c_int64, cp, cp, cp, cp, ctypes.c_int]
-        ncpu = len(os.sched_getaffinity(0))
+        ptr = lambda a: a.ctypes.data_as(cp)
         xf = [np.ascontiguousarray(O.bf16_bits_to_f32(x).reshape(-1), dtype=np.float32) for x in xh]
         yf = [np.zeros(n, np.float32) for (_, n, k) in synth.LLAMA7B_BLOCK]
-        ptr = lambda a: a.ctypes.data_as(cp)
+        # CPU-B, codegen-faithful: the loop nest the reference's Rust emitter writes for
+        # fused_qmatmul (dequant inline in the k loop), built like its JIT (-O3, no -march,
+        # no contraction), one thread (oracle/cpu_codegen.c)
+        cpg = ctypes.CDLL(str(ROOT / "oracle" / "_build" / "libcf_cpucodegen.so"))
+        cpg.cpcg_gemv_w4a16.argtypes = [cp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, cp, cp, cp, cp]
+        passes_b, t_b = 0, 0.0
+        while t_b < 6.0 and passes_b < 8:
+            t1 = time.perf_counter()
+            for (c, s_, z, n, k), x, y in zip(host, xf, yf):
+                cpg.cpcg_gemv_w4a16(ptr(x), 1, n, k, ptr(c), ptr(s_), ptr(z), ptr(y))
+            t_b += time.perf_counter() - t1
+            passes_b += 1
+        cpu["codegen_faithful"] = {
+            "value": round(w4_bytes(1) * passes_b / t_b / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "CPU-B codegen-faithful (oracle/cpu_codegen.c)",
+            "sample": f"{passes_b} pass(es) of the full block W4A16 GEMV at M=1 through the emitted "
+                      f"loop nest of rust_composites.rs:176-244 (dequant inline, f32 accumulator, no "
+                      f"FMA), gcc -O3 without -march, single thread, {t_b:.1f} s"}
+        log(f"[bench] cpu codegen-faithful {cpu['codegen_faithful']['value']} GB/s over {passes_b} passes "
+            f"({t_b:.1f}s)")
+        # CPU-C, the best-effort host figure (blocked, SIMD, all visible cores; oracle/cpu_best.c):
+        # reported beside the port, which stays the baseline
+        cpub = ctypes.CDLL(str(ROOT / "oracle" / "_build" / "libcf_cpubest.so"))
+        cpub.cpub_gemv_w4a16.argtypes = [cp, ctypes.c_int64, ctypes.c_int64, cp, cp, cp, cp, ctypes.c_int]
+        ncpu = len(os.sched_getaffinity(0))
         # 6 rotating copies of the block (630 MB), more than a host's last-level cache, as the GPU
         # side rotates copies past the MALL
         hosts = [host] + [[(c.copy(), s_.copy(), z.copy(), n, k) for (c, s_, z, n, k) in host] for _ in range(5)]

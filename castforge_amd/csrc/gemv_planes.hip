@@ -439,6 +439,7 @@ constexpr int kI4Depth = CFH_PLANES_I4_DEPTH;
 #ifndef CFH_PLANES_M1_GENERIC
 #define CFH_PLANES_M1_GENERIC 1  // M = 1 over INT4 GEMV planes on planes_m1_kernel (0: planes_kernel)
 #endif
+constexpr int kXRegs = 2;  // x loads (four chunks each) a wave issues ahead of its ring (K <= 16384)
 constexpr int kNf4LutCopies = 32;
 constexpr int kNf4LutBytes = 256 * kNf4LutCopies * 8;
 constexpr float kNf4Values[16] = {
@@ -511,29 +512,18 @@ void planes_m1_kernel(NBatch b) {
     const uint32_t aoff = soff + ((static_cast<uint32_t>(G) * 4 + 15) & ~15u);
     float *const accs = reinterpret_cast<float *>(lds + aoff);
 
-    // the decode table and the partials, before any copy into LDS is in flight
-    for (int i = tid; i < (KIND == kKindNf4 ? 256 * kNf4LutCopies : 0); i += 64 * NW) {
-        const int e = i / kNf4LutCopies;
-        const float v0 = kNf4Values[e & 15], v1 = kNf4Values[e >> 4];
-        const _Float16 h0 = static_cast<_Float16>(v0), h1 = static_cast<_Float16>(v1);
-        const _Float16 l0 = static_cast<_Float16>(v0 - static_cast<float>(h0));
-        const _Float16 l1 = static_cast<_Float16>(v1 - static_cast<float>(h1));
-        const half2_t hi = {h0, h1}, lo = {l0, l1};
-        reinterpret_cast<uint2 *>(lds)[i] = make_uint2(as_u(hi), as_u(lo));
-    }
-    for (int i = tid; i < ntiles * NW * 16; i += 64 * NW) accs[i] = 0.0f;
-
-    // x (bf16) straight into LDS, 1 KB per wave-wide copy
-    const int nblk = static_cast<int>((rowb + 1023u) / 1024u);
-    for (int i = wave; i < nblk; i += NW) {
-        const uint32_t e = i * 1024u + lane * 16u;
-        if (e < rowb)
-            __builtin_amdgcn_global_load_lds(
-                static_cast<const void *>(P.x + (e >> 1)),
-                reinterpret_cast<__attribute__((address_space(3))) void *>(reinterpret_cast<uintptr_t>(lds) + xoff +
-                                                                           i * 1024),
-                16, 0, 0);
-    }
+    // x first (straight into registers, 16 bytes a lane: wave load i holds chunks 4 i .. 4 i + 3,
+    // lane (c4, j) elements 8 j .. 8 j + 7 of chunk 4 i + c4), then the ring; the LDS work and the
+    // conversion run while both are in flight
+    const int nxl = (G + 3) >> 2;
+    const rsrc_t rx = make_rsrc(P.x, rowb);
+    uint4 xr[kXRegs];
+    static_for<kXRegs>([&](auto ii) __attribute__((always_inline)) {
+        constexpr int i = decltype(ii)::value;
+        const int xl = wave + i * NW;
+        xr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rx, (xl < nxl ? 0u : kOob) | (lane * 16u), static_cast<uint32_t>(xl) * 1024u, 0));
+    });
 
     const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
     const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
@@ -547,8 +537,11 @@ void planes_m1_kernel(NBatch b) {
     }
     int pt = lt, pg = lg;
     // per-lane offsets, pushed out of range (OR kOob) for rows outside [rlo, rhi) and past the
-    // workgroup's tiles; the absmax values multiply the MFMA result, whose rows lanes 0..15 hold
-    // (INT4: every lane needs its row's zero point for the exact q - z decode)
+    // workgroup's tiles; the chunk's own offset is wave-uniform (the loads' scalar offset).  The
+    // absmax values multiply the MFMA result, whose rows lanes 0..15 hold (INT4: every lane
+    // needs its row's zero point for the exact q - z decode).  A position past the workgroup's
+    // tiles reads scale 0 (out of range): its partial is 0 times a finite value or, for
+    // non-finite x, lands after the workgroup's last store of its running sum.
     uint32_t vcode, vam, vzero;
     auto lane_offsets = [&]() __attribute__((always_inline)) {
         const int row = (t0 + lt) * 16 + r16;
@@ -556,33 +549,33 @@ void planes_m1_kernel(NBatch b) {
         const uint32_t m = ok ? 0u : kOob;
         vcode = (static_cast<uint32_t>(lane) * 16u) | m;
         vam = (static_cast<uint32_t>(r16) * kMetaRow) | (lane < 16 ? m : kOob);
-        vzero = static_cast<uint32_t>(r16 >> 1) | m;
+        vzero = static_cast<uint32_t>((r16 >> 3) * 4) | m;  // the dword with rows 8 (r / 8) .. + 7
     };
     lane_offsets();
     auto load = [&](NStage &st) __attribute__((always_inline)) {
         const uint32_t chunk = static_cast<uint32_t>((t0 + lt) * G + lg);
         const uint4 v = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, vcode + chunk * 1024u, 0, CFH_PLANES_CPOL));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, vcode, chunk * 1024u, CFH_PLANES_CPOL));
         st.w[0] = v.x;
         st.w[1] = v.y;
         st.w[2] = v.z;
         st.w[3] = v.w;
-        const uint32_t ao = vam + chunk * (16u * kMetaRow);
+        const uint32_t ao = chunk * (16u * kMetaRow);
         if constexpr (I4) {  // the group's f16 scale (lanes 0..15) and zero-point byte (all lanes)
-            st.am[0] = __builtin_amdgcn_raw_buffer_load_b16(ramax, ao, 0, 0);
-            st.am[1] = __builtin_amdgcn_raw_buffer_load_b8(rzero, vzero + chunk * 8u, 0, 0);
+            st.am[0] = __builtin_amdgcn_raw_buffer_load_b16(ramax, vam, ao, 0);
+            st.am[1] = __builtin_amdgcn_raw_buffer_load_b32(rzero, vzero, chunk * 8u, 0);
         } else if constexpr (Q40) {  // the 4 blocks' f16 d
-            const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ramax, ao, 0, 0));
+            const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ramax, vam, ao, 0));
             st.am[0] = a.x;
             st.am[1] = a.y;
         } else if constexpr (NBPC == 1) {
-            st.am[0] = __builtin_amdgcn_raw_buffer_load_b32(ramax, ao, 0, 0);
+            st.am[0] = __builtin_amdgcn_raw_buffer_load_b32(ramax, vam, ao, 0);
         } else if constexpr (NBPC == 2) {
-            const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ramax, ao, 0, 0));
+            const uint2 a = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(ramax, vam, ao, 0));
             st.am[0] = a.x;
             st.am[1] = a.y;
         } else {
-            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ramax, ao, 0, 0));
+            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ramax, vam, ao, 0));
             st.am[0] = a.x;
             st.am[1] = a.y;
             st.am[2] = a.z;
@@ -602,56 +595,68 @@ void planes_m1_kernel(NBatch b) {
         load(st[i]);
         __builtin_amdgcn_sched_barrier(0);
     });
-    lds_barrier<(I4 ? 3 : 2) * D>();  // this wave's copies of x have landed; the table is written
 
-    // x to f16 in natural order, each chunk of 128 scaled by the power of two that brings its
-    // largest |x| into [2^14, 2^15) (every finite bf16 is then exact in f16 down to 2^-38 of
-    // that value); 2^sh is kept per chunk.  Eight lanes (16 values each) hold one chunk.
-    {
-        const int total = G * 8;
-        for (int base = 0; base < total; base += 64 * NW) {  // uniform trip count
-            const int i = base + tid;
-            const bool act = i < total;
-            const int j = act ? i : 0;
-            uint16_t *px = reinterpret_cast<uint16_t *>(lds + xoff) + j * 16;
-            const uint4 r0 = *reinterpret_cast<const uint4 *>(px);
-            const uint4 r1 = *reinterpret_cast<const uint4 *>(px + 8);
-            const uint32_t wv[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-            uint32_t emax = 0;
+    // the decode table and the partials
+    for (int i = tid; i < (KIND == kKindNf4 ? 256 * kNf4LutCopies : 0); i += 64 * NW) {
+        const int e = i / kNf4LutCopies;
+        const float v0 = kNf4Values[e & 15], v1 = kNf4Values[e >> 4];
+        const _Float16 h0 = static_cast<_Float16>(v0), h1 = static_cast<_Float16>(v1);
+        const _Float16 l0 = static_cast<_Float16>(v0 - static_cast<float>(h0));
+        const _Float16 l1 = static_cast<_Float16>(v1 - static_cast<float>(h1));
+        const half2_t hi = {h0, h1}, lo = {l0, l1};
+        reinterpret_cast<uint2 *>(lds)[i] = make_uint2(as_u(hi), as_u(lo));
+    }
+    for (int i = tid; i < ntiles * NW * 16; i += 64 * NW) accs[i] = 0.0f;
+
+    // x to f16, each chunk of 128 scaled by the power of two that brings its largest |x| into
+    // [2^14, 2^15) (every finite bf16 is then exact in f16 down to 2^-38 of that value); 2^sh is
+    // kept per chunk.  The 16 lanes of a DPP row hold one chunk.  NF4 keeps the natural order;
+    // Q4_0 and INT4 take, per 8 values, the pairs (0, 4), (1, 5), (2, 6), (3, 7) of their decode.
+    auto convert = [&](const uint4 &r, int xl) __attribute__((always_inline)) {
+        const uint32_t wv[4] = {r.x, r.y, r.z, r.w};
+        uint32_t emax = 0;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                emax = max(emax, (wv[q] >> 7) & 0xFFu);
-                emax = max(emax, (wv[q] >> 23) & 0xFFu);
-            }
-            {
-                int e = static_cast<int>(emax);
-                e = max(e, __builtin_amdgcn_mov_dpp(e, 0xB1, 0xF, 0xF, false));
-                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x4E, 0xF, 0xF, false));
-                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x141, 0xF, 0xF, false));
-                emax = static_cast<uint32_t>(e);
-            }
-            int sh = static_cast<int>(emax) - 127 - 14;
-            sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
-            const float pre = __uint_as_float(static_cast<uint32_t>(127 - sh) << 23);
-            const float post = __uint_as_float(static_cast<uint32_t>(127 + sh) << 23);
-            // NF4: natural order; Q4_0: per 8 values the pairs (0, 4), (1, 5), (2, 6), (3, 7) of
-            // the INT4 decode
-            constexpr int kPerm[16] = {0, 4, 1, 5, 2, 6, 3, 7, 8, 12, 9, 13, 10, 14, 11, 15};
-            uint32_t o[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int s0 = Q40 || I4 ? kPerm[2 * q] : 2 * q, s1 = Q40 || I4 ? kPerm[2 * q + 1] : 2 * q + 1;
-                const float f0 = bf16_to_f32(static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)))) * pre;
-                const float f1 = bf16_to_f32(static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)))) * pre;
-                o[q] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f0))) |
-                       (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f1))) << 16);
-            }
-            if (act) {
-                *reinterpret_cast<uint4 *>(px) = make_uint4(o[0], o[1], o[2], o[3]);
-                *reinterpret_cast<uint4 *>(px + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-                if ((i & 7) == 0) reinterpret_cast<float *>(lds + soff)[j >> 3] = post;
-            }
+        for (int q = 0; q < 4; ++q) {
+            emax = max(emax, (wv[q] >> 7) & 0xFFu);
+            emax = max(emax, (wv[q] >> 23) & 0xFFu);
         }
+        {
+            int e = static_cast<int>(emax);
+            e = max(e, __builtin_amdgcn_mov_dpp(e, 0x128, 0xF, 0xF, false));  // row_ror:8
+            e = max(e, __builtin_amdgcn_mov_dpp(e, 0x124, 0xF, 0xF, false));  // row_ror:4
+            e = max(e, __builtin_amdgcn_mov_dpp(e, 0x4E, 0xF, 0xF, false));
+            e = max(e, __builtin_amdgcn_mov_dpp(e, 0xB1, 0xF, 0xF, false));
+            emax = static_cast<uint32_t>(e);
+        }
+        int sh = static_cast<int>(emax) - 127 - 14;
+        sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
+        const float pre = __uint_as_float(static_cast<uint32_t>(127 - sh) << 23);
+        constexpr int kPerm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int s0 = Q40 || I4 ? kPerm[2 * q] : 2 * q, s1 = Q40 || I4 ? kPerm[2 * q + 1] : 2 * q + 1;
+            const float f0 = bf16_to_f32(static_cast<uint16_t>(wv[s0 >> 1] >> (16 * (s0 & 1)))) * pre;
+            const float f1 = bf16_to_f32(static_cast<uint16_t>(wv[s1 >> 1] >> (16 * (s1 & 1)))) * pre;
+            o[q] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f0))) |
+                   (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f1))) << 16);
+        }
+        const int g = 4 * xl + part;
+        if (xl < nxl && g < G) {
+            *reinterpret_cast<uint4 *>(lds + xoff + static_cast<uint32_t>(g) * 256u + r16 * 16u) =
+                make_uint4(o[0], o[1], o[2], o[3]);
+            if (r16 == 0)
+                reinterpret_cast<float *>(lds + soff)[g] = __uint_as_float(static_cast<uint32_t>(127 + sh) << 23);
+        }
+    };
+    static_for<kXRegs>([&](auto ii) __attribute__((always_inline)) {
+        constexpr int i = decltype(ii)::value;
+        convert(xr[i], wave + i * NW);
+    });
+    for (int xl = wave + kXRegs * NW; xl < nxl; xl += NW) {  // K > 16384 only (waits for the ring too)
+        const uint4 r = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, lane * 16u, static_cast<uint32_t>(xl) * 1024u, 0));
+        convert(r, xl);
     }
     lds_barrier<63>();
 
@@ -670,7 +675,7 @@ void planes_m1_kernel(NBatch b) {
             constexpr int i = decltype(ii)::value;
             const bool live = pt < ntiles;
             const NStage &s = st[i];
-            const int g = live ? pg : 0;
+            const int g = pg;
             // A fragment of MFMA q: x[128 g + 32 q + 8 p .. + 7] (INT4: x[128 g + 32 p + 8 q ..])
             const uint8_t *xa = lds + xoff + g * (kGroup * 2) + part * (I4 ? 64 : 16);
             constexpr int xq = I4 ? 16 : 64;
@@ -689,7 +694,7 @@ void planes_m1_kernel(NBatch b) {
                 if constexpr (Q40 || I4) {
                     // (1024 + q) - (1024 + z) and (1024 + 16 q) / 16 - (64 + z): the exact
                     // integers q - z (Q4_0: z = 8)
-                    const uint32_t zi = I4 ? (s.am[1] >> (4 * (r16 & 1))) & 15u : 8u;
+                    const uint32_t zi = I4 ? (s.am[1] >> (4 * (r16 & 7))) & 15u : 8u;
                     const half2_t zc1024 = as_h2((0xE400u + zi) * 0x00010001u);
                     const half2_t zc64 = as_h2((0xD400u + (zi << 4)) * 0x00010001u);
                     const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
@@ -723,7 +728,8 @@ void planes_m1_kernel(NBatch b) {
                 for (int j = 0; j < NBPC; ++j) t = __fadd_rn(t, __fmul_rn(c[j][0], __uint_as_float(s.am[j])));
                 v = __fmul_rn(t, post);
             }
-            acc = __fadd_rn(acc, live ? v : 0.0f);
+            asm volatile("" : "+v"(v));  // the product rounds on its own: no fused multiply-add into acc
+            acc = __fadd_rn(acc, v);
             const int tile = pt;
             pg += NW;
             while (pg >= G) {

@@ -289,3 +289,98 @@ def test_tanh_silu_epilogues_vs_float64():
     s = _epi(x, [0.25], None, "silu").astype(np.float64)
     v = x.astype(np.float64) + 0.25
     np.testing.assert_allclose(s, v / (1.0 + np.exp(-v)), rtol=1e-6, atol=1e-7)
+
+
+# --------------------------------------------------- composed dequant + matmul functions ----
+# orc_gemm_w8a16 / orc_gemm_nf4 / orc_gemm_fp8 restate eval.rs:303-318 (dequantize the constant
+# to f32) followed by eval_matmul_2d (eval.rs:1465-1507) over packed [N, K] weights.  Each is
+# checked against float64 products of weights decoded here from their bit layouts with numpy
+# (nibble k % 8 of word k / 8, block k // b, E4M3 through torch's float8 view), so a wrong
+# nibble order, block index, scale index (row vs column), or a transposed operand fails.
+def _nibbles(codes: np.ndarray, k: int) -> np.ndarray:
+    return np.stack([(codes >> (4 * i)) & 15 for i in range(8)], axis=-1).reshape(codes.shape[0], k)
+
+
+def test_dequantize_nf4_is_table_times_block_absmax():
+    """Bit-exact: out[r, i] = T[code] * absmax[r, i // block] as one f32 product; the absmax of
+    each block differs so a wrong block index changes the bits."""
+    rng = np.random.default_rng(101)
+    for n, k, block in [(5, 256, 32), (3, 512, 64), (4, 384, 128)]:
+        codes = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+        absmax = (rng.random((n, (k + block - 1) // block)) * 3 + 0.5).astype(np.float32)
+        got = O.dequantize_nf4(codes, absmax, n, k, block)
+        t = O.nf4_table().astype(np.float32)
+        want = (t[_nibbles(codes, k)] * np.repeat(absmax, block, axis=1)[:, :k]).astype(np.float32)
+        assert np.array_equal(got, want)
+
+
+def test_gemm_nf4_oracle_vs_float64():
+    rng = np.random.default_rng(102)
+    n, k, m, block = 20, 512, 3, 64
+    codes = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+    absmax = (rng.random((n, k // block)) * 0.05 + 0.01).astype(np.float32)
+    x = O.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    y = O.gemm_nf4(x, codes, absmax, n, k, block)
+    t = O.nf4_table().astype(np.float64)
+    w = t[_nibbles(codes, k)] * np.repeat(absmax.astype(np.float64), block, axis=1)
+    ref = O.bf16_bits_to_f32(x).astype(np.float64) @ w.T
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_gemm_w8a16_oracle_vs_float64():
+    """Per-row (output channel) scales: swapping rows and columns of the scale, or reading
+    the codes unsigned, fails."""
+    rng = np.random.default_rng(103)
+    n, k, m = 24, 320, 4
+    codes = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    scales = (rng.random(n) * 0.01 + 1e-3).astype(np.float32)
+    x = O.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    y = O.gemm_w8a16(x, codes, scales)
+    ref = O.bf16_bits_to_f32(x).astype(np.float64) @ (codes.astype(np.float64) * scales[:, None].astype(np.float64)).T
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_gemm_fp8_oracle_vs_float64():
+    """Activations per token (row of A) and weights per row of W, both E4M3FN codes: decoded
+    here by torch's float8_e4m3fn view (not the oracle's codec)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(104)
+    m, n, k = 6, 10, 256
+    qa = rng.integers(0, 256, (m, k)).astype(np.uint8)
+    qw = rng.integers(0, 256, (n, k)).astype(np.uint8)
+    qa[(qa & 0x7F) == 0x7F] = 0x10   # the two NaN codes
+    qw[(qw & 0x7F) == 0x7F] = 0x22
+    sa = (rng.random(m) + 0.25).astype(np.float32)
+    sw = (rng.random(n) * 0.01 + 1e-3).astype(np.float32)
+    y = O.gemm_fp8(qa, sa, qw, sw)
+    da = torch.from_numpy(qa).view(torch.float8_e4m3fn).double().numpy()
+    dw = torch.from_numpy(qw).view(torch.float8_e4m3fn).double().numpy()
+    ref = (da * sa[:, None].astype(np.float64)) @ (dw * sw[:, None].astype(np.float64)).T
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_quantize_int4g_awq_prescales_columns():
+    """AWQ pre-scale W'[r, c] = f32(W[r, c] * s[c]) (per input channel, i.e. column):
+    * s = 1 gives the plain quantizer's arrays;
+    * s = 2^j for all columns leaves codes and zero points unchanged and multiplies every f16
+      scale by exactly 2^j (every step of the quantizer is homogeneous in powers of two);
+    * per-column s on a non-square matrix matches the plain quantizer of numpy's f32 W * s,
+      and not of W * s applied along rows."""
+    rng = np.random.default_rng(105)
+    n, k = 12, 384
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    base = O.quantize_int4g(w, 128)
+    for a, b in zip(O.quantize_int4g_awq(w, np.ones(k, np.float32), 128), base):
+        assert np.array_equal(a, b)
+    c4, s4, z4 = O.quantize_int4g_awq(w, np.full(k, 4.0, np.float32), 128)
+    assert np.array_equal(c4, base[0]) and np.array_equal(z4, base[2])
+    g = k // 128
+    assert np.array_equal(s4[:, :g].view(np.float16).astype(np.float32),
+                          base[1][:, :g].view(np.float16).astype(np.float32) * 4)
+    s = np.exp(rng.standard_normal(k) * 0.5).astype(np.float32)
+    got = O.quantize_int4g_awq(w, s, 128)
+    want = O.quantize_int4g((w * s[None, :]).astype(np.float32), 128)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)
+    wrong = O.quantize_int4g((w * s[:n, None]).astype(np.float32), 128)
+    assert not np.array_equal(got[0], wrong[0])
