@@ -583,7 +583,7 @@ def main():
                    "value_is": "W4A16 GEMV GB/s at M=1 (algorithmic bytes / whole-job time per step)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "planes_m1_kernel<16, 2, 1, 2>", "bytes_per_launch": bytes_m1,
+                     "kernel": "planes_i8_kernel<16, 2>", "bytes_per_launch": bytes_m1,
                      "us_per_launch": round(ms_step * 1e3, 2), "timing": timing},
         "cpu_baseline": cpu,
         "components": components,

@@ -1,7 +1,8 @@
 // W4A16 decode GEMV (M = 1..8) over INT4 g128 weights in the GEMV planes layout, and the M = 1
 // decode GEMV over NF4 planes and GGUF Q4_0 GEMV planes, gfx950.  planes_kernel serves INT4 at
-// M = 2..8; planes_m1_kernel (after it) serves M = 1 for the three formats, INT4 with the same
-// arithmetic as planes_kernel at M = 1.
+// M = 2..8; planes_m1_kernel (after it) serves M = 1 for the three formats; planes_i8_kernel
+// serves INT4 at M = 1 on the integer MFMA wherever its x pieces fit LDS (planes_m1_kernel's
+// INT4 form, with the same arithmetic as planes_kernel, beyond).
 //
 // Replaces the evaluation of `castforge.fused_qmatmul` at decode (eval.rs:1145-1179 with
 // eval_matmul_2d, eval.rs:1465-1507; packed_rhs [N, K] weights, fold.rs:549-554) for the
@@ -759,6 +760,289 @@ void planes_m1_kernel(NBatch b) {
     }
 }
 
+// ---- M = 1, INT4 g128 GEMV planes on the integer MFMA ------------------------------------------
+// planes_i8_kernel: the M = 1 INT4 GEMV over the same GEMV planes, work split, ring and
+// per-(tile, wave) partials as planes_m1_kernel, with the products formed exactly in integers:
+//   * x: each chunk of 128 (one group) is scaled by 2^(147 - e), e the biased exponent of its
+//     largest |x| (1 for zero and subnormal chunks): t = x * 2^(147 - e), |t| < 2^21.  Its nearest
+//     integer X = p0 + 256 p1 + 65536 p2 (signed bytes p0, p1 in [-128, 127], p2 in [-32, 31])
+//     comes from t + (2^23 + 0x408080), a float in [2^23, 2^24) whose low 23 bits are
+//     X + 0x408080 (one xor and add give the three bytes); the residual t - X, |t - X| <= 1/2,
+//     is the fourth piece p3 = RN(128 (t - X)).  So t = X + p3 / 128 exactly for every element
+//     within 2^-20 of the chunk's largest, and to within 2^-28 of the largest for the others.  The
+//     pieces are rows 0..3 of the MFMA's A operand (rows 4..15 repeat row 3; their results are
+//     not used).
+//   * codes: nibble q of the planes becomes the signed byte 16 (q - 8) = (q ^ 8) << 4: the high
+//     nibbles of a word by one and-xor, the low ones after a 4-bit rotation.  Even elements of a
+//     lane's 32 take one v_mfma_i32_16x16x64_i8, odd ones a second, into one i32 accumulator:
+//     c_i = sum over the group of p_i 16 (q - 8), exact.
+//   * the zero point: D_i = c_i + 16 (8 - z) S_i = 16 sum p_i (q - z) exactly, S_i = sum of p_i
+//     over the chunk (kept per chunk in LDS, |D_i| < 2^22), and 16 sum t (q - z) =
+//     L + D_3 / 128 + 65536 D_2 with L = D_0 + 256 D_1 (exact in i32), made f32 by two fmas,
+//     smallest term first.  The chunk's f32 partial is ((that * s) * 2^a) * 2^b with
+//     2^(a + b) = 2^(e - 151), so y(2^k x) = 2^k y(x) bit for bit while no partial leaves the
+//     f32 range.  A chunk holding inf or NaN gives NaN partials.
+//   * per chunk: 12 VALU for the decode, 2 MFMAs and 3 LDS reads, against 36 VALU, 4 MFMAs and
+//     4 LDS reads of the f16 form.
+// LDS: [x pieces: per chunk 4 parts x (4 pieces x (16 B even, 16 B odd)) = 512 B][per chunk
+// S0 | S1 << 16, S2 | S3 << 16, 2^a, 2^b: 16 B][partials: tiles x NW x 16 f32]
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kI8ChunkX = 512;
+constexpr uint32_t kI8ChunkRec = 16;
+// positions a wave loads into registers of their own before the ring (E + D in flight while x
+// is converted); E = 4 over D = 2 measured 20.45 against 20.66 us for the ring alone (D = 3: 20.76)
+constexpr int kI8Pre = 4;
+
+template <int NW, int D>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)))
+void planes_i8_kernel(NBatch b) {
+    constexpr int E = kI8Pre;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = uni(tid >> 6);
+    const int w = blockIdx.x;
+    const int r16 = lane & 15, part = lane >> 4;
+
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < CFH_MAX_BATCH; ++i)
+        if (i < b.count && w >= b.p[i].wg0) pi = i;
+    const NProblem &P = b.p[pi];
+    const int G = P.G, local = w - P.wg0;
+    const int u0 = static_cast<int>(static_cast<uint32_t>(local * P.units) / static_cast<uint32_t>(P.wgs));
+    const int u1 = static_cast<int>(static_cast<uint32_t>((local + 1) * P.units) / static_cast<uint32_t>(P.wgs));
+    const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
+    const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
+    const int ntiles = t1 - t0, npos = ntiles * G;
+    const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2);
+    const uint32_t soff = static_cast<uint32_t>(G) * kI8ChunkX;
+    const uint32_t aoff = soff + static_cast<uint32_t>(G) * kI8ChunkRec;
+    float *const accs = reinterpret_cast<float *>(lds + aoff);
+
+    // x first (straight into registers, 16 bytes a lane: wave load i holds chunks 4 i .. 4 i + 3,
+    // lane (c4, j) elements 8 j .. 8 j + 7 of chunk 4 i + c4), then the ring
+    const int nxl = (G + 3) >> 2;
+    const rsrc_t rx = make_rsrc(P.x, rowb);
+    uint4 xr[kXRegs];
+    static_for<kXRegs>([&](auto ii) __attribute__((always_inline)) {
+        constexpr int i = decltype(ii)::value;
+        const int xl = wave + i * NW;
+        xr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rx, (xl < nxl ? 0u : kOob) | (lane * 16u), static_cast<uint32_t>(xl) * 1024u, 0));
+    });
+
+    const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
+    const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
+    const rsrc_t rscale = make_rsrc(P.absmax, chunks * 32u);
+    const rsrc_t rzero = make_rsrc(P.zeros, chunks * 8u);
+    int lt = 0, lg = wave;
+    while (lg >= G) {
+        lg -= G;
+        ++lt;
+    }
+    int pt = lt, pg = lg;
+    // per-lane offsets, pushed out of range (OR kOob) for rows outside [rlo, rhi) and past the
+    // workgroup's tiles: the f16 scale on lanes 0..15 (whose rows the MFMA result holds), the
+    // zero-point dword with rows 8 (r / 8) .. + 7 on every lane.  A position past the tiles reads
+    // scale 0 and is never stored.
+    uint32_t vcode, vsc, vzero;
+    auto lane_offsets = [&]() __attribute__((always_inline)) {
+        const int row = (t0 + lt) * 16 + r16;
+        const bool ok = lt < ntiles && row >= rlo && row < rhi;
+        const uint32_t m = ok ? 0u : kOob;
+        vcode = (static_cast<uint32_t>(lane) * 16u) | m;
+        vsc = (static_cast<uint32_t>(r16) * 2u) | (lane < 16 ? m : kOob);
+        vzero = static_cast<uint32_t>((r16 >> 3) * 4) | m;
+    };
+    lane_offsets();
+    auto load = [&](NStage &st) __attribute__((always_inline)) {
+        const uint32_t chunk = static_cast<uint32_t>((t0 + lt) * G + lg);
+        const uint4 v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, vcode, chunk * 1024u, CFH_PLANES_CPOL));
+        st.w[0] = v.x;
+        st.w[1] = v.y;
+        st.w[2] = v.z;
+        st.w[3] = v.w;
+        st.am[0] = __builtin_amdgcn_raw_buffer_load_b16(rscale, vsc, chunk * 32u, 0);
+        st.am[1] = __builtin_amdgcn_raw_buffer_load_b32(rzero, vzero, chunk * 8u, 0);
+        lg += NW;
+        if (lg >= G) {
+            do {
+                lg -= G;
+                ++lt;
+            } while (lg >= G);
+            lane_offsets();
+        }
+    };
+    // the wave's first E positions go into registers of their own, then the ring's D: E + D
+    // positions in flight while x is converted
+    NStage pre[E], st[D];
+    static_for<E>([&](auto i) __attribute__((always_inline)) {
+        load(pre[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<D>([&](auto i) __attribute__((always_inline)) {
+        load(st[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+
+    for (int i = tid; i < ntiles * NW * 16; i += 64 * NW) accs[i] = 0.0f;
+
+    // x to pieces.  The 16 lanes of a DPP row hold one chunk; lane j's 8 elements are the even
+    // and odd elements 4 (j % 4) .. + 3 of part j / 4, i.e. dword j % 4 of each 16-byte block.
+    auto convert = [&](const uint4 &r, int xl) __attribute__((always_inline)) {
+        const uint32_t wv[4] = {r.x, r.y, r.z, r.w};  // element 2 q: low half of wv[q], 2 q + 1: high half
+        int e = 1;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            e = max(e, static_cast<int>((wv[q] >> 7) & 0xFFu));
+            e = max(e, static_cast<int>((wv[q] >> 23) & 0xFFu));
+        }
+        e = max(e, __builtin_amdgcn_mov_dpp(e, 0x128, 0xF, 0xF, false));  // row_ror:8
+        e = max(e, __builtin_amdgcn_mov_dpp(e, 0x124, 0xF, 0xF, false));  // row_ror:4
+        e = max(e, __builtin_amdgcn_mov_dpp(e, 0x4E, 0xF, 0xF, false));
+        e = max(e, __builtin_amdgcn_mov_dpp(e, 0xB1, 0xF, 0xF, false));
+        const int kx = 147 - e;
+        // bytes 0..2 of pc[k] are the pieces p0, p1, p2 of element k, byte 0 of rc[k] is p3
+        uint32_t pc[8], rc[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t h = wv[k >> 1];
+            const float xf = __uint_as_float((k & 1) ? (h & 0xFFFF0000u) : (h << 16));
+            const float t = __builtin_amdgcn_ldexpf(xf, kx);
+            const float rf = t + 12615808.0f;  // 2^23 + 0x408080: rounds t to an integer
+            const float res = t - (rf - 12615808.0f);  // both steps exact
+            pc[k] = (__float_as_uint(rf) ^ 0x8080u) + 0xC00000u;
+            rc[k] = __float_as_uint(__builtin_fmaf(res, 128.0f, 12582912.0f));  // 1.5 * 2^23 + p3
+        }
+        // gather: piece i of elements 0, 2, 4, 6 (even) and 1, 3, 5, 7 (odd), one byte each
+        uint32_t ev[4], od[4];
+        auto gather = [&](int k0, uint32_t *out) __attribute__((always_inline)) {
+            const uint32_t a01 = __builtin_amdgcn_perm(pc[k0 + 2], pc[k0], 0x05010400u);  // p0[0] p0[2] p1[0] p1[2]
+            const uint32_t a45 = __builtin_amdgcn_perm(pc[k0 + 6], pc[k0 + 4], 0x05010400u);
+            const uint32_t b01 = __builtin_amdgcn_perm(pc[k0 + 2], pc[k0], 0x0C0C0602u);  // p2[0] p2[2]
+            const uint32_t b45 = __builtin_amdgcn_perm(pc[k0 + 6], pc[k0 + 4], 0x0C0C0602u);
+            const uint32_t c01 = __builtin_amdgcn_perm(rc[k0 + 2], rc[k0], 0x0C0C0400u);  // p3[0] p3[2]
+            const uint32_t c45 = __builtin_amdgcn_perm(rc[k0 + 6], rc[k0 + 4], 0x0C0C0400u);
+            out[0] = __builtin_amdgcn_perm(a45, a01, 0x05040100u);
+            out[1] = __builtin_amdgcn_perm(a45, a01, 0x07060302u);
+            out[2] = __builtin_amdgcn_perm(b45, b01, 0x05040100u);
+            out[3] = __builtin_amdgcn_perm(c45, c01, 0x05040100u);
+        };
+        gather(0, ev);
+        gather(1, od);
+        // S_i over the chunk: this lane's 8 bytes, then the 16 lanes of the row
+        int s[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s[i] = __builtin_amdgcn_sdot4(static_cast<int>(ev[i]), 0x01010101, 0, false);
+            s[i] = __builtin_amdgcn_sdot4(static_cast<int>(od[i]), 0x01010101, s[i], false);
+            s[i] += __builtin_amdgcn_mov_dpp(s[i], 0x128, 0xF, 0xF, false);
+            s[i] += __builtin_amdgcn_mov_dpp(s[i], 0x124, 0xF, 0xF, false);
+            s[i] += __builtin_amdgcn_mov_dpp(s[i], 0x4E, 0xF, 0xF, false);
+            s[i] += __builtin_amdgcn_mov_dpp(s[i], 0xB1, 0xF, 0xF, false);
+        }
+        const int g = 4 * xl + part;
+        if (xl < nxl && g < G) {
+            uint8_t *const px = lds + static_cast<uint32_t>(g) * kI8ChunkX + (r16 >> 2) * 128u + (r16 & 3) * 4u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                *reinterpret_cast<uint32_t *>(px + i * 32) = ev[i];
+                *reinterpret_cast<uint32_t *>(px + i * 32 + 16) = od[i];
+            }
+            if (r16 == 0) {
+                // 2^(e - 151) as 2^a * 2^b, both normal: a = max(e - 151, -126)
+                const int a = max(e - 151, -126), bx = e - 151 - a;
+                const float pa = e == 255 ? __uint_as_float(0x7FC00000u) : __uint_as_float(static_cast<uint32_t>(127 + a) << 23);
+                const float pb = __uint_as_float(static_cast<uint32_t>(127 + bx) << 23);
+                *reinterpret_cast<uint4 *>(lds + soff + static_cast<uint32_t>(g) * kI8ChunkRec) =
+                    make_uint4((static_cast<uint32_t>(s[0]) & 0xFFFFu) | (static_cast<uint32_t>(s[1]) << 16),
+                               (static_cast<uint32_t>(s[2]) & 0xFFFFu) | (static_cast<uint32_t>(s[3]) << 16),
+                               __float_as_uint(pa), __float_as_uint(pb));
+            }
+        }
+    };
+    static_for<kXRegs>([&](auto ii) __attribute__((always_inline)) {
+        constexpr int i = decltype(ii)::value;
+        convert(xr[i], wave + i * NW);
+    });
+    for (int xl = wave + kXRegs * NW; xl < nxl; xl += NW) {  // K > 16384 only (waits for the ring too)
+        const uint4 r = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, lane * 16u, static_cast<uint32_t>(xl) * 1024u, 0));
+        convert(r, xl);
+    }
+    lds_barrier<63>();
+
+    // A operand of lane (i, p): piece min(i, 3) of part p, the even block (+16: the odd block)
+    const uint32_t xlane = static_cast<uint32_t>(part) * 128u + static_cast<uint32_t>(min(r16, 3)) * 32u;
+    float acc = 0.0f;
+    const int steps = npos > wave ? (npos - wave + NW - 1) / NW : 0;
+    auto consume = [&](const NStage &s) __attribute__((always_inline)) {
+        const bool live = pt < ntiles;
+        const int g = pg;
+        const uint8_t *xa = lds + static_cast<uint32_t>(g) * kI8ChunkX + xlane;
+        const int32x4 a1 = *reinterpret_cast<const int32x4 *>(xa);
+        const int32x4 a2 = *reinterpret_cast<const int32x4 *>(xa + 16);
+        const uint4 rec = *reinterpret_cast<const uint4 *>(lds + soff + static_cast<uint32_t>(g) * kI8ChunkRec);
+        int32x4 blo, bhi;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            blo[q] = static_cast<int>((__builtin_rotateleft32(s.w[q], 4) ^ 0x88888888u) & 0xF0F0F0F0u);
+            bhi[q] = static_cast<int>((s.w[q] ^ 0x88888888u) & 0xF0F0F0F0u);
+        }
+        int32x4 c = {0, 0, 0, 0};
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, blo, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, bhi, c, 0, 0, 0);
+        const int zc = 128 - static_cast<int>(((s.am[1] >> (4 * (r16 & 7))) & 15u) << 4);  // 16 (8 - z)
+        const int d0 = c[0] + zc * (static_cast<int>(rec.x << 16) >> 16);
+        const int d1 = c[1] + zc * (static_cast<int>(rec.x) >> 16);
+        const int d2 = c[2] + zc * (static_cast<int>(rec.y << 16) >> 16);
+        const int d3 = c[3] + zc * (static_cast<int>(rec.y) >> 16);
+        const int lo = d0 + (d1 << 8);
+        const float f = __builtin_fmaf(static_cast<float>(d2), 65536.0f,
+                                       __builtin_fmaf(static_cast<float>(d3), 0.0078125f, static_cast<float>(lo)));
+        float v = __fmul_rn(f, f16_to_f32(static_cast<uint16_t>(s.am[0])));
+        v = __fmul_rn(__fmul_rn(v, __uint_as_float(rec.z)), __uint_as_float(rec.w));
+        asm volatile("" : "+v"(v));  // the product rounds on its own: no fused multiply-add into acc
+        acc = __fadd_rn(acc, v);
+        const int tile = pt;
+        pg += NW;
+        while (pg >= G) {
+            pg -= G;
+            ++pt;
+        }
+        if (live && pt != tile) {
+            if (lane < 16) accs[(tile * NW + wave) * 16 + lane] = acc;
+            acc = 0.0f;
+        }
+    };
+    static_for<E>([&](auto i) __attribute__((always_inline)) {
+        if (decltype(i)::value < steps) consume(pre[decltype(i)::value]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    for (int k = E; k < steps; k += D) {
+        static_for<D>([&](auto ii) __attribute__((always_inline)) {
+            constexpr int i = decltype(ii)::value;
+            consume(st[i]);
+            load(st[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    lds_barrier<63>();
+
+    for (int i = tid; i < ntiles * 16; i += 64 * NW) {
+        const int row = (t0 + (i >> 4)) * 16 + (i & 15);
+        if (row >= rlo && row < rhi) {
+            const float *pa = accs + (i >> 4) * NW * 16 + (i & 15);
+            float v = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) v += pa[w2 * 16];
+            if (b.y_bf16) static_cast<uint16_t *>(P.y)[row] = f32_to_bf16_rne(v);
+            else static_cast<float *>(P.y)[row] = v;
+        }
+    }
+}
+
 // ---- canonical <-> planes ------------------------------------------------------------------
 // One thread per 16-byte unit of the codes planes / per (tile, group, row) of the metadata.
 __global__ void to_planes_kernel(const uint32_t *codes, const uint16_t *scales, const uint32_t *zeros, int64_t n,
@@ -970,6 +1254,7 @@ int64_t planes_lds(int mr, int nw, const PProblem &P) {
 
 template <int NBPC, int KIND = kKindNf4>
 void launch_planes_m1(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st);
+void launch_planes_i8(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st);
 
 // M = 1: one row of x per problem (16 waves); M = 2..4: up to 4 rows (16 waves); M = 5..8:
 // up to 8 rows (8 waves), a problem whose 8 rows of x do not fit LDS next to its partials
@@ -1005,7 +1290,7 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
         }
         const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
         NBatch nb{};
-        int64_t need_max = 0, ngrid = 0;
+        int64_t need_max = 0, need_i8 = 0, ngrid = 0;
         for (int j = 0; j < count; ++j) {
             const cfh_w4a16_problem_t &q = problems[j];
             NProblem &P = nb.p[j];
@@ -1024,9 +1309,14 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
             const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
             need_max = std::max<int64_t>(need_max, int64_t(P.G) * 256 + (int64_t(P.G) * 4 + 15) / 16 * 16 +
                                                        tiles * kWaves * 64);
+            need_i8 = std::max<int64_t>(need_i8, int64_t(P.G) * (kI8ChunkX + kI8ChunkRec) + tiles * kWaves * 64);
         }
         nb.count = count;
         nb.y_bf16 = y_dtype == CFH_DTYPE_BF16;
+        if (need_i8 <= kLdsMax / kWgPerCu) {  // the integer form wherever its x pieces fit LDS
+            launch_planes_i8(nb, ngrid, std::max<int64_t>(need_i8, kLdsFloor), st);
+            return;
+        }
         require(need_max <= kLdsMax / kWgPerCu, "a problem of the batch exceeds the GEMV planes kernel's LDS (m * k too "
                                                 "large or too many rows per workgroup)");
         launch_planes_m1<1, kKindInt4>(nb, ngrid, std::max<int64_t>(need_max, kLdsFloor), st);
@@ -1112,6 +1402,25 @@ void launch_planes_m1(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st
     planes_m1_kernel<kWaves, D, NBPC, KIND>
         <<<dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), static_cast<size_t>(lds), st>>>(b);
     check_launch("planes_m1_kernel");
+}
+
+void launch_planes_i8(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st) {
+    static std::mutex mu;
+    static std::map<int, bool> attr_set;  // per device
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    {
+        std::lock_guard<std::mutex> g(mu);
+        if (!attr_set[dev]) {
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_i8_kernel<kWaves, kI4Depth>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
+                      "hipFuncSetAttribute");
+            attr_set[dev] = true;
+        }
+    }
+    planes_i8_kernel<kWaves, kI4Depth>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(64 * kWaves), static_cast<size_t>(lds), st>>>(b);
+    check_launch("planes_i8_kernel");
 }
 
 bool nf4_block_ok(int64_t block) { return block >= 32 && block <= (int64_t(1) << 20) && (block & (block - 1)) == 0; }
