@@ -789,9 +789,11 @@ void planes_m1_kernel(NBatch b) {
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kI8ChunkX = 512;
 constexpr uint32_t kI8ChunkRec = 16;
-// positions a wave loads into registers of their own before the ring (E + D in flight while x
-// is converted); E = 4 over D = 2 measured 20.45 against 20.66 us for the ring alone (D = 3: 20.76)
-constexpr int kI8Pre = 4;
+// positions a wave loads into registers of their own ahead of the ring, after its x has landed
+// (x first: weight loads issued together with x delay every CU's x behind the others' weight
+// traffic).  More in flight per CU is slower: E = 1 / 4 / 6 / 8 over D = 2 measured 20.22 /
+// 20.46 / 20.85 / 21.18 us.
+constexpr int kI8Pre = 1;
 
 template <int NW, int D>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)))
@@ -820,7 +822,7 @@ void planes_i8_kernel(NBatch b) {
     float *const accs = reinterpret_cast<float *>(lds + aoff);
 
     // x first (straight into registers, 16 bytes a lane: wave load i holds chunks 4 i .. 4 i + 3,
-    // lane (c4, j) elements 8 j .. 8 j + 7 of chunk 4 i + c4), then the ring
+    // lane (c4, j) elements 8 j .. 8 j + 7 of chunk 4 i + c4); the weight loads once it has landed
     const int nxl = (G + 3) >> 2;
     const rsrc_t rx = make_rsrc(P.x, rowb);
     uint4 xr[kXRegs];
@@ -831,6 +833,7 @@ void planes_i8_kernel(NBatch b) {
                                               rx, (xl < nxl ? 0u : kOob) | (lane * 16u), static_cast<uint32_t>(xl) * 1024u, 0));
     });
 
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // see kI8Pre
     const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
     const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
     const rsrc_t rscale = make_rsrc(P.absmax, chunks * 32u);
