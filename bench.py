@@ -471,9 +471,20 @@ def main():
             components[f"fp8_gemm_exact_{tag}_pct_f16_peak"] = round(100 * 2.0 * m * n * k / (le * 1e-3) / 2.5e15, 1)
             lq = time_steps(lambda i: ops.quantize_fp8(a16), 20, 3)
             components[f"fp8_act_quant_{tag}_GBps"] = round((m * k * 3 + m * 4) / (lq * 1e-3) / 1e9, 1)
+
+            # the W8A8 step end to end: per-token E4M3 quantize of the bf16 activations, then
+            # the GEMM on the fresh codes (weights quantized once, outside the step)
+            def w8a8(i):
+                qx, sx = ops.quantize_fp8(a16)
+                ops.gemm_fp8(qx, sx, qw, sw, y)
+
+            lw = time_steps(w8a8, 20, 3)
+            components[f"fp8_w8a8_step_{tag}_us"] = round(lw * 1e3, 2)
+            components[f"fp8_w8a8_step_{tag}_TFLOPs"] = round(2.0 * m * n * k / (lw * 1e-3) / 1e12, 1)
             log(f"[bench] FP8 GEMM {tag}: {la * 1e3:.1f} us, {components[f'fp8_gemm_{tag}_TFLOPs']} TFLOP/s "
                 f"(exact form {le * 1e3:.1f} us, {components[f'fp8_gemm_exact_{tag}_TFLOPs']} TFLOP/s); "
-                f"act quant {components[f'fp8_act_quant_{tag}_GBps']} GB/s")
+                f"act quant {components[f'fp8_act_quant_{tag}_GBps']} GB/s; W8A8 step (quantize + GEMM) "
+                f"{lw * 1e3:.1f} us, {components[f'fp8_w8a8_step_{tag}_TFLOPs']} TFLOP/s")
             del w, a16, qw, sw, qa, sa, y
 
     components["w4a16_gemv_m1_GBps"] = round(value, 1)

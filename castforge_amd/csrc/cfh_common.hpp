@@ -216,6 +216,13 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 template <int WIDTH>
+__device__ __forceinline__ uint32_t wave_umax(uint32_t v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, o, 64)));
+    return v;
+}
+
+template <int WIDTH>
 __device__ __forceinline__ uint32_t wave_or(uint32_t v) {
 #pragma unroll
     for (int o = WIDTH / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);

@@ -253,53 +253,135 @@ __global__ __launch_bounds__(kBlock) void rows_quant_reg_kernel(RowSets<typename
     if (threadIdx.x == 0) scales[row] = scale;
 }
 
-// Per-token E4M3 of bf16 rows with cols % 8 == 0: rows_quant_reg_kernel's computation with one
-// 16-byte load of 8 values and one 8-byte store of 8 codes per lane and step (the 4-value form
-// issues twice the memory instructions; measured 3.1 TB/s on 4096 x 11008 with it).
-template <int VPT>
-__global__ __launch_bounds__(kBlock) void fp8_rows_bf16x8_kernel(const uint16_t *__restrict__ src, int64_t cols,
-                                                                 uint8_t *__restrict__ codes,
-                                                                 float *__restrict__ scales) {
-    __shared__ float red[kBlock / 64];
-    const int64_t row = blockIdx.x;
+// Per-token E4M3 of bf16 rows with cols % 8 == 0: rows_quant_reg_kernel's codes and scales
+// with one 16-byte load of 8 values and one 8-byte store of 8 codes per lane and step.  TPR
+// threads share a row: a workgroup of 256 threads holds 4 rows at TPR = 64 (no barrier), else
+// one row over NT = TPR threads.  Each thread keeps VPT 16-byte pieces of its row in
+// registers, so HBM sees each input byte once.  Threads past the row's end load its last 8
+// values again (an index clamp, not a branch: a load under a divergent branch gets a wait of
+// its own, and the loads would run one after another); a repeated element leaves the absmax
+// unchanged, and those threads store nothing.
+//
+// For a row without NaN or infinity (the case this kernel is built for):
+// - the absmax comes from the bit patterns: |v| of non-NaN bf16 values orders as the
+//   magnitude bits, so a packed 16-bit max of (bits & 0x7fff) is the absmax's top half (a
+//   result of 0x7f80 means an infinity, above it a NaN; both take the general path below);
+// - amax finite gives 2.2e-15 <= scale <= 7.6e35 and y = 1 / scale normal, |v * y| <= 448.0001,
+//   so div_by_scale's clamp never acts and is left out.  q0 = v * y corrected by two fmas,
+//   q = q0 - (q0 * scale - v) * y, is the rounded quotient v / scale: div_by_scale's
+//   residual with its sign flipped, which rounds to the same magnitudes and also keeps the
+//   sign of a zero quotient (v = -0, or -tiny / scale underflowing: the last fma then adds
+//   -0 to -0 or rounds a negative product, where q0 + (v - q0 * scale) * y gives +0);
+// - |q| < 464, so q is never NaN and never reaches the conversion's NaN range: of the inputs
+//   where v_cvt_pk_fp8_f32 differs from f32_to_e4m3fn only the log2-quirk mantissas
+//   (0x7ffffe / 0x7fffff) remain, found by one unsigned max over 8 bit fields of 22 bits.
+template <int VPT, int TPR, int NT>
+__global__ __launch_bounds__(NT) void fp8_rows_bf16x8_kernel(const uint16_t *__restrict__ src, int64_t rows,
+                                                             int64_t cols, uint8_t *__restrict__ codes,
+                                                             float *__restrict__ scales) {
+    static_assert(TPR % 64 == 0 && (TPR == 64 ? NT == 256 : NT == TPR), "4 one-wave rows or one row per workgroup");
+    constexpr int kWavesPerRow = TPR / 64;
+    __shared__ uint32_t red[kWavesPerRow];
+    const int t = threadIdx.x % TPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (NT / TPR) + threadIdx.x / TPR;
+    const bool live = row < rows;  // only a last, partial workgroup at TPR = 64 has rows past the end
     const int64_t nv = cols >> 3;
-    const uint4 *p = reinterpret_cast<const uint4 *>(src + row * cols);
-    float4 lo[VPT], hi[VPT];
-    float am = 0.0f;
+    const uint4 *p = reinterpret_cast<const uint4 *>(src + (live ? row : 0) * cols);
+    uint4 u[VPT];
+    static_for<VPT>([&](auto i) __attribute__((always_inline)) {
+        u[i] = p[min(t + static_cast<int64_t>(i) * TPR, nv - 1)];
+    });
+    // row-wide max of a non-negative u32 (workgroup-uniform call: one row per workgroup when
+    // the row spans several waves)
+    auto row_umax = [&](uint32_t v) {
+        v = wave_umax<64>(v);
+        if constexpr (kWavesPerRow > 1) {
+            __syncthreads();  // red[] may still be read by a previous call
+            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+            __syncthreads();
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
-        if (idx < nv) {
-            const uint4 u = p[idx];
-            lo[i] = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                                __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
-            hi[i] = make_float4(__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
-                                __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u));
-            am = amax4(amax4(am, lo[i]), hi[i]);
+            for (int w = 0; w < kWavesPerRow; ++w) v = max(v, red[w]);
         }
-    }
-    am = block_max(am, red);
+        return v;
+    };
+    typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+    us2 mh = {0, 0};
+    static_for<VPT>([&](auto i) __attribute__((always_inline)) {
+        const uint4 w = u[i];
+        mh = __builtin_elementwise_max(mh, __builtin_bit_cast(us2, w.x & 0x7fff7fffu));
+        mh = __builtin_elementwise_max(mh, __builtin_bit_cast(us2, w.y & 0x7fff7fffu));
+        mh = __builtin_elementwise_max(mh, __builtin_bit_cast(us2, w.z & 0x7fff7fffu));
+        mh = __builtin_elementwise_max(mh, __builtin_bit_cast(us2, w.w & 0x7fff7fffu));
+    });
+    const uint32_t mx = mh.x, my = mh.y;
+    const uint32_t mbits = row_umax(mx > my ? mx : my);
+    auto lo4 = [](const uint4 &w) {
+        return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                           __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+    };
+    auto hi4 = [](const uint4 &w) {
+        return make_float4(__uint_as_float(w.z << 16), __uint_as_float(w.z & 0xffff0000u),
+                           __uint_as_float(w.w << 16), __uint_as_float(w.w & 0xffff0000u));
+    };
+    uint2 *out = reinterpret_cast<uint2 *>(codes + (live ? row : 0) * cols);
     const Fp8Enc e{};
+    if (mbits < 0x7f80u) {
+        const float scale = e.scale_of(__uint_as_float(mbits << 16));
+        const float y = 1.0f / scale;
+        static_for<VPT>([&](auto i) __attribute__((always_inline)) {
+            const uint4 w = u[i];
+            const uint32_t b[8] = {w.x << 16, w.x & 0xffff0000u, w.y << 16, w.y & 0xffff0000u,
+                                   w.z << 16, w.z & 0xffff0000u, w.w << 16, w.w & 0xffff0000u};
+            float q[8];
+            uint32_t f = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = __uint_as_float(b[j]);
+                const float q0 = v * y;
+                q[j] = __builtin_fmaf(-__builtin_fmaf(q0, scale, -v), y, q0);
+                f = max(f, __builtin_amdgcn_ubfe(__float_as_uint(q[j]), 1, 22));
+            }
+            uint32_t c0, c1;
+            if (f == 0x3fffffu) {
+                c0 = f32_to_e4m3fn(q[0]) | (f32_to_e4m3fn(q[1]) << 8) | (f32_to_e4m3fn(q[2]) << 16) |
+                     (static_cast<uint32_t>(f32_to_e4m3fn(q[3])) << 24);
+                c1 = f32_to_e4m3fn(q[4]) | (f32_to_e4m3fn(q[5]) << 8) | (f32_to_e4m3fn(q[6]) << 16) |
+                     (static_cast<uint32_t>(f32_to_e4m3fn(q[7])) << 24);
+            } else {
+                c0 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(
+                    q[2], q[3], __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false), true));
+                c1 = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(
+                    q[6], q[7], __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false), true));
+            }
+            const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+            if (live && idx < nv) out[idx] = make_uint2(c0, c1);
+        });
+        if (live && t == 0) scales[row] = scale;
+        return;
+    }
+    // A NaN or an infinity in the row (uniform over the workgroup when it spans several waves):
+    // the absmax of the values (fmaxf drops NaN) and the per-value special handling.
+    float am = 0.0f;
+    static_for<VPT>([&](auto i) __attribute__((always_inline)) { am = amax4(amax4(am, lo4(u[i])), hi4(u[i])); });
+    am = __uint_as_float(row_umax(__float_as_uint(am)));  // non-negative, non-NaN: orders as u32
     const float scale = e.scale_of(am);
     const float y = 1.0f / scale;
-    uint2 *out = reinterpret_cast<uint2 *>(codes + row * cols);
+    if (!live) return;
     if (e.fast_ok(y)) {
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
-            if (idx < nv) out[idx] = make_uint2(e.enc4_y(lo[i], scale, y), e.enc4_y(hi[i], scale, y));
-        }
+        static_for<VPT>([&](auto i) __attribute__((always_inline)) {
+            const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+            if (idx < nv) out[idx] = make_uint2(e.enc4_y(lo4(u[i]), scale, y), e.enc4_y(hi4(u[i]), scale, y));
+        });
     } else {
         auto enc4 = [&](const float4 &v) {
             return e.enc(v.x, scale) | (e.enc(v.y, scale) << 8) | (e.enc(v.z, scale) << 16) | (e.enc(v.w, scale) << 24);
         };
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
-            if (idx < nv) out[idx] = make_uint2(enc4(lo[i]), enc4(hi[i]));
-        }
+        static_for<VPT>([&](auto i) __attribute__((always_inline)) {
+            const int64_t idx = t + static_cast<int64_t>(i) * TPR;
+            if (idx < nv) out[idx] = make_uint2(enc4(lo4(u[i])), enc4(hi4(u[i])));
+        });
     }
-    if (threadIdx.x == 0) scales[row] = scale;
+    if (t == 0) scales[row] = scale;
 }
 
 // Any row length / alignment: two passes over the row (the second pass hits L2/MALL).
@@ -1230,6 +1312,47 @@ int32_t castforge_hip_dequantize_nf4(const uint32_t *codes, const float *absmax,
     });
 }
 
+// Threads per row and 16-byte pieces per thread for fp8_rows_bf16x8_kernel, by row length
+// (nv8 = cols / 8 pieces, at most 8 per thread).
+#ifndef CFH_FP8_TPR
+#define CFH_FP8_TPR 0
+#endif
+void launch_fp8_rows_bf16x8(const uint16_t *src, int64_t rows, int64_t cols, uint8_t *codes, float *scales,
+                            hipStream_t st) {
+    const int64_t nv8 = cols / 8;
+    auto go = [&](auto vpt, auto tpr) {
+        constexpr int V = decltype(vpt)::value, T = decltype(tpr)::value, N = T == 64 ? 256 : T;
+        constexpr int rpw = N / T;
+        require((rows + rpw - 1) / rpw <= 0x7fffffff, "too many rows for one launch");
+        const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw)), block(N);
+        fp8_rows_bf16x8_kernel<V, T, N><<<grid, block, 0, st>>>(src, rows, cols, codes, scales);
+        check_launch("fp8_rows_bf16x8");
+    };
+    int tpr = CFH_FP8_TPR ? CFH_FP8_TPR : (nv8 <= 2048 ? 256 : 1024);
+    if (nv8 > 16 * tpr) tpr = 1024;
+    auto by_vpt = [&](auto tprc) {
+        constexpr int T = decltype(tprc)::value;
+        if (nv8 <= 1 * T) go(std::integral_constant<int, 1>{}, tprc);
+        else if (nv8 <= 2 * T) go(std::integral_constant<int, 2>{}, tprc);
+        else if (nv8 <= 3 * T) go(std::integral_constant<int, 3>{}, tprc);
+        else if (nv8 <= 4 * T) go(std::integral_constant<int, 4>{}, tprc);
+        else if (nv8 <= 6 * T) go(std::integral_constant<int, 6>{}, tprc);
+        else if (nv8 <= 8 * T) go(std::integral_constant<int, 8>{}, tprc);
+        else if (nv8 <= 11 * T) go(std::integral_constant<int, 11>{}, tprc);
+        else {
+            require(nv8 <= 16 * T, "row too long for fp8_rows_bf16x8_kernel");
+            go(std::integral_constant<int, 16>{}, tprc);
+        }
+    };
+    switch (tpr) {
+        case 64: by_vpt(std::integral_constant<int, 64>{}); break;
+        case 128: by_vpt(std::integral_constant<int, 128>{}); break;
+        case 512: by_vpt(std::integral_constant<int, 512>{}); break;
+        case 1024: by_vpt(std::integral_constant<int, 1024>{}); break;
+        default: by_vpt(std::integral_constant<int, 256>{}); break;
+    }
+}
+
 int32_t castforge_hip_quantize_fp8(const void *src, int32_t src_dtype, int64_t rows, int64_t cols,
                                    uint8_t *codes, float *scales, void *stream, char **out_error) {
     return guarded(out_error, [&] {
@@ -1246,16 +1369,8 @@ int32_t castforge_hip_quantize_fp8(const void *src, int32_t src_dtype, int64_t r
                               codes, scales, st);
         } else {
             const int64_t nv8 = cols / 8;
-            if (cols % 8 == 0 && aligned(src, 16) && aligned(codes, 8) && nv8 <= 8 * kBlock) {
-                require(rows <= 0x7fffffff, "too many rows for one launch");
-                const auto *s16 = static_cast<const uint16_t *>(src);
-                const dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
-                if (nv8 <= 1 * kBlock) fp8_rows_bf16x8_kernel<1><<<grid, block, 0, st>>>(s16, cols, codes, scales);
-                else if (nv8 <= 2 * kBlock) fp8_rows_bf16x8_kernel<2><<<grid, block, 0, st>>>(s16, cols, codes, scales);
-                else if (nv8 <= 4 * kBlock) fp8_rows_bf16x8_kernel<4><<<grid, block, 0, st>>>(s16, cols, codes, scales);
-                else if (nv8 <= 6 * kBlock) fp8_rows_bf16x8_kernel<6><<<grid, block, 0, st>>>(s16, cols, codes, scales);
-                else fp8_rows_bf16x8_kernel<8><<<grid, block, 0, st>>>(s16, cols, codes, scales);
-                check_launch("fp8_rows_bf16x8");
+            if (cols > 0 && cols % 8 == 0 && aligned(src, 16) && aligned(codes, 8) && nv8 <= 8 * 1024) {
+                launch_fp8_rows_bf16x8(static_cast<const uint16_t *>(src), rows, cols, codes, scales, st);
                 return;
             }
             const bool vec = (cols % 4 == 0) && aligned(src, 8) && aligned(codes, 4);

@@ -112,7 +112,9 @@ def test_fp8_gemm_config4_sampled_vs_oracle(cuda, m, n, k, exact):
                   sw.cpu().numpy()[cols], exact, f"config4 {m}x{n}x{k}")
     if not exact:
         print(f"fp8 MFMA, config4 {m}x{n}x{k}: {nbad} / {ys.size} sampled outputs past the plain bound")
-        assert nbad <= ys.size // 100
+        # the full-size rate is 0.23-0.27 % (test_fp8_gemm_baseline_shapes); a 9216-output
+        # sample at that rate has a mean of 25 and a standard deviation of 5
+        assert nbad <= ys.size * 5 // 1000
 
 
 @pytest.mark.parametrize("exact", [True, False])
@@ -138,7 +140,8 @@ def test_fp8_gemm_baseline_shapes(cuda, m, n, k, exact):
             rel = float(((y.double() - ref) ** 2).mean().sqrt() / (ref ** 2).mean().sqrt())
             print(f"fp8 MFMA, config4 {m}x{n}x{k} {out}: {nbad} / {ref.numel()} outputs past the plain "
                   f"bound, max err {float(err.max()):.3e}, relative RMS {rel:.2e}")
-            assert rel <= 2e-3 and nbad <= ref.numel() // 100
+            # measured: 0.23 % (n = 11008) and 0.27 % (n = 4096) of all outputs on these inputs
+            assert rel <= 2e-3 and nbad <= ref.numel() * 3 // 1000
 
 
 @pytest.mark.parametrize("exact", [True, False])

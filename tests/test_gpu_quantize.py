@@ -254,7 +254,7 @@ def test_fp8_rows_boundaries_many_scale_decades(cuda):
 
 
 @pytest.mark.parametrize("r,c", [(16, 512), (4096, 4096 // 8), (3, 11), (5, 4096), (7, 11008), (6, 520),
-                                 (2, 12288), (3, 12296), (4097, 64)])
+                                 (2, 12288), (3, 12296), (4097, 64), (2, 16384), (2, 16392)])
 def test_fp8_rows_bf16_bit_exact(cuda, r, c):
     x = synth.activations_bf16(42, 1, r, c)
     c_ref, s_ref = O.quantize_fp8_rows(x)
@@ -268,13 +268,23 @@ def test_fp8_rows_bf16_bit_exact(cuda, r, c):
 
 def test_fp8_rows_bf16_special_values(cuda):
     """bf16 rows with NaN, Inf, signed zeros, subnormals, values at the saturation edges and
-    an all-zero row, through the one-wave-per-row kernel (cols % 8 == 0)."""
-    x = synth.activations_bf16(43, 1, 6, 1024).copy()
+    an all-zero row (cols % 8 == 0).  Rows 0 and 2 hold a NaN or an infinity (the kernel's
+    general path); rows 4..7 stay finite (its fast path) with signed zeros, bf16 subnormals and,
+    under an absmax of 3e38 or 1.7e38, negative values whose quotient underflows to -0 (code
+    0x80) next to positive ones that underflow to +0."""
+    x = synth.activations_bf16(43, 1, 8, 1024).copy()
     f = np.array([np.nan, np.inf, -np.inf, -0.0, 0.0, 1e-40, -1e-40, 448.0, -464.0, 3e38], np.float32)
     x[0, :f.size] = O.f32_to_bf16_bits(f)
     x[1, :] = O.f32_to_bf16_bits(np.zeros(1024, np.float32))
     x[2, 5] = O.f32_to_bf16_bits(np.array([np.inf], np.float32))[0]
     x[3, 7] = O.f32_to_bf16_bits(np.array([1e-38], np.float32))[0]
+    tiny = np.array([-0.0, 0.0, -1e-40, 1e-40, -1e-30, 1e-30, -1e-38, -3e-39, -2.0, 5.0], np.float32)
+    x[4, :tiny.size] = O.f32_to_bf16_bits(tiny)
+    x[5, :tiny.size] = O.f32_to_bf16_bits(tiny)
+    x[5, 100] = O.f32_to_bf16_bits(np.array([3e38], np.float32))[0]
+    x[6, :] = O.f32_to_bf16_bits(np.resize(tiny, 1024))
+    x[6, 1023] = O.f32_to_bf16_bits(np.array([-1.7e38], np.float32))[0]
+    x[7, :] = O.f32_to_bf16_bits(np.resize(tiny[:4], 1024))
     c_ref, s_ref = O.quantize_fp8_rows(x)
     codes, scales = ops.quantize_fp8(torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(cuda))
     assert np.array_equal(scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
