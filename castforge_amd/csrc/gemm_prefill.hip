@@ -23,6 +23,11 @@
 //   at every group start was measured and dropped: the rounding of the running sum put
 //   near-zero outputs of cancellation-heavy rows further from the exact value than the
 //   evaluator's own f32 sum.)
+//   Range of that kernel: its partials hold sum x * q with |q| <= 127 (INT4: 15, Q4_0: 8)
+//   before any scale, so they reach |x| * 127 * K.  It is exact-range for |x| <= 2^100 and
+//   K <= 2^20 (2^127 < f32 max); past that a partial can overflow to +-inf where the
+//   evaluator's x * (q * s) stays finite.  The two-term kernel (CASTFORGE_PREFILL_I4=0)
+//   keeps the scale inside the weight and has no such bound.
 //
 // Design:
 //   * workgroup tile BN (n) x BM (m) with 4 waves; W is the MFMA row operand, so each lane

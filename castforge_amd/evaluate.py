@@ -8,7 +8,10 @@ libcastforge_hip.so.
                              evaluates to its dequantized f32 values
   stablehlo.uniform_dequantize  the same dequantization (eval.rs:324-343)
   stablehlo.convert          a copy (eval.rs:674-676)
-  stablehlo.dot_general      eval_matmul_2d, bit-identical on the GPU (castforge_hip_matmul_f32)
+  stablehlo.dot_general      eval_matmul_2d, bit-identical on the GPU (castforge_hip_matmul_f32);
+                             with batching dimensions or an operand of rank > 2, eval_dot_general's
+                             flat [batch, m, k] x [batch, (n, k) | (k, n)] form (eval.rs:1509-1604)
+                             as one such matmul per batch
   castforge.fused_qmatmul    the dequant-fused GEMV / GEMM kernels, then the epilogue
                              (eval.rs:1145-1179)
   castforge.fused_matmul_epilogue  f32 matmul + epilogue
@@ -87,6 +90,63 @@ class _Evaluator:
         a = self._act(_as2d(self.env[lhs], self.m.values[lhs].ty.shape).contiguous())
         b = rhs_vals.reshape(rhs_shape).contiguous()
         return ops.matmul_f32(a, b, packed)
+
+    def _dot_general(self, op, ty) -> torch.Tensor:
+        """eval.rs:934-952 + eval_dot_general (eval.rs:1509-1604).
+
+        Without batching dimensions and with both operands of rank <= 2 this is
+        eval_matmul_2d, packed when the rhs is 2-D and contracts its last dimension.  Otherwise
+        the reference reads both operands flat: batch = product of the lhs batching dimensions,
+        k = product of the lhs contracting dimensions, m = |lhs| / (batch k), n = |rhs| / (batch k);
+        lhs as [batch, m, k] and rhs as [batch, n, k] when its last contracting dimension is its
+        last dimension, else [batch, k, n]; out [batch, m, n], each output an f32 sum over kk
+        in order -- per batch exactly eval_matmul_2d's loop, which castforge_hip_matmul_f32
+        reproduces bit for bit.  Operands that do not factor that way (the reference would read
+        zeros past their ends) are rejected."""
+        lhs, rhs = op.operands[0], op.operands[1]
+        ls, rs = tuple(self.m.values[lhs].ty.shape), tuple(self.m.values[rhs].ty.shape)
+        at = op.attributes
+        lb = list(at.get("lhs_batching_dimensions") or [])
+        rb = list(at.get("rhs_batching_dimensions") or [])
+        lc = list(at.get("lhs_contracting_dimensions") or [])
+        rc = list(at.get("rhs_contracting_dimensions") or [])
+        if not lb and not rb and len(ls) <= 2 and len(rs) <= 2:
+            if "rhs_contracting_dimensions" in at:
+                packed = len(rs) == 2 and bool(rc) and rc[-1] == len(rs) - 1
+            else:
+                packed = bool(at.get("packed_rhs", False))
+            return self._matmul(lhs, self.env[rhs], rs, packed).reshape(ty.shape)
+
+        def prod(v):
+            r = 1
+            for d in v:
+                r *= int(d)
+            return r
+
+        def dims_of(shape, axes, what):
+            for ax in axes:
+                if not 0 <= int(ax) < len(shape):
+                    raise ValueError(f"dot_general: {what} dimension {ax} is outside an operand of rank {len(shape)}")
+            return [int(shape[int(ax)]) for ax in axes]
+
+        batch = max(prod(dims_of(ls, lb, "lhs batching")), 1)
+        k = max(prod(dims_of(ls, lc, "lhs contracting")), 1)
+        dims_of(rs, rc, "rhs contracting")
+        lt, rt = max(prod(ls), 1), max(prod(rs), 1)
+        mm = max(lt // max(batch * k, 1), 1)
+        nn = max(rt // max(batch * k, 1), 1)
+        if lt != batch * mm * k or rt != batch * k * nn or prod(ty.shape) != batch * mm * nn:
+            raise ValueError(
+                f"dot_general: lhs {ls} and rhs {rs} (batching {lb} x {rb}, contracting {lc} x {rc}) do not "
+                f"factor as [batch={batch}, m, k={k}] x [batch, k, n] with a result of {batch * mm * nn} elements "
+                f"(result type {tuple(ty.shape)}); the reference evaluator would read zeros past the operands")
+        contract_last = bool(rc) and rc[-1] + 1 == len(rs)
+        a = self._act(self.env[lhs].reshape(batch, mm, k).contiguous())
+        b = self.env[rhs].reshape((batch, nn, k) if contract_last else (batch, k, nn)).contiguous()
+        out = torch.empty((batch, mm, nn), dtype=torch.float32, device=a.device)
+        for i in range(batch):
+            out[i] = ops.matmul_f32(a[i], b[i], contract_last)
+        return out.reshape(ty.shape)
 
     def _fused(self, op) -> torch.Tensor:
         lhs, wq = op.operands[0], op.operands[1]
@@ -173,9 +233,7 @@ class _Evaluator:
             elif op.is_op("stablehlo", "convert"):
                 self.env[res] = self.env[op.operands[0]]
             elif op.is_op("stablehlo", "dot_general"):
-                rhs = op.operands[1]
-                self.env[res] = self._matmul(op.operands[0], self.env[rhs], m.values[rhs].ty.shape,
-                                             bool(op.attributes.get("packed_rhs", False))).reshape(ty.shape)
+                self.env[res] = self._dot_general(op, ty)
             elif op.is_op("stablehlo", "composite") and op.attributes.get("name") == "castforge.fused_qmatmul":
                 self.env[res] = self._epilogue(op, self._fused(op)).reshape(ty.shape)
             elif op.is_op("stablehlo", "composite") and op.attributes.get("name") == "castforge.static_quantize":

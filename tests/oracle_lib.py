@@ -239,6 +239,21 @@ def matmul_2d(a: np.ndarray, b: np.ndarray, packed_rhs: bool) -> np.ndarray:
     return out
 
 
+def dot_general_flat(a: np.ndarray, b: np.ndarray, batch: int, k: int, rhs_contract_last: bool) -> np.ndarray:
+    """eval_dot_general (eval.rs:1509-1604) past its 2-D case: both operands read flat, m and n
+    from their element counts, lhs as [batch, m, k], rhs as [batch, n, k] (rhs_contract_last)
+    or [batch, k, n]; each batch is eval_matmul_2d's loop (orc_matmul_2d).  Operands that do not
+    factor that way are refused here (the reference reads zeros past them)."""
+    a = np.ascontiguousarray(a, np.float32).reshape(-1)
+    b = np.ascontiguousarray(b, np.float32).reshape(-1)
+    m, n = a.size // (batch * k), b.size // (batch * k)
+    if a.size != batch * m * k or b.size != batch * k * n:
+        raise ValueError("operands do not factor as [batch, m, k] x [batch, k, n]")
+    a3 = a.reshape(batch, m, k)
+    b3 = b.reshape((batch, n, k) if rhs_contract_last else (batch, k, n))
+    return np.stack([matmul_2d(a3[i], b3[i], rhs_contract_last) for i in range(batch)])
+
+
 def gemm_w8a16(x_bf16: np.ndarray, codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
     m, k = x_bf16.shape
     n = codes.shape[0]

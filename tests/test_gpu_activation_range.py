@@ -41,19 +41,24 @@ def _xdev(xb, dev):
     return torch.from_numpy(np.ascontiguousarray(xb).view(np.int16)).view(torch.bfloat16).to(dev)
 
 
-def _weight(seed, n, k, halves):
+def _weight(seed, n, k, halves, positive=False):
     rng = np.random.default_rng(seed)
     if halves:
         wh = (rng.standard_normal((n, k // 2)) * 0.02).astype(np.float32)
         return np.concatenate([wh, wh], axis=1)
-    return (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    return np.abs(w) if positive else w
 
 
-def _gguf_raw(ty, seed, n, k, halves):
+def _gguf_raw(ty, seed, n, k, halves, positive=False):
     rng = np.random.default_rng(seed)
     bpr = k // 32
     raw = rng.integers(0, 256, (n, bpr, BB[ty]), dtype=np.uint8)
+    if positive:  # every code at its largest q - 8 (Q4_0: 7) or q (Q8_0: 127), d > 0
+        raw[:] = 0xFF if ty == Q4_0 else 0x7F
     d = (rng.standard_normal((n, bpr)) * 0.002).astype(np.float16)
+    if positive:
+        d = np.abs(d)
     raw[:, :, 0:2] = d.view(np.uint8).reshape(n, bpr, 2)
     if halves:
         raw[:, bpr // 2:] = raw[:, : bpr // 2]
@@ -63,11 +68,11 @@ def _gguf_raw(ty, seed, n, k, halves):
 class Case:
     """One packed weight: run(x) on the GPU, the oracle's f32 result and the exact f64 one."""
 
-    def __init__(self, fmt, n, k, dev, seed=11, halves=False):
+    def __init__(self, fmt, n, k, dev, seed=11, halves=False, positive=False):
         self.fmt, self.n, self.k = fmt, n, k
         if fmt.startswith("int4"):
             g = int(fmt.split("_")[1][1:])
-            w = _weight(seed, n, k, halves)
+            w = _weight(seed, n, k, halves, positive)
             c, s, z = O.quantize_int4g(w, g)
             self.p = ops.Int4Packed(torch.from_numpy(c.view(np.int32)).to(dev),
                                     torch.from_numpy(s.view(np.float16)).to(dev),
@@ -79,7 +84,7 @@ class Case:
             self.oracle = lambda xb: O.gemm_w4a16(xb, c, s, z, n, k, g)
             self.deq = O.dequantize_int4g(c, s, z, n, k, g)
         elif fmt.startswith("int8"):
-            w = _weight(seed, n, k, halves)
+            w = _weight(seed, n, k, halves, positive)
             c, s = O.quantize_int8_rows(w)
             cd, sd = torch.from_numpy(c).to(dev), torch.from_numpy(s).to(dev)
             if fmt.endswith("_one"):  # the one-MFMA prefill kernel, forced at every M > 64
@@ -97,7 +102,7 @@ class Case:
             self.deq = O.dequantize_nf4(c, am, n, k, 64)
         else:
             ty = Q4_0 if fmt.startswith("q4_0") else Q8_0
-            raw = _gguf_raw(ty, seed, n, k, halves)
+            raw = _gguf_raw(ty, seed, n, k, halves, positive)
             self.p = ops.gguf_repack(ty, torch.from_numpy(raw).to(dev), n, k)
             if fmt.endswith("_one"):  # the one-MFMA prefill kernel, forced at every M > 64
                 self.run = lambda x, out: _one_mfma(lambda: ops.gemm_gguf(x, self.p, out))
@@ -208,3 +213,26 @@ def test_nonfinite_x_gives_nonfinite_rows(cuda, fmt, m):
     x[:, 5] = np.inf
     y = c.run(_xdev(O.f32_to_bf16_bits(x), cuda), torch.float32)
     assert not torch.isfinite(y).any()
+
+
+@pytest.mark.parametrize("fmt", [f for f in FORMATS if f.endswith("_one")])
+def test_one_mfma_prefill_at_activation_bound(cuda, fmt):
+    """The one-MFMA prefill kernel feeds the unscaled integer (q - z), q - 8 or q and scales
+    the f32 partial afterwards, so its partials reach |x| * 127 * K.  Its documented range is
+    |x| <= 2^100 with K <= 2^20 (2^100 * 2^7 * 2^20 = 2^127 < f32 max).  At that bound, with
+    every activation of one sign and every weight positive (the largest partials), each output
+    is finite and meets the plain bound against the oracle."""
+    n, k, m = 64, 2048, 100
+    rng = np.random.default_rng(15)
+    c = Case(fmt, n, k, cuda, seed=15)
+    c_pos = Case(fmt, n, k, cuda, seed=15, positive=True)
+    x = (np.float32(2.0 ** 100) * rng.uniform(0.5, 1.0, (m, k))).astype(np.float32)
+    x[m // 2:] *= np.float32(-1.0)
+    x[:, 0] = np.float32(2.0 ** 100)  # the bound itself
+    xb = O.f32_to_bf16_bits(x)
+    assert np.abs(O.bf16_bits_to_f32(xb)).max() == np.float32(2.0 ** 100)
+    for case in (c, c_pos):
+        y = case.run(_xdev(xb, cuda), torch.float32).cpu().numpy()
+        ref = case.oracle(xb)
+        assert np.all(np.isfinite(ref)) and np.all(np.isfinite(y))
+        assert np.all(np.abs(y - ref) <= ATOL + RTOL * np.abs(ref))

@@ -351,6 +351,27 @@ def test_gemm_w4a16_oracle_vs_float64():
     np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-6)
 
 
+def test_dot_general_flat_oracle_vs_float64():
+    """The batched / rank-3 form of eval_dot_general (eval.rs:1509-1604): every batch against a
+    float64 product of the same slices, both rhs layouts; batch = 1 is eval_matmul_2d itself,
+    and a batch-swapped rhs (a plausible indexing slip) is caught."""
+    rng = np.random.default_rng(12)
+    bt, m, k, n = 3, 5, 40, 7
+    a = rng.standard_normal((bt, m, k)).astype(np.float32)
+    bkn = rng.standard_normal((bt, k, n)).astype(np.float32)
+    bnk = np.ascontiguousarray(bkn.transpose(0, 2, 1))
+    ref = np.einsum("bmk,bkn->bmn", a.astype(np.float64), bkn.astype(np.float64))
+    bound = 1e-6 * np.einsum("bmk,bkn->bmn", np.abs(a).astype(np.float64), np.abs(bkn).astype(np.float64))
+    for y in (O.dot_general_flat(a, bkn, bt, k, False), O.dot_general_flat(a, bnk, bt, k, True)):
+        assert y.shape == (bt, m, n)
+        assert np.all(np.abs(y - ref) <= bound)
+    assert np.array_equal(O.dot_general_flat(a[:1], bkn[:1], 1, k, False)[0], O.matmul_2d(a[0], bkn[0], False))
+    wrong = O.dot_general_flat(a, bkn[::-1].copy(), bt, k, False)
+    assert not np.all(np.abs(wrong - ref) <= bound)
+    with pytest.raises(ValueError):
+        O.dot_general_flat(a, bkn[:, :, :3].reshape(-1)[:-1], bt, k, False)
+
+
 def test_epilogues():
     out = np.array([1.0, -2.0, 0.5], np.float32)
     bias = np.array([0.5], np.float32)
