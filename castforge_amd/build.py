@@ -59,7 +59,8 @@ def build(verbose: bool = False) -> Path:
             if warn:
                 print(f"[{obj.name}] {warn}", file=sys.stderr)
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+    # --no-undefined: a kernel whose host stub the compiler failed to emit fails here, not at load
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", str(tmp),
            *[str(o) for o, _ in results]]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

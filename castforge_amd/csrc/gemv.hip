@@ -24,6 +24,8 @@
 //     exact (q - z) / q / NF4 hi+lo operands;
 //   * problems with the longest K are dispatched first so no long workgroup forms a tail.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 #include "../../include/castforge_hip.h"
 #include "cfh_common.hpp"
@@ -1612,6 +1614,16 @@ void common_checks(const void *x, int64_t m, int64_t n, int64_t k, const void *c
 
 }  // namespace
 
+// NF4 on one bf16 MFMA pair per product (gemm_nf4.hip), for M > 16.
+bool nf4_mfma_ok(const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t block, const void *codes);
+void nf4_mfma_launch(const cfh_nf4_problem_t *ps, int count, int64_t m, int y_bf16, hipStream_t st);
+
+// CASTFORGE_NF4_MFMA=0 keeps NF4 at M > 16 on the skinny / prefill kernels (for comparison).
+bool nf4_mfma_enabled() {
+    const char *e = std::getenv("CASTFORGE_NF4_MFMA");
+    return !(e && std::strcmp(e, "0") == 0);
+}
+
 // Prefill MFMA kernel (gemm_prefill.hip); false when the shape does not fit it.
 bool prefill_try(int fmt, const uint16_t *x, int64_t m, int64_t n, int64_t k, int64_t group,
                  const void *codes, const void *scales, const uint32_t *zeros, int per_row, void *y,
@@ -1695,6 +1707,11 @@ int32_t castforge_hip_gemv_nf4(const uint16_t *x, int64_t m, int64_t n, int64_t 
         require(k == 0 || absmax, "absmax must not be NULL");
         hipStream_t st = static_cast<hipStream_t>(stream);
         const int yb = y_dtype == CFH_DTYPE_BF16;
+        if (nf4_mfma_enabled() && nf4_mfma_ok(x, m, n, k, block, codes)) {
+            const cfh_nf4_problem_t p{x, codes, absmax, y, n, k, block};
+            nf4_mfma_launch(&p, 1, m, yb, st);
+            return;
+        }
         if (!gemv_try_skinny(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st) &&
             !prefill_try(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st))
             gemv_generic(FMT_NF4, x, m, n, k, block, codes, absmax, nullptr, 1, y, yb, st);
@@ -1822,20 +1839,25 @@ int32_t castforge_hip_gemv_nf4_batched(const cfh_nf4_problem_t *problems, int32_
         require(m >= 1 && m <= 64, "batched GEMV requires 1 <= m <= 64");
         require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
         Problem ps[kMaxProblems];
+        cfh_nf4_problem_t mf[kMaxProblems];
         int used = 0;
+        bool mfma = nf4_mfma_enabled();
         for (int i = 0; i < count; ++i) {
             const cfh_nf4_problem_t &q = problems[i];
             common_checks(q.x, m, q.n, q.k, q.codes, q.y, y_dtype);
             require(q.block == problems[0].block, "batched problems must share the block size");
             if (q.n == 0) continue;
             require(q.k > 0 && q.absmax, "problem buffers must not be NULL");
+            mfma = mfma && nf4_mfma_ok(q.x, m, q.n, q.k, q.block, q.codes);
+            mf[used] = q;
             Problem p{q.x, q.codes, q.absmax, nullptr, q.y, q.n, q.k, static_cast<int32_t>(q.block), 1, 0, 0};
             require(q.block >= 32 && skinny_ok(FMT_NF4, p, m),
                     "batched GEMV needs block 32, 64 or a power-of-two multiple of 128, k a multiple "
                     "of the chunk (block 32: 32, 64: 64, else 128) and 16-byte aligned x/codes");
             ps[used++] = p;
         }
-        if (used) launch_skinny(FMT_NF4, ps, used, m, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
+        if (used && mfma) nf4_mfma_launch(mf, used, m, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
+        else if (used) launch_skinny(FMT_NF4, ps, used, m, y_dtype == CFH_DTYPE_BF16, static_cast<hipStream_t>(stream));
     });
 }
 

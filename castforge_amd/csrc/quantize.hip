@@ -152,7 +152,52 @@ struct SymEnc {
         return enc_y(v.x, scale, y) | (enc_y(v.y, scale, y) << 8) | (enc_y(v.z, scale, y) << 16) |
                (enc_y(v.w, scale, y) << 24);
     }
+    static constexpr bool finite_path() { return false; }
 };
+
+// Low bytes of four i32 -> one word (byte i = value i).
+__device__ __forceinline__ uint32_t pack_low_bytes(int32_t a, int32_t b, int32_t c, int32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(static_cast<uint32_t>(b), static_cast<uint32_t>(a), 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(static_cast<uint32_t>(d), static_cast<uint32_t>(c), 0x04000c0cu);
+    return ab | cd;
+}
+
+// SymEnc with the rounding mode fixed at compile time, and a path for rows that hold neither
+// NaN nor an infinity (rows_quant_reg_kernel checks that from the bit patterns).  There
+// amax is finite, so |v * y| <= qmax (1 + 2^-22): div_by_scale's clamp never acts, the quotient
+// is never NaN and its rounding already lies in [qmin, qmax] (qmin <= -qmax - 1), so the code
+// is the rounded quotient itself.
+template <int MODE>
+struct SymEncM : SymEnc {
+    __device__ __forceinline__ float rnd(float q) const {
+        return MODE == CFH_ROUND_HALF_EVEN ? rintf(q) : roundf(q);
+    }
+    __device__ __forceinline__ uint32_t enc(float v, float scale) const {
+        return quant_sym_byte(v, scale, qmin, qmax, MODE);
+    }
+    __device__ __forceinline__ uint32_t enc_y(float v, float scale, float y) const {
+        return quant_sym_byte_y(v, scale, y, qmin, qmax, MODE);
+    }
+    __device__ __forceinline__ uint32_t enc4_y(float4 v, float scale, float y) const {
+        return enc_y(v.x, scale, y) | (enc_y(v.y, scale, y) << 8) | (enc_y(v.z, scale, y) << 16) |
+               (enc_y(v.w, scale, y) << 24);
+    }
+    static constexpr bool finite_path() { return true; }
+    __device__ __forceinline__ uint32_t enc4_finite(float4 v, float scale, float y) const {
+        auto q = [&](float x) {
+            const float q0 = x * y;
+            return static_cast<int32_t>(rnd(__builtin_fmaf(__builtin_fmaf(-q0, scale, x), y, q0)));
+        };
+        return pack_low_bytes(q(v.x), q(v.y), q(v.z), q(v.w));
+    }
+};
+
+// Calls f with e as the SymEncM of its rounding mode.
+template <class F>
+void with_round_mode(const SymEnc &e, F &&f) {
+    if (e.mode == CFH_ROUND_HALF_EVEN) f(SymEncM<CFH_ROUND_HALF_EVEN>{e});
+    else f(SymEncM<CFH_ROUND_HALF_AWAY>{e});
+}
 
 // E4M3 bytes of four values (byte i = value i).  gfx950's v_cvt_pk_fp8_f32 (OCP E4M3FN, round
 // to nearest even) gives f32_to_e4m3fn's byte for every f32 except NaN (the reference's 0x7F
@@ -197,6 +242,29 @@ struct Fp8Enc {
     __device__ __forceinline__ uint32_t enc4_y(float4 v, float scale, float y) const {
         return e4m3x4(quot(v.x, scale, y), quot(v.y, scale, y), quot(v.z, scale, y), quot(v.w, scale, y));
     }
+    // Rows without NaN or infinity (amax finite): |v * y| <= 448.0001, so no clamp is needed,
+    // the quotient is never NaN and stays below the conversion's NaN range (464), and only
+    // the log2-quirk mantissas (0x7ffffe / 0x7fffff) need the exact encoder.  The quotient
+    // q0 - (q0 * scale - v) * y is div_by_scale's with the residual's sign flipped: the same
+    // magnitudes, and the sign of a zero quotient (v = -0, or a negative quotient that
+    // underflows) kept without the OR that quot() needs.
+    static constexpr bool finite_path() { return true; }
+    __device__ __forceinline__ uint32_t enc4_finite(float4 v, float scale, float y) const {
+        const float x[4] = {v.x, v.y, v.z, v.w};
+        float q[4];
+        uint32_t f = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float q0 = x[j] * y;
+            q[j] = __builtin_fmaf(-__builtin_fmaf(q0, scale, -x[j]), y, q0);
+            f = max(f, __builtin_amdgcn_ubfe(__float_as_uint(q[j]), 1, 22));
+        }
+        if (f == 0x3fffffu)
+            return f32_to_e4m3fn(q[0]) | (f32_to_e4m3fn(q[1]) << 8) | (f32_to_e4m3fn(q[2]) << 16) |
+                   (static_cast<uint32_t>(f32_to_e4m3fn(q[3])) << 24);
+        return static_cast<uint32_t>(
+            __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false), true));
+    }
 };
 
 __device__ __forceinline__ float amax4(float a, float4 v) {
@@ -220,20 +288,49 @@ __global__ __launch_bounds__(kBlock) void rows_quant_reg_kernel(RowSets<typename
     float *__restrict__ scales = static_cast<float *>(sets.scales[set]);
     const int64_t nv = cols >> 2;
     const int64_t base = row * nv;
+    // Threads past the row's end load its last 4 values again: an index clamp rather than a
+    // branch, since a load under a divergent branch gets a wait of its own and the loads would
+    // run one after another.  A repeated element leaves the absmax unchanged; those threads
+    // store nothing.
     float4 v[VPT];
-    float am = 0.0f;
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
-        if (idx < nv) {
-            v[i] = src.load4(base + idx);
-            am = amax4(am, v[i]);
+    for (int i = 0; i < VPT; ++i) v[i] = src.load4(base + min(threadIdx.x + static_cast<int64_t>(i) * kBlock, nv - 1));
+    uint32_t *out = reinterpret_cast<uint32_t *>(codes + row * cols);
+    if constexpr (Enc::finite_path()) {
+        // the largest magnitude bit pattern: below 0x7f800000 the row is finite and it is the
+        // absmax itself (non-NaN floats order like their magnitude bits)
+        uint32_t mb = 0;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const uint32_t a = __float_as_uint(v[i].x) & 0x7fffffffu, b = __float_as_uint(v[i].y) & 0x7fffffffu;
+            const uint32_t c = __float_as_uint(v[i].z) & 0x7fffffffu, d = __float_as_uint(v[i].w) & 0x7fffffffu;
+            mb = max(max(mb, max(a, b)), max(c, d));
+        }
+        mb = wave_umax<64>(mb);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) reinterpret_cast<uint32_t *>(red)[threadIdx.x >> 6] = mb;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) mb = max(mb, reinterpret_cast<const uint32_t *>(red)[w]);
+        if (mb < 0x7f800000u) {  // uniform over the workgroup (one row)
+            const float scale = e.scale_of(__uint_as_float(mb));
+            const float y = 1.0f / scale;
+#pragma unroll
+            for (int i = 0; i < VPT; ++i) {
+                const int64_t idx = threadIdx.x + static_cast<int64_t>(i) * kBlock;
+                const uint32_t w = e.enc4_finite(v[i], scale, y);
+                if (idx < nv) out[idx] = w;
+            }
+            if (threadIdx.x == 0) scales[row] = scale;
+            return;
         }
     }
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) am = amax4(am, v[i]);
     am = block_max(am, red);
     const float scale = e.scale_of(am);
     const float y = 1.0f / scale;
-    uint32_t *out = reinterpret_cast<uint32_t *>(codes + row * cols);
     if (e.fast_ok(y)) {
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
@@ -408,7 +505,7 @@ void launch_rows_quant_sets(const RowSets<typename Src::elem> &sets, int64_t row
     if (rows == 0) return;
     require(rows <= 0x7fffffff, "too many rows for one launch");
     const int64_t nv = cols / 4;
-    require(nv <= 16 * kBlock, "row too long for the register kernel");
+    require(nv >= 1 && nv <= 16 * kBlock, "row length outside the register kernel's range");
     dim3 grid(static_cast<unsigned>(rows)), block(kBlock);
     if (nv <= 1 * kBlock)
         rows_quant_reg_kernel<1, Src><<<grid, block, 0, st>>>(sets, cols, e);
@@ -430,7 +527,7 @@ void launch_rows_quant(Src src, bool vec_ok, int64_t rows, int64_t cols, Enc e, 
                        float *scales, hipStream_t st) {
     if (rows == 0) return;
     require(rows <= 0x7fffffff, "too many rows for one launch");
-    if (vec_ok && cols / 4 <= 16 * kBlock) {
+    if (vec_ok && cols >= 4 && cols / 4 <= 16 * kBlock) {
         launch_rows_quant_sets<Src>(one_set(src.p, nullptr, codes, scales, nullptr, rows), rows, cols, e, st);
         return;
     }
@@ -739,48 +836,49 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
     const bool task_ok = zw < ZW;
     const uint32_t w0 = zw * (2 * T) + 2 * t;  // this thread's first code word
     const bool ok0 = task_ok && w0 < KW, ok1 = task_ok && w0 + 1 < KW;
-    // the thread's 16 AWQ pre-scales (1 outside the row): loaded once for R > 1, after the
-    // row's own loads for R = 1 so that they are not waited for before those are issued
+    // the thread's 16 AWQ pre-scales (1 outside the row): loaded once, after the rows' own
+    // loads, so that those are all issued before anything waits
     float sc[16];
     auto load_scales = [&]() {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sc[i] = 1.0f;
-#pragma unroll
         for (int h = 0; h < 2; ++h) {
-            if (h == 0 ? ok0 : ok1) {
-                const float4 *q = reinterpret_cast<const float4 *>(in_scale + (w0 + h) * 8);
-                const float4 c = q[0], d = q[1];
-                float *ss = sc + 8 * h;
-                ss[0] = c.x; ss[1] = c.y; ss[2] = c.z; ss[3] = c.w;
-                ss[4] = d.x; ss[5] = d.y; ss[6] = d.z; ss[7] = d.w;
-            }
+            const bool okh = h == 0 ? ok0 : ok1;
+            const float4 *q = reinterpret_cast<const float4 *>(in_scale + (okh ? w0 + h : 0u) * 8);
+            const float4 c = q[0], d = q[1];
+            float *ss = sc + 8 * h;
+            ss[0] = okh ? c.x : 1.0f; ss[1] = okh ? c.y : 1.0f; ss[2] = okh ? c.z : 1.0f; ss[3] = okh ? c.w : 1.0f;
+            ss[4] = okh ? d.x : 1.0f; ss[5] = okh ? d.y : 1.0f; ss[6] = okh ? d.z : 1.0f; ss[7] = okh ? d.w : 1.0f;
         }
     };
-    if constexpr (R > 1) {
-        if (in_scale) load_scales();
+    // every row's values are loaded before the first row is processed, so the R rows' loads
+    // are in flight together (the loop below stores between rows, and loads are not moved
+    // across those stores)
+    float xr[R][16];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+        const float *rsrc = src + (row0 + rr) * cols;
+        // a part past the row's end reads the row's first word and is zeroed: unconditional
+        // loads (a load under a divergent branch gets a wait of its own before the next one
+        // is issued); every launch has cols >= 8, so word 0 exists
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool okh = h == 0 ? ok0 : ok1;
+            const float4 *p = reinterpret_cast<const float4 *>(rsrc + (okh ? w0 + h : 0u) * 8);
+            const float4 a = p[0], b = p[1];
+            float *xx = xr[rr] + 8 * h;
+            xx[0] = okh ? a.x : 0.0f; xx[1] = okh ? a.y : 0.0f; xx[2] = okh ? a.z : 0.0f; xx[3] = okh ? a.w : 0.0f;
+            xx[4] = okh ? b.x : 0.0f; xx[5] = okh ? b.y : 0.0f; xx[6] = okh ? b.z : 0.0f; xx[7] = okh ? b.w : 0.0f;
+        }
     }
+    if (in_scale) load_scales();  // uniform; after the rows' loads, which it would otherwise wait for
 #pragma unroll
     for (int rr = 0; rr < R; ++rr) {
         const int64_t row = row0 + rr;
-        const float *rsrc = src + row * cols;
         uint32_t *rcodes = codes + row * KW;
         uint16_t *rscales = scales + row * GP;
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) x[i] = 0.0f;
+        float (&x)[16] = xr[rr];
         float mx = -INFINITY, mn = INFINITY;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (h == 0 ? ok0 : ok1) {
-                const float4 *p = reinterpret_cast<const float4 *>(rsrc + (w0 + h) * 8);
-                const float4 a = p[0], b = p[1];
-                float *xx = x + 8 * h;
-                xx[0] = a.x; xx[1] = a.y; xx[2] = a.z; xx[3] = a.w;
-                xx[4] = b.x; xx[5] = b.y; xx[6] = b.z; xx[7] = b.w;
-            }
-        }
         if (in_scale) {  // uniform
-            if constexpr (R == 1) load_scales();
 #pragma unroll
             for (int i = 0; i < 16; ++i) x[i] *= sc[i];  // 0 * 1 outside the row
         }
@@ -999,8 +1097,9 @@ int32_t castforge_hip_quantize_int8(const float *src, int64_t rows, int64_t cols
         hipStream_t st = static_cast<hipStream_t>(stream);
         if (granularity == CFH_GRAN_CHANNEL) {
             const bool vec = (cols % 4 == 0) && aligned(src, 16) && aligned(codes, 4);
-            launch_rows_quant(F32x4Src{src}, vec, rows, cols, e,
-                              reinterpret_cast<uint8_t *>(codes), scales, st);
+            with_round_mode(e, [&](auto em) {
+                launch_rows_quant(F32x4Src{src}, vec, rows, cols, em, reinterpret_cast<uint8_t *>(codes), scales, st);
+            });
             return;
         }
         uint32_t *acc = reinterpret_cast<uint32_t *>(scales);
@@ -1122,7 +1221,9 @@ void quantize_int4g_impl(const float *src, const float *in_scale, int64_t rows, 
 void quantize_int8_rows(const float *src, int64_t rows, int64_t cols, SymEnc e, int8_t *codes,
                         float *scales, hipStream_t st) {
     const bool vec = (cols % 4 == 0) && aligned(src, 16) && aligned(codes, 4);
-    launch_rows_quant(F32x4Src{src}, vec, rows, cols, e, reinterpret_cast<uint8_t *>(codes), scales, st);
+    with_round_mode(e, [&](auto em) {
+        launch_rows_quant(F32x4Src{src}, vec, rows, cols, em, reinterpret_cast<uint8_t *>(codes), scales, st);
+    });
 }
 
 // Batched quantize: the problems are grouped by column count (in order of first appearance);
@@ -1159,7 +1260,7 @@ void quantize_batched(const cfh_quant_problem_t *ps, const float *const *in_scal
         auto flush = [&]() {
             if (sets.count > 0) {
                 if (int4) launch_int4g16(sets, rows, cols, group, st);
-                else launch_rows_quant_sets<F32x4Src>(sets, rows, cols, e, st);
+                else with_round_mode(e, [&](auto em) { launch_rows_quant_sets<F32x4Src>(sets, rows, cols, em, st); });
             }
             sets = RowSets<float>{};
             rows = 0;
