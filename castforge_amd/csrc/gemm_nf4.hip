@@ -54,8 +54,8 @@ constexpr int kLutBytes = 256 * kCopies * 8;  // 64 KB
 constexpr int kMaxP = CFH_MAX_BATCH;
 constexpr int kStages = 3;  // x ring per K part (L2-resident activations)
 constexpr int kWDepth = 6;  // code / absmax register ring (HBM weights: the longer lead)
-// LDS: the table, then KP rings of kStages stages (32 J rows x 128 bytes, plus J KB of slack with 2 parts)
-constexpr int lds_bytes(int J, int kp) { return kLutBytes + kp * kStages * (kp == 2 ? 5 : 4) * J * 1024; }
+// LDS: the table, then KP rings of kStages stages of 32 J rows x 128 bytes
+constexpr int lds_bytes(int J, int kp) { return kLutBytes + kp * kStages * 4 * J * 1024; }
 
 // the NF4 table (QLoRA's 16 quantiles of N(0, 1), scaled to [-1, 1]), as the f32 values the
 // evaluator uses; kNf4Tc is the same table for indices known at compile time
@@ -146,32 +146,26 @@ void nf4_mfma_kernel(Nf4Batch b) {
     const int steps = uni((chunks + kparts - 1) / kparts);
     const int cshift = __builtin_ctz(static_cast<uint32_t>(P.block / 64));  // chunk -> absmax block
 
-    // this part's x ring: stage i at ring + i * stage; row q, 16-byte piece p at 128 q + 16 (p ^ ((q >> 1) & 7))
-    // A stage holds 4 J loads of 1 KB (64 lanes x 16 bytes), issued by the part's nblk waves: with
-    // nblk = 2 a wave issues 2 J of them; with nblk = 4, J of them plus J loads from past the end of
-    // x (they read zero and fetch nothing) into J KB of slack behind the stage, so that every wave
-    // issues the same kDma loads per chunk and the steps need no branches.  (The slack is inside
-    // the stage, so the compiler sees the loads' LDS targets derive from the stage pointer alone.)
-    constexpr int kDma = 2 * J;
-    constexpr int kPerChunk = kDma + 2;  // + the code load and the absmax load
-    const int stage = uni((kparts == 2 ? 5 : 4) * J * 1024);
-    uint8_t *const ring = lds + kLutBytes + kp * kStages * stage;
+    // this part's x ring: stage i at ring + i * kStage; row q, 16-byte piece p at 128 q + 16 (p ^ ((q >> 1) & 7))
+    // A stage is 4 J loads of 1 KB (64 lanes x 16 bytes), issued by the part's nblk waves: 2 J each
+    // with nblk = 2, J each with nblk = 4.  The loop below is instantiated for both counts (a
+    // wave-uniform choice), so every load carries data and the steps have no branches.
+    constexpr int kStage = 4 * J * 1024;
+    uint8_t *const ring = lds + kLutBytes + kp * kStages * kStage;
     // a load t covers stage pieces 64 t .. 64 t + 63: lane -> row 8 t + lane / 8, physical piece lane % 8
     const int lrow = lane >> 3, lpiece = lane & 7;
-    const int real = uni(4 * J / nblk);  // this wave's loads that carry x
     // the lane's offset does not depend on the chunk (the compiler keeps it out of the loop); the
     // chunk adds a wave-uniform byte offset (soffset)
-    auto issue = [&](uint8_t *__restrict__ dst, int c) __attribute__((always_inline)) {
+    auto issue = [&](auto RC, uint8_t *__restrict__ dst, int c) __attribute__((always_inline)) {
+        constexpr int R = decltype(RC)::value;
 #pragma unroll
-        for (int t0 = 0; t0 < kDma; ++t0) {
-            const int t = nb * real + t0;
+        for (int t0 = 0; t0 < R; ++t0) {
+            const int t = nb * R + t0;
             const int row = 8 * t + lrow;
             const int q = lpiece ^ ((row >> 1) & 7);
-            const bool live = t0 < real;
-            const uint32_t off = live ? static_cast<uint32_t>((row * K + q * 8) * 2) : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rx, (__attribute__((address_space(3))) void *)(dst + (live ? t : 4 * J + t0 - real) * 1024), 16,
-                off, c * 128, 0, 0);
+                rx, (__attribute__((address_space(3))) void *)(dst + t * 1024), 16,
+                static_cast<uint32_t>((row * K + q * 8) * 2), c * 128, 0, 0);
         }
     };
     struct WRegs {
@@ -241,73 +235,78 @@ void nf4_mfma_kernel(Nf4Batch b) {
             for (int e = 0; e < 16; ++e) tot[j][e] = __builtin_fmaf(am, part[j][e], tot[j][e]);
     };
 
-    // Rings: step t consumes chunk c_lo + t, its x from stage t % kStages and its codes / absmax
-    // from register slot t % kWDepth.  Step t issues the x of chunk t + kStages - 1 (L2) and then
-    // the codes of chunk t + kWDepth - 1 (HBM: the deeper lead).  vmcnt counts in issue order, so
-    // chunk t's x has landed once at most the 2 code loads issued right after it and step t - 1's
-    // kPerChunk loads are outstanding -- and chunk t's codes, issued kWDepth - 1 steps back, are in
-    // too.  Step t: wait for that, barrier (every wave's x pieces of chunk t are in LDS, and no
-    // wave still reads the stage of chunk t - 1), issue, consume.  Chunk indices past a part's end are clamped to
-    // its last chunk (a reload that nothing consumes), so every step issues the same loads and
-    // every wave passes the same barriers; a part with one chunk fewer skips its last consume.
-    WRegs wr[kWDepth];
-    auto chunk_of = [&](int t) { return min(c_lo + t, c_hi - 1); };
     __syncthreads();  // decode table written (the rings are written only by LDS-DMA below)
-    // prologue, in the steady order: the codes of chunks 0 .. kWDepth - kStages - 1, then for the
-    // pseudo-steps t = -(kStages - 1) .. -1 the x of chunk t + kStages - 1 and the codes of chunk
-    // t + kWDepth - 1
-    static_for<kWDepth - kStages>([&](auto I) { wload(wr[decltype(I)::value], chunk_of(decltype(I)::value)); });
-    static_for<kStages - 1>([&](auto I) {
-        constexpr int t = decltype(I)::value;
-        issue(ring + t * stage, chunk_of(t));
-        wload(wr[t + kWDepth - kStages], chunk_of(t + kWDepth - kStages));
-    });
-    // Step t runs chunk t's MFMAs from operands decoded in step t - 1 and, between them, folds
-    // chunk t - 1's partial into the totals (VALU beside the MFMAs) and decodes chunk t + 1 (the
-    // table and the code registers do not depend on the barrier).  A part with one chunk fewer
-    // runs its last step on a repeat of its last chunk with absmax 0.
-    Dec dec[2];
-    floatx16 part[2][J];
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) part[1][j][e] = 0.0f;
-    dec[1].am = 0.0f;  // step 0 folds this empty "chunk -1"
-    auto am_of = [&](int t, const WRegs &R) { return c_lo + t < c_hi ? R.am : 0.0f; };
-    // chunk 0's codes: issued before the two pseudo-steps' kPerChunk + 2 loads each
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kPerChunk + 4) & ~(15 << 8));
-    decode(lds, wr[0], am_of(0, wr[0]), dec[0]);
-    // One step's work.  The three LDS pointers are restrict-qualified parameters of this one
-    // function: the compiler then knows that the table and fragment reads do not touch the
-    // stage the step's buffer->LDS loads write, and need not wait for those loads.
-    auto body = [&](const uint8_t *__restrict__ lut, const uint8_t *__restrict__ cur, uint8_t *__restrict__ nxt,
-                    auto I, int t) __attribute__((always_inline)) {
-        constexpr int i = decltype(I)::value;
-        issue(nxt, chunk_of(t + kStages - 1));
-        wload(wr[(i + kWDepth - 1) % kWDepth], chunk_of(t + kWDepth - 1));
-        mma(cur, dec[i & 1], part[i & 1]);
-        fold(dec[(i + 1) & 1].am, part[(i + 1) & 1]);
-        decode(lut, wr[(i + 1) % kWDepth], am_of(t + 1, wr[(i + 1) % kWDepth]), dec[(i + 1) & 1]);
+    auto main_loop = [&](auto RC) __attribute__((always_inline)) {
+        constexpr int kPer = decltype(RC)::value + 2;  // a wave's loads per chunk: its x loads, codes, absmax
+        // Rings: step t consumes chunk c_lo + t, its x from stage t % kStages and its codes / absmax
+        // from register slot t % kWDepth.  Step t issues the x of chunk t + kStages - 1 (L2) and then
+        // the codes of chunk t + kWDepth - 1 (HBM: the deeper lead).  vmcnt counts in issue order, so
+        // chunk t's x has landed once at most the 2 code loads issued right after it and step t - 1's
+        // kPer loads are outstanding -- and chunk t's codes, issued kWDepth - 1 steps back, are in
+        // too.  Step t: wait for that, barrier (every wave's x pieces of chunk t are in LDS, and no
+        // wave still reads the stage of chunk t - 1), issue, consume.  Chunk indices past a part's end are clamped to
+        // its last chunk (a reload that nothing consumes), so every step issues the same loads and
+        // every wave passes the same barriers; a part with one chunk fewer skips its last consume.
+        WRegs wr[kWDepth];
+        auto chunk_of = [&](int t) { return min(c_lo + t, c_hi - 1); };
+        // prologue, in the steady order: the codes of chunks 0 .. kWDepth - kStages - 1, then for the
+        // pseudo-steps t = -(kStages - 1) .. -1 the x of chunk t + kStages - 1 and the codes of chunk
+        // t + kWDepth - 1
+        static_for<kWDepth - kStages>([&](auto I) { wload(wr[decltype(I)::value], chunk_of(decltype(I)::value)); });
+        static_for<kStages - 1>([&](auto I) {
+            constexpr int t = decltype(I)::value;
+            issue(RC, ring + t * kStage, chunk_of(t));
+            wload(wr[t + kWDepth - kStages], chunk_of(t + kWDepth - kStages));
+        });
+        // Step t runs chunk t's MFMAs from operands decoded in step t - 1 and, between them, folds
+        // chunk t - 1's partial into the totals (VALU beside the MFMAs) and decodes chunk t + 1 (the
+        // table and the code registers do not depend on the barrier).  A part with one chunk fewer
+        // runs its last step on a repeat of its last chunk with absmax 0.
+        Dec dec[2];
+        floatx16 part[2][J];
+    #pragma unroll
+        for (int j = 0; j < J; ++j)
+    #pragma unroll
+            for (int e = 0; e < 16; ++e) part[1][j][e] = 0.0f;
+        dec[1].am = 0.0f;  // step 0 folds this empty "chunk -1"
+        auto am_of = [&](int t, const WRegs &R) { return c_lo + t < c_hi ? R.am : 0.0f; };
+        // chunk 0's codes: issued before the two pseudo-steps' kPer + 2 loads each
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kPer + 4) & ~(15 << 8));
+        decode(lds, wr[0], am_of(0, wr[0]), dec[0]);
+        // One step's work.  The three LDS pointers are restrict-qualified parameters of this one
+        // function: the compiler then knows that the table and fragment reads do not touch the
+        // stage the step's buffer->LDS loads write, and need not wait for those loads.
+        auto body = [&](const uint8_t *__restrict__ lut, const uint8_t *__restrict__ cur, uint8_t *__restrict__ nxt,
+                        auto I, int t) __attribute__((always_inline)) {
+            constexpr int i = decltype(I)::value;
+            issue(RC, nxt, chunk_of(t + kStages - 1));
+            wload(wr[(i + kWDepth - 1) % kWDepth], chunk_of(t + kWDepth - 1));
+            mma(cur, dec[i & 1], part[i & 1]);
+            fold(dec[(i + 1) & 1].am, part[(i + 1) & 1]);
+            decode(lut, wr[(i + 1) % kWDepth], am_of(t + 1, wr[(i + 1) % kWDepth]), dec[(i + 1) & 1]);
+        };
+        auto step = [&](auto I, int t) {
+            constexpr int i = decltype(I)::value;  // t modulo kWDepth (a multiple of kStages and of 2)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPer + 2) & ~(15 << 8));
+            // unconditional: the compiler's own wait tracking then sees every LDS read retired
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));
+            __builtin_amdgcn_s_barrier();
+            body(lds, ring + (i % kStages) * kStage, ring + ((i + kStages - 1) % kStages) * kStage, I, t);
+        };
+        static_assert(kWDepth % kStages == 0 && kWDepth % 2 == 0, "one unrolled group covers every ring");
+        int t = 0;
+        for (; t + kWDepth <= steps; t += kWDepth)
+            static_for<kWDepth>([&](auto I) { step(I, t + decltype(I)::value); });
+        static_for<kWDepth>([&](auto I) {
+            if (t + decltype(I)::value < steps) step(I, t + decltype(I)::value);
+        });
+        // the last chunk's partial: part[(steps - 1) & 1], its absmax in dec[(steps - 1) & 1]
+        if ((steps - 1) & 1) fold(dec[1].am, part[1]);
+        else fold(dec[0].am, part[0]);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // the trailing reloads
     };
-    auto step = [&](auto I, int t) {
-        constexpr int i = decltype(I)::value;  // t modulo kWDepth (a multiple of kStages and of 2)
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPerChunk + 2) & ~(15 << 8));
-        // unconditional: the compiler's own wait tracking then sees every LDS read retired
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(63) & ~(15 << 8));
-        __builtin_amdgcn_s_barrier();
-        body(lds, ring + (i % kStages) * stage, ring + ((i + kStages - 1) % kStages) * stage, I, t);
-    };
-    static_assert(kWDepth % kStages == 0 && kWDepth % 2 == 0, "one unrolled group covers every ring");
-    int t = 0;
-    for (; t + kWDepth <= steps; t += kWDepth)
-        static_for<kWDepth>([&](auto I) { step(I, t + decltype(I)::value); });
-    static_for<kWDepth>([&](auto I) {
-        if (t + decltype(I)::value < steps) step(I, t + decltype(I)::value);
-    });
-    // the last chunk's partial: part[(steps - 1) & 1], its absmax in dec[(steps - 1) & 1]
-    if ((steps - 1) & 1) fold(dec[1].am, part[1]);
-    else fold(dec[0].am, part[0]);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // the trailing reloads
+    if (nblk == 2) main_loop(std::integral_constant<int, 2 * J>{});
+    else main_loop(std::integral_constant<int, J>{});
 
     // K parts of one n block: parts 1.. write their totals over the table, part 0 adds them in
     // part order and stores
