@@ -288,9 +288,8 @@ def main():
         del src, dst
 
     if not args.only_headline:
-        # small-batch decode over the planes (M = 2..8; W_down's 8 rows of x run as two halves
-        # at M > 4, each streaming its planes: the bytes below count them once)
-        for m in (4, 8):
+        # small-batch decode over the planes (M = 2..16, every matrix's planes streamed once)
+        for m in (4, 8, 16):
             st = time_steps(planes_case(m), max(20, args.steps // 4), 5, min_ms=20.0, replays=3)
             components[f"w4a16_planes_gemv_m{m}_GBps"] = round(planes_bytes(m) / (st * 1e-3) / 1e9, 1)
             components[f"w4a16_planes_gemv_m{m}_us"] = round(st * 1e3, 2)

@@ -1,8 +1,9 @@
-// W4A16 decode GEMV (M = 1..8) over INT4 g128 weights in the GEMV planes layout, and the M = 1
+// W4A16 decode GEMV (M = 1..16) over INT4 g128 weights in the GEMV planes layout, and the M = 1
 // decode GEMV over NF4 planes and GGUF Q4_0 GEMV planes, gfx950.  planes_kernel serves INT4 at
-// M = 2..8; planes_m1_kernel (after it) serves M = 1 for the three formats; planes_i8_kernel
-// serves INT4 at M = 1 on the integer MFMA wherever its x pieces fit LDS (planes_m1_kernel's
-// INT4 form, with the same arithmetic as planes_kernel, beyond).
+// M = 2..4 wherever x fits LDS; planes_xr_kernel (after it) serves M = 5..16, and M = 2..4
+// beyond; planes_m1_kernel serves M = 1 for the three formats; planes_i8_kernel serves INT4 at
+// M = 1 on the integer MFMA wherever its x pieces fit LDS (planes_m1_kernel's INT4 form, with
+// the same arithmetic as planes_kernel, beyond).
 //
 // Replaces the evaluation of `castforge.fused_qmatmul` at decode (eval.rs:1145-1179 with
 // eval_matmul_2d, eval.rs:1465-1507; packed_rhs [N, K] weights, fold.rs:549-554) for the
@@ -62,26 +63,11 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 constexpr int kGroup = 128;
 constexpr uint32_t kOob = 0x80000000u;  // past every descriptor's range: reads 0, no traffic
-// problems of a launch: one per matrix at M <= 4; at M = 5..8 a matrix whose 8 rows of x do
-// not fit LDS splits into two problems of 4 rows.  Each kernel instance's argument holds only
-// as many problems as it can get (a smaller argument shortens the prologue's reads of it).
-constexpr int kMaxP = 2 * CFH_MAX_BATCH;
-template <int MR>
-__host__ __device__ constexpr int max_problems() { return MR == 8 ? kMaxP : CFH_MAX_BATCH; }
-
 #ifndef CFH_PLANES_WAVES
 #define CFH_PLANES_WAVES 16
 #endif
 #ifndef CFH_PLANES_DEPTH
 #define CFH_PLANES_DEPTH 3
-#endif
-// M = 5..8: 8 waves per workgroup (the partials of 8 rows per wave and tile would not fit
-// LDS next to x at 16) and their ring depth
-#ifndef CFH_PLANES_WAVES8
-#define CFH_PLANES_WAVES8 8
-#endif
-#ifndef CFH_PLANES_DEPTH8
-#define CFH_PLANES_DEPTH8 4
 #endif
 constexpr int kWaves = CFH_PLANES_WAVES;
 constexpr int kDepth = CFH_PLANES_DEPTH;
@@ -153,17 +139,16 @@ struct Stage {
     uint32_t sc, zb;
 };
 
-// x rows staged in LDS (M = 1: one row; otherwise up to MR = 4 or 8 fragment rows) and their
-// row stride
+// x rows staged in LDS (M = 1: one row; otherwise up to MR = 4 fragment rows) and their row
+// stride
 template <int MR>
 __host__ __device__ constexpr uint32_t x_row_stride(uint32_t G) { return MR == 1 ? G * 256 : G * 256 + 16; }
 
 // LDS: [x as f16, M rows of G * 256 B at x_row_stride][per (chunk, row) 2^sh, G * MR * 4 B
 // (16-byte padded)][partials: tiles x NW x 16 x MR f32]
-// MR = 8: A row i is x row min(i mod 8, M - 1); D rows 0..7 are lanes 0..31 (4 rows each).
 template <int NW, int D, int MR>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW * kWgPerCu / 4)))
-void planes_kernel(PBatch<max_problems<MR>()> b) {
+void planes_kernel(PBatch<CFH_MAX_BATCH> b) {
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = uni(tid >> 6);
@@ -174,7 +159,7 @@ void planes_kernel(PBatch<max_problems<MR>()> b) {
     // workgroups (host-checked: wgs * units < 2^31)
     int pi = 0;
 #pragma unroll
-    for (int i = 1; i < max_problems<MR>(); ++i)
+    for (int i = 1; i < CFH_MAX_BATCH; ++i)
         if (i < b.count && w >= b.p[i].wg0) pi = i;
     const PProblem &P = b.p[pi];
     const int G = P.G, local = w - P.wg0;
@@ -221,14 +206,14 @@ void planes_kernel(PBatch<max_problems<MR>()> b) {
     // per-lane offsets within a chunk, pushed out of range (OR kOob) for rows outside
     // [rlo, rhi) and for positions past the workgroup's tiles: recomputed when the tile changes.
     // Every lane needs its row's zero point (its codes are decoded as exact q - z); the scale
-    // multiplies the MFMA result, whose output rows lanes 0..15 hold (0..31 at MR = 8).
+    // multiplies the MFMA result, whose output rows lanes 0..15 hold.
     uint32_t vcode, vscale, vzero;
     auto lane_offsets = [&]() __attribute__((always_inline)) {
         const int row = (t0 + lt) * 16 + r16;
         const bool ok = lt < ntiles && row >= rlo && row < rhi;
         const uint32_t m = ok ? 0u : kOob;
         vcode = (static_cast<uint32_t>(lane) * 16u) | m;
-        vscale = (static_cast<uint32_t>(r16) * 2u) | (lane < (MR == 8 ? 32 : 16) ? m : kOob);
+        vscale = (static_cast<uint32_t>(r16) * 2u) | (lane < 16 ? m : kOob);
         vzero = static_cast<uint32_t>(r16 >> 1) | m;
     };
     lane_offsets();
@@ -414,6 +399,276 @@ void planes_kernel(PBatch<max_problems<MR>()> b) {
     }
 }
 
+// ---- M = 2..16: x in registers --------------------------------------------------------------------
+// planes_xr_kernel: the design above with x held in registers instead of LDS, so that x's size
+// bounds neither K nor M and every matrix streams its planes once.  A row of x is an A row of
+// the MFMA (A row i is x row min(i mod MR, M - 1), MR = 4, 8 or 16), so one chunk costs the same
+// 4 MFMAs at every M up to 16.
+//   * Each wave owns chunks g = wave, wave + NW, ... of its workgroup's tiles and walks them
+//     chunk by chunk, every tile of a chunk in turn.  A chunk's x fragment (64 bytes a lane: the
+//     32 values of the lane's A row that its part of the MFMA reads) is loaded with the chunk's
+//     first position, ahead of that position's codes in the same ring stage, and converted to
+//     f16 with the per-(row, chunk) power of two when the wave reaches that position; the
+//     chunk's other tiles reuse it.  Per workgroup x is read once, from L2.
+//   * Each position's partial (D rows 0..MR-1: 16 bytes a lane) is added into the wave's own LDS
+//     slot of its tile, in the wave's chunk order; only the wave itself touches its slots, so
+//     there is no barrier until the end, where the workgroup sums each row's slots in wave
+//     order (the same bits on every run).
+//   * LDS holds only the slots: tiles x NW x 16 x MR f32 per workgroup.
+// waves and ring depth: 16 waves at MR = 4 and 8; at MR = 16 the slots of 16 waves would not
+// fit LDS next to the waves' x areas for the row counts of a 7B block, so 8 with a deeper ring
+#ifndef CFH_PLANES_XR_WAVES
+#define CFH_PLANES_XR_WAVES 16
+#endif
+#ifndef CFH_PLANES_XR_DEPTH
+#define CFH_PLANES_XR_DEPTH 3
+#endif
+#ifndef CFH_PLANES_XR_WAVES16
+#define CFH_PLANES_XR_WAVES16 8
+#endif
+#ifndef CFH_PLANES_XR_DEPTH16
+#define CFH_PLANES_XR_DEPTH16 4
+#endif
+#ifndef CFH_PLANES_XR_XCOST
+#define CFH_PLANES_XR_XCOST 1.0
+#endif
+#ifndef CFH_PLANES_XR_TILES
+#define CFH_PLANES_XR_TILES 1
+#endif
+#ifndef CFH_PLANES_XR_ROT
+#define CFH_PLANES_XR_ROT 0
+#endif
+
+// one ring stage: TP tiles of one chunk (their codes, scales and zero points) and, when they are
+// the chunk's first, the chunk's x fragment
+template <int TP, int MR>
+struct XStage {
+    uint32_t w[TP][4];
+    uint32_t sc[TP], zb[TP];
+    uint4 x[MR / 4];
+};
+
+template <int NW, int D, int MR, int TP>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW * kWgPerCu / 4)))
+void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
+    // a chunk's partial is rounded on its own before it is added (no contraction into an fma):
+    // chunk results that cancel exactly sum to exactly zero
+#pragma clang fp contract(off)
+    static_assert(MR == 4 || MR == 8 || MR == 16, "MR is 4, 8 or 16");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = uni(tid >> 6);
+    const int w = blockIdx.x;
+    const int r16 = lane & 15, part = lane >> 4;
+
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < CFH_MAX_BATCH; ++i)
+        if (i < b.count && w >= b.p[i].wg0) pi = i;
+    const PProblem &P = b.p[pi];
+    const int G = P.G, M = P.m, local = w - P.wg0;
+    const int u0 = static_cast<int>(static_cast<uint32_t>(local * P.units) / static_cast<uint32_t>(P.wgs));
+    const int u1 = static_cast<int>(static_cast<uint32_t>((local + 1) * P.units) / static_cast<uint32_t>(P.wgs));
+    const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
+    const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
+    const int ntiles = t1 - t0;
+    const int ngrp = (ntiles + TP - 1) / TP;  // steps per chunk: TP tiles each (the last may hold dead tiles)
+    constexpr int kSlot = 16 * MR;             // floats of one (tile, wave) slot
+    const bool out_lane = lane < 4 * MR;       // lanes holding D rows 0..MR-1
+    float *const accs = reinterpret_cast<float *>(lds);
+    float *const mine = accs + wave * kSlot + 4 * lane;  // slot (t, wave) at mine + t * NW * kSlot
+    // this wave's x area after the slots: MR rows of a chunk as f16 (256 bytes each), then their
+    // post factors
+    uint8_t *const xarea = lds + ntiles * NW * kSlot * 4 + wave * (MR * 256 + 64);
+
+    for (int t = 0; t < ntiles; ++t)
+        if (out_lane) *reinterpret_cast<floatx4 *>(mine + t * NW * kSlot) = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int nc = G > wave ? (G - wave + NW - 1) / NW : 0;  // chunks of this wave
+    const int nsteps = nc * ngrp;
+    const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
+    const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
+    const rsrc_t rscale = make_rsrc(P.scales, chunks * 32u);
+    const rsrc_t rzero = make_rsrc(P.zeros, chunks * 8u);
+    const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2);
+    const rsrc_t rx = make_rsrc(P.x, static_cast<uint32_t>(M) * rowb);
+    // a chunk's x: load i brings rows 4 i .. 4 i + 3 (clamped to M - 1), 16 bytes a lane
+    auto xrow = [&](int i) __attribute__((always_inline)) { return min(4 * i + part, M - 1); };
+
+    int lc = 0, lg = 0;  // load cursor: the wave's chunk index, tile group
+    auto load_x = [&](uint4 (&xr)[MR / 4], int c) __attribute__((always_inline)) {
+        const uint32_t xo = c < nc ? static_cast<uint32_t>(wave + c * NW) * (kGroup * 2) + static_cast<uint32_t>(r16) * 16u : kOob;
+        static_for<MR / 4>([&](auto jj) __attribute__((always_inline)) {
+            constexpr int j = decltype(jj)::value;
+            xr[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rx, xo + static_cast<uint32_t>(xrow(j)) * rowb, 0, 0));
+        });
+    };
+    auto load = [&](XStage<TP, MR> &st) __attribute__((always_inline)) {
+        const uint32_t g = static_cast<uint32_t>(wave + lc * NW);
+        if (lg == ngrp - 1) load_x(st.x, lc + 1);  // the chunk's last tiles: the next chunk's x first
+        static_for<TP>([&](auto uu) __attribute__((always_inline)) {
+            constexpr int u = decltype(uu)::value;
+            const int lt = lg * TP + u;
+            // rows outside [rlo, rhi), tiles past the workgroup's and chunks past the wave's read
+            // zeros (offsets pushed out of range) and add nothing
+            const int row = (t0 + lt) * 16 + r16;
+            const uint32_t m = lc < nc && lt < ntiles && row >= rlo && row < rhi ? 0u : kOob;
+            const uint32_t chunk = static_cast<uint32_t>(t0 + lt) * static_cast<uint32_t>(G) + g;
+            const uint4 v = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, ((static_cast<uint32_t>(lane) * 16u) | m) + chunk * 1024u,
+                                                             0, CFH_PLANES_CPOL));
+            st.w[u][0] = v.x;
+            st.w[u][1] = v.y;
+            st.w[u][2] = v.z;
+            st.w[u][3] = v.w;
+            st.sc[u] = __builtin_amdgcn_raw_buffer_load_b16(
+                rscale, ((static_cast<uint32_t>(r16) * 2u) | (out_lane ? m : kOob)) + chunk * 32u, 0, 0);
+            st.zb[u] = __builtin_amdgcn_raw_buffer_load_b8(rzero, (static_cast<uint32_t>(r16 >> 1) | m) + chunk * 8u, 0, 0);
+        });
+        if (++lg == ngrp) {
+            lg = 0;
+            ++lc;
+        }
+    };
+
+    // a chunk's x to f16 in the decode's order (per 8 values the pairs (0, 4), (1, 5), (2, 6),
+    // (3, 7)), scaled by 2^-sh so that the largest |x| of the row's chunk (its 16 lanes of a load)
+    // lands in [2^14, 2^15), written to the wave's x area; then each lane reads its A fragment
+    // (row r16 mod MR, values 32 part .. 32 part + 31) and the post factors 2^sh of its D rows
+    // 4 (part mod MR / 4) + q
+    const int prow = 4 * (part & (MR / 4 - 1));
+    half8_t xa[4];
+    floatx4 post;
+    auto convert = [&](const uint4 (&xr)[MR / 4]) __attribute__((always_inline)) {
+        static_for<MR / 4>([&](auto ii) __attribute__((always_inline)) {
+            constexpr int i = decltype(ii)::value;
+            const uint32_t wv[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+            uint32_t emax = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t a = (wv[q] >> 7) & 0xFFu, c = (wv[q] >> 23) & 0xFFu;
+                emax = emax > a ? emax : a;
+                emax = emax > c ? emax : c;
+            }
+            {  // over the row's 16 lanes (DPP row rotations by 1, 2, 4, 8)
+                int e = static_cast<int>(emax);
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x121, 0xF, 0xF, false));
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x122, 0xF, 0xF, false));
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x124, 0xF, 0xF, false));
+                e = max(e, __builtin_amdgcn_mov_dpp(e, 0x128, 0xF, 0xF, false));
+                emax = static_cast<uint32_t>(e);
+            }
+            int sh = static_cast<int>(emax) - 127 - 14;
+            sh = sh < -126 ? -126 : (sh > 126 ? 126 : sh);
+            const float pre = __uint_as_float(static_cast<uint32_t>(127 - sh) << 23);
+            auto h = [&](int e) __attribute__((always_inline)) {
+                const uint32_t u = wv[e >> 1];
+                const float f = __uint_as_float((e & 1) ? (u & 0xFFFF0000u) : (u << 16)) * pre;
+                return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f)));
+            };
+            const int row = 4 * i + part;
+            *reinterpret_cast<uint4 *>(xarea + row * 256 + r16 * 16) =
+                make_uint4(h(0) | (h(4) << 16), h(1) | (h(5) << 16), h(2) | (h(6) << 16), h(3) | (h(7) << 16));
+            if (r16 == 0)
+                reinterpret_cast<float *>(xarea + MR * 256)[row] = __uint_as_float(static_cast<uint32_t>(127 + sh) << 23);
+        });
+        const uint8_t *xs = xarea + (r16 & (MR - 1)) * 256 + part * 64;
+        static_for<4>([&](auto jj) __attribute__((always_inline)) {
+            constexpr int j = decltype(jj)::value;
+            xa[j] = *reinterpret_cast<const half8_t *>(xs + 16 * j);
+        });
+        post = *reinterpret_cast<const floatx4 *>(xarea + MR * 256 + prow * 4);
+    };
+
+    // the first chunk's x, then the ring; each stage of a chunk's last tiles carries the next
+    // chunk's x, converted right after that stage's refill is issued (while the wave waits for
+    // the next stage's loads)
+    uint4 x0[MR / 4];
+    load_x(x0, 0);
+    XStage<TP, MR> st[D];
+    static_for<D>([&](auto i) __attribute__((always_inline)) {
+        load(st[i]);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    convert(x0);
+
+    const uint32_t LO = vgpr_const(0x000F000Fu), HI = vgpr_const(0x00F000F0u), MG = vgpr_const(0x64006400u);
+    int pc = 0, pg = 0;  // process cursor
+    const int steps = (nsteps + D - 1) / D * D;
+    for (int k = 0; k < steps; k += D) {
+        static_for<D>([&](auto ii) __attribute__((always_inline)) {
+            constexpr int i = decltype(ii)::value;
+            XStage<TP, MR> &s = st[i];
+            static_for<TP>([&](auto uu) __attribute__((always_inline)) {
+                constexpr int u = decltype(uu)::value;
+                const int pt = pg * TP + u;
+                const uint32_t w0 = s.w[u][0], w1 = s.w[u][1], w2 = s.w[u][2], w3 = s.w[u][3];
+                const uint32_t w08 = w0 >> 8, w18 = w1 >> 8, w28 = w2 >> 8, w38 = w3 >> 8;
+                const uint32_t zi = (s.zb[u] >> (4 * (r16 & 1))) & 15u;
+                const float sc = f16_to_f32(static_cast<uint16_t>(s.sc[u]));
+                // (1024 + q) - (1024 + z) and (1024 + 16 q) / 16 - (64 + z): exact small integers
+                const half2_t zc1024 = as_h2((0xE400u + zi) * 0x00010001u);
+                const half2_t zc64 = as_h2((0xD400u + (zi << 4)) * 0x00010001u);
+                const half2_t sixteenth = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+                auto dec = [&](uint32_t ww, uint32_t w8) __attribute__((always_inline)) {
+                    return pack8(as_u(as_h2((ww & LO) | MG) + zc1024), as_u(as_h2((ww & HI) | MG) * sixteenth + zc64),
+                                 as_u(as_h2((w8 & LO) | MG) + zc1024), as_u(as_h2((w8 & HI) | MG) * sixteenth + zc64));
+                };
+                // two accumulation chains halve the MFMA dependency latency
+                floatx4 pa = floatx4{0.f, 0.f, 0.f, 0.f}, pb = pa;
+                pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0], dec(w0, w08), pa, 0, 0, 0);
+                pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1], dec(w1, w18), pb, 0, 0, 0);
+                pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2], dec(w2, w28), pa, 0, 0, 0);
+                pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[3], dec(w3, w38), pb, 0, 0, 0);
+                if (pc < nc && pt < ntiles && out_lane) {
+                    floatx4 *dst = reinterpret_cast<floatx4 *>(mine + pt * NW * kSlot);
+                    floatx4 a = *dst;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) a[q] = a[q] + (pa[q] + pb[q]) * (sc * post[q]);
+                    *dst = a;
+                }
+            });
+            const bool last = pg == ngrp - 1;
+            // the next chunk's x moved out of the stage (opaque copies: the refill may then load
+            // into the stage's own registers, none rotate between iterations)
+            uint4 xn[MR / 4];
+            if (last) {
+#pragma unroll
+                for (int j = 0; j < MR / 4; ++j) {
+                    uint32_t a = s.x[j].x, c = s.x[j].y, d = s.x[j].z, e = s.x[j].w;
+                    asm volatile("v_mov_b32 %0, %1" : "=v"(xn[j].x) : "v"(a));
+                    asm volatile("v_mov_b32 %0, %1" : "=v"(xn[j].y) : "v"(c));
+                    asm volatile("v_mov_b32 %0, %1" : "=v"(xn[j].z) : "v"(d));
+                    asm volatile("v_mov_b32 %0, %1" : "=v"(xn[j].w) : "v"(e));
+                }
+            }
+            if (++pg == ngrp) {
+                pg = 0;
+                ++pc;
+            }
+            load(s);
+            if (last) convert(xn);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    }
+    lds_barrier<63>();  // every wave's slots are final
+
+    for (int i = tid; i < ntiles * 16 * M; i += 64 * NW) {
+        const int r = i / M, m = i - r * M;
+        const int row = (t0 + (r >> 4)) * 16 + (r & 15);
+        if (row >= rlo && row < rhi) {
+            const float *pa = accs + (r >> 4) * NW * kSlot + ((r & 15) + 16 * (m >> 2)) * 4 + (m & 3);
+            float v = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; ++w2) v += pa[w2 * kSlot];
+            const int64_t o = static_cast<int64_t>(m) * P.n + row;
+            if (b.y_bf16) static_cast<uint16_t *>(P.y)[o] = f32_to_bf16_rne(v);
+            else static_cast<float *>(P.y)[o] = v;
+        }
+    }
+}
+
 // ---- M = 1: INT4 g128, NF4 and GGUF Q4_0 planes ------------------------------------------------
 // planes_m1_kernel: the design above specialised to one row of x (a scalar partial per lane, a
 // 64-byte problem record, 8 problems per launch), with the decode and metadata of its KIND.
@@ -437,6 +692,9 @@ constexpr int kNf4Depth = CFH_NF4_PLANES_DEPTH;
 #define CFH_PLANES_I4_DEPTH 2  // the INT4 kind of the kernel below (M = 1 over INT4 GEMV planes)
 #endif
 constexpr int kI4Depth = CFH_PLANES_I4_DEPTH;
+#ifndef CFH_PLANES_XR_FROM
+#define CFH_PLANES_XR_FROM 5  // M from which planes_xr_kernel serves every batch (2..5)
+#endif
 #ifndef CFH_PLANES_M1_GENERIC
 #define CFH_PLANES_M1_GENERIC 1  // M = 1 over INT4 GEMV planes on planes_m1_kernel (0: planes_kernel)
 #endif
@@ -1223,12 +1481,7 @@ std::vector<int> workgroups_per_problem(const std::vector<int64_t> &bytes, const
 }
 
 template <int NW, int D, int MR>
-void launch_planes(const PBatch<kMaxP> &all, int64_t grid, int64_t lds, hipStream_t st) {
-    require(all.count >= 1 && all.count <= max_problems<MR>(), "too many problems for one launch");
-    PBatch<max_problems<MR>()> b{};
-    for (int i = 0; i < all.count; ++i) b.p[i] = all.p[i];
-    b.count = all.count;
-    b.y_bf16 = all.y_bf16;
+void launch_planes(const PBatch<CFH_MAX_BATCH> &b, int64_t grid, int64_t lds, hipStream_t st) {
     static std::mutex mu;
     static std::map<int, bool> attr_set;  // per device
     int dev = 0;
@@ -1247,6 +1500,130 @@ void launch_planes(const PBatch<kMaxP> &all, int64_t grid, int64_t lds, hipStrea
     check_launch("planes_kernel");
 }
 
+
+template <int NW, int D, int MR, int TP>
+void launch_planes_xr(const PBatch<CFH_MAX_BATCH> &b, int64_t grid, int64_t lds, hipStream_t st) {
+    static std::mutex mu;
+    static std::map<int, bool> attr_set;  // per device
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    {
+        std::lock_guard<std::mutex> g(mu);
+        if (!attr_set[dev]) {
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_xr_kernel<NW, D, MR, TP>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
+                      "hipFuncSetAttribute");
+            attr_set[dev] = true;
+        }
+    }
+    planes_xr_kernel<NW, D, MR, TP>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), static_cast<size_t>(lds), st>>>(b);
+    check_launch("planes_xr_kernel");
+}
+
+// workgroups per problem such that bytes[i] / wgs[i] + fixed[i] is about equal over the problems
+// (fixed: work every workgroup of problem i does whatever its share), at most units[i] each and W
+// in total (at least one each): the level T solves sum bytes[i] / (T - fixed[i]) = W, the shares
+// are rounded by largest remainder.  All fixed equal to 0 is workgroups_per_problem's split.
+std::vector<int> workgroups_balanced(const std::vector<int64_t> &bytes, const std::vector<int64_t> &fixed,
+                                     const std::vector<int64_t> &units, int W) {
+    const size_t n = bytes.size();
+    double fmax = 0.0;
+    for (int64_t f : fixed) fmax = std::max(fmax, static_cast<double>(f));
+    auto total = [&](double T) {
+        double t = 0.0;
+        for (size_t i = 0; i < n; ++i) t += static_cast<double>(bytes[i]) / (T - static_cast<double>(fixed[i]));
+        return t;
+    };
+    double lo = fmax, hi = fmax + 1.0;
+    while (total(hi) > W) hi = fmax + 2.0 * (hi - fmax);
+    for (int it = 0; it < 100; ++it) {
+        const double mid = 0.5 * (lo + hi);
+        if (mid <= fmax || total(mid) > W) lo = mid;
+        else hi = mid;
+    }
+    std::vector<int> wgs(n, 1);
+    int used = 0;
+    std::vector<std::pair<double, size_t>> rem;
+    for (size_t i = 0; i < n; ++i) {
+        const double share = static_cast<double>(bytes[i]) / (hi - static_cast<double>(fixed[i]));
+        wgs[i] = static_cast<int>(std::min<int64_t>(std::max(1, static_cast<int>(share)), units[i]));
+        used += wgs[i];
+        rem.push_back({share - static_cast<double>(wgs[i]), i});
+    }
+    std::sort(rem.begin(), rem.end(), [](const auto &a, const auto &c) { return a.first > c.first; });
+    for (size_t j = 0; used < W && j < rem.size(); ++j) {
+        const size_t i = rem[j].second;
+        if (wgs[i] < units[i]) {
+            ++wgs[i];
+            ++used;
+        }
+    }
+    return wgs;
+}
+
+// tiles one workgroup of a problem spans at most, for `units` 8-row units over `wgs` workgroups
+int64_t planes_tiles(int64_t units, int64_t wgs) { return (units + wgs - 1) / wgs / 2 + 2; }
+
+// M = 2..16 on planes_xr_kernel: every problem's planes streamed once, each problem's share of
+// the CUs by its bytes; a problem whose workgroups would span more tiles than their slots fit in
+// LDS gets more workgroups.
+template <int NW, int D, int MR>
+void planes_xr_launch(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
+                      hipStream_t st) {
+    constexpr int TP = CFH_PLANES_XR_TILES;
+    const int64_t slot_bytes = int64_t(NW) * 64 * MR;          // one tile's slots
+    const int64_t x_bytes = int64_t(NW) * (int64_t(MR) * 256 + 64);  // the waves' x areas
+    const int64_t max_tiles = (kLdsMax / kWgPerCu - x_bytes) / slot_bytes;
+    std::vector<int64_t> bytes, units;
+    for (int i = 0; i < count; ++i) {
+        const cfh_w4a16_problem_t &q = problems[i];
+        require(m * q.k * 2 < (int64_t(1) << 31), "x of one problem must stay below 2 GiB");
+        bytes.push_back(((q.n + 15) / 16) * (q.k / kGroup) * 1024);
+        units.push_back((q.n + 7) / 8);
+    }
+    // every workgroup converts its problem's whole x (M x K values) besides streaming its share of
+    // the planes: the split equalises bytes / wgs + c M K over the problems (c: the cost of
+    // converting one value in bytes streamed)
+    std::vector<int64_t> xcost;
+    for (int i = 0; i < count; ++i) xcost.push_back(static_cast<int64_t>(CFH_PLANES_XR_XCOST * m * problems[i].k));
+    std::vector<int> wgs = workgroups_balanced(bytes, xcost, units, cu_count() * kWgPerCu);
+    PBatch<CFH_MAX_BATCH> b{};
+    int64_t lds = 0, grid = 0;
+    for (int j = 0; j < count; ++j) {
+        const cfh_w4a16_problem_t &q = problems[j];
+        int64_t wj = wgs[static_cast<size_t>(j)];
+        const int64_t u = units[static_cast<size_t>(j)];
+        if (planes_tiles(u, wj) > max_tiles) wj = std::min<int64_t>(u, (u + 2 * (max_tiles - 2) - 1) / (2 * (max_tiles - 2)));
+        require(planes_tiles(u, wj) <= max_tiles, "a problem's rows exceed the GEMV planes kernel's LDS");
+        PProblem &P = b.p[j];
+        P.codes = reinterpret_cast<const uint8_t *>(q.codes);
+        P.scales = q.scales_f16;
+        P.zeros = reinterpret_cast<const uint8_t *>(q.zeros);
+        P.x = q.x;
+        P.y = q.y;
+        P.n = static_cast<int32_t>(q.n);
+        P.G = static_cast<int32_t>(q.k / kGroup);
+        P.units = static_cast<int32_t>(u);
+        P.wg0 = static_cast<int32_t>(grid);
+        P.wgs = static_cast<int32_t>(wj);
+        P.m = static_cast<int32_t>(m);
+        require(wj * u < (int64_t(1) << 31), "too many rows for one launch");
+        grid += wj;
+        lds = std::max<int64_t>(lds, planes_tiles(u, wj) * slot_bytes + x_bytes);
+    }
+    b.count = count;
+    b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
+    launch_planes_xr<NW, D, MR, TP>(b, grid, std::max<int64_t>(lds, kLdsFloor), st);
+}
+
+void planes_xr_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
+                       hipStream_t st) {
+    if (m <= 4) planes_xr_launch<CFH_PLANES_XR_WAVES, CFH_PLANES_XR_DEPTH, 4>(problems, count, m, y_dtype, st);
+    else if (m <= 8) planes_xr_launch<CFH_PLANES_XR_WAVES, CFH_PLANES_XR_DEPTH, 8>(problems, count, m, y_dtype, st);
+    else planes_xr_launch<CFH_PLANES_XR_WAVES16, CFH_PLANES_XR_DEPTH16, 16>(problems, count, m, y_dtype, st);
+}
+
 // LDS bytes of one problem: its x rows, their post factors and the partials of the tiles one
 // of its workgroups spans (at most ceil(units / wgs) / 2 + 2)
 int64_t planes_lds(int mr, int nw, const PProblem &P) {
@@ -1259,22 +1636,17 @@ template <int NBPC, int KIND = kKindNf4>
 void launch_planes_m1(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st);
 void launch_planes_i8(const NBatch &b, int64_t grid, int64_t lds, hipStream_t st);
 
-// M = 1: one row of x per problem (16 waves); M = 2..4: up to 4 rows (16 waves); M = 5..8:
-// up to 8 rows (8 waves), a problem whose 8 rows of x do not fit LDS next to its partials
-// split into two problems of 4 rows that stream the same planes.  Beyond M = 8 the partials of
-// a workgroup (16 rows per tile and wave) outgrow LDS for matrices that get few workgroups,
-// and every further group of rows would stream the planes again: the canonical-layout kernels
-// serve M > 8.
+// M = 1: one row of x per problem (planes_i8_kernel, planes_m1_kernel); M = 2..4: up to 4 rows
+// staged in LDS (planes_kernel, 16 waves), measured faster there than planes_xr_kernel, which
+// serves M = 5..16 and every batch whose x does not fit LDS.
 void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
                     hipStream_t st) {
     require(count >= 1 && count <= CFH_MAX_BATCH, "count must be in 1..8");
     require(problems != nullptr, "problems must not be NULL");
-    require(m >= 1 && m <= 8, "the GEMV planes kernel takes M = 1..8");
+    require(m >= 1 && m <= 16, "the GEMV planes kernels take M = 1..16");
     require(y_dtype == CFH_DTYPE_F32 || y_dtype == CFH_DTYPE_BF16, "y_dtype must be F32 or BF16");
-    const int mr = m == 1 ? 1 : m <= 4 ? 4 : 8;
-    const int nw = mr == 8 ? CFH_PLANES_WAVES8 : kWaves;
+    const int mr = m == 1 ? 1 : 4;
     const int W = cu_count() * kWgPerCu;
-    const int esz = y_dtype == CFH_DTYPE_BF16 ? 2 : 4;
     for (int i = 0; i < count; ++i) {
         const cfh_w4a16_problem_t &q = problems[i];
         require(q.group == kGroup, "GEMV planes hold INT4 groups of 128");
@@ -1284,6 +1656,10 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
                 "x and codes planes must be 16-byte aligned, scales and y 4-byte aligned");
         require(((q.n + 15) / 16) * (q.k / kGroup) * 1024 < (int64_t(1) << 31),
                 "GEMV planes of one matrix must stay below 2 GiB");
+    }
+    if (m > CFH_PLANES_XR_FROM - 1) {
+        planes_xr_batched(problems, count, m, y_dtype, st);
+        return;
     }
     if (m == 1 && CFH_PLANES_M1_GENERIC) {
         std::vector<int64_t> bytes, units;
@@ -1325,65 +1701,45 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
         launch_planes_m1<1, kKindInt4>(nb, ngrid, std::max<int64_t>(need_max, kLdsFloor), st);
         return;
     }
-    // row groups: rows [r0, r0 + rows) of problem src
-    struct Group {
-        int src, r0, rows;
-    };
-    std::vector<int> split4(static_cast<size_t>(count), 0);  // problems whose groups hold 4 rows
-    PBatch<kMaxP> b{};
+    // M = 1 (the generic build) and M = 2..4: x of every problem staged in LDS, one problem per
+    // matrix; M = 2..4 takes planes_xr_kernel where x does not fit
+    PBatch<CFH_MAX_BATCH> b{};
     int64_t lds_max = 0, grid = 0;
-    for (int attempt = 0; attempt <= count; ++attempt) {  // each retry splits at least one more problem
-        std::vector<Group> groups;
-        for (int i = 0; i < count; ++i) {
-            const int gr = mr == 8 && split4[static_cast<size_t>(i)] ? 4 : mr;
-            for (int r0 = 0; r0 < m; r0 += gr) groups.push_back({i, r0, static_cast<int>(std::min<int64_t>(gr, m - r0))});
-        }
-        require(groups.size() <= static_cast<size_t>(kMaxP), "too many problems for one launch");
-        std::vector<int64_t> bytes, units;
-        for (const Group &g : groups) {
-            const cfh_w4a16_problem_t &q = problems[g.src];
-            bytes.push_back(((q.n + 15) / 16) * (q.k / kGroup) * 1024);
-            units.push_back((q.n + 7) / 8);
-        }
-        const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
-        b = PBatch<kMaxP>{};
-        lds_max = 0;
-        grid = 0;
-        bool retry = false;
-        for (size_t j = 0; j < groups.size(); ++j) {
-            const Group &g = groups[j];
-            const cfh_w4a16_problem_t &q = problems[g.src];
-            PProblem &P = b.p[j];
-            P.codes = reinterpret_cast<const uint8_t *>(q.codes);
-            P.scales = q.scales_f16;
-            P.zeros = reinterpret_cast<const uint8_t *>(q.zeros);
-            P.x = q.x + static_cast<int64_t>(g.r0) * q.k;
-            P.y = static_cast<uint8_t *>(q.y) + static_cast<int64_t>(g.r0) * q.n * esz;
-            P.n = static_cast<int32_t>(q.n);
-            P.G = static_cast<int32_t>(q.k / kGroup);
-            P.units = static_cast<int32_t>(units[j]);
-            P.wg0 = static_cast<int32_t>(grid);
-            P.wgs = wgs[j];
-            P.m = g.rows;
-            require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
-            grid += P.wgs;
-            const int64_t need = planes_lds(mr, nw, P);
-            if (need > kLdsMax / kWgPerCu && mr == 8 && g.rows > 4 && !split4[static_cast<size_t>(g.src)]) {
-                split4[static_cast<size_t>(g.src)] = 1;
-                retry = true;
-            }
-            lds_max = std::max<int64_t>(lds_max, need);
-        }
-        b.count = static_cast<int32_t>(groups.size());
-        if (!retry) break;
+    std::vector<int64_t> bytes, units;
+    for (int i = 0; i < count; ++i) {
+        bytes.push_back(((problems[i].n + 15) / 16) * (problems[i].k / kGroup) * 1024);
+        units.push_back((problems[i].n + 7) / 8);
     }
+    const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+    for (int j = 0; j < count; ++j) {
+        const cfh_w4a16_problem_t &q = problems[j];
+        PProblem &P = b.p[j];
+        P.codes = reinterpret_cast<const uint8_t *>(q.codes);
+        P.scales = q.scales_f16;
+        P.zeros = reinterpret_cast<const uint8_t *>(q.zeros);
+        P.x = q.x;
+        P.y = q.y;
+        P.n = static_cast<int32_t>(q.n);
+        P.G = static_cast<int32_t>(q.k / kGroup);
+        P.units = static_cast<int32_t>(units[static_cast<size_t>(j)]);
+        P.wg0 = static_cast<int32_t>(grid);
+        P.wgs = wgs[static_cast<size_t>(j)];
+        P.m = static_cast<int32_t>(m);
+        require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
+        grid += P.wgs;
+        lds_max = std::max<int64_t>(lds_max, planes_lds(mr, kWaves, P));
+    }
+    b.count = count;
     b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
+    if (lds_max > kLdsMax / kWgPerCu && m >= 2) {
+        planes_xr_batched(problems, count, m, y_dtype, st);
+        return;
+    }
     require(lds_max <= kLdsMax / kWgPerCu, "a problem of the batch exceeds the GEMV planes kernel's LDS (m * k too large "
                                 "or too many rows per workgroup)");
     const int64_t req = std::max<int64_t>(lds_max, kLdsFloor);
     if (mr == 1) launch_planes<kWaves, kDepth, 1>(b, grid, req, st);
-    else if (mr == 4) launch_planes<kWaves, kDepth, 4>(b, grid, req, st);
-    else launch_planes<CFH_PLANES_WAVES8, CFH_PLANES_DEPTH8, 8>(b, grid, req, st);
+    else launch_planes<kWaves, kDepth, 4>(b, grid, req, st);
 }
 
 template <int NBPC, int KIND>

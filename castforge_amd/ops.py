@@ -366,13 +366,13 @@ def int4g_from_planes(pl: Int4Planes) -> Int4Packed:
 
 
 def gemv_w4a16_planes_batched(xs: list[torch.Tensor], ps: list[Int4Planes], ys: list[torch.Tensor]) -> None:
-    """Decode (M = 1..8 rows of x, the same M for every problem) over GEMV planes, all problems
+    """Decode (M = 1..16 rows of x, the same M for every problem) over GEMV planes, all problems
     in one launch (one workgroup per CU)."""
     if not (len(xs) == len(ps) == len(ys)) or not 1 <= len(ps) <= ffi.MAX_BATCH:
         raise ValueError("xs, ps, ys must have the same length in 1..8")
     m = xs[0].shape[0] if xs[0].dim() == 2 else 0
-    if not 1 <= m <= 8:
-        raise ValueError("the GEMV planes kernel takes x of 1..8 rows")
+    if not 1 <= m <= 16:
+        raise ValueError("the GEMV planes kernels take x of 1..16 rows")
     yd = _check_batch(xs, ys, m, [p.n for p in ps], [p.k for p in ps])
     arr = (ffi.W4A16Problem * len(ps))()
     for i, (x, p, y) in enumerate(zip(xs, ps, ys)):
@@ -381,7 +381,7 @@ def gemv_w4a16_planes_batched(xs: list[torch.Tensor], ps: list[Int4Planes], ys: 
 
 
 def gemv_w4a16_planes(x: torch.Tensor, p: Int4Planes, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """y [M, n] for x bf16 [M, k], M = 1..8, over GEMV planes."""
+    """y [M, n] for x bf16 [M, k], M = 1..16, over GEMV planes."""
     y = torch.empty((x.shape[0] if x.dim() == 2 else 1, p.n), dtype=out_dtype, device=x.device)
     gemv_w4a16_planes_batched([x], [p], [y])
     return y

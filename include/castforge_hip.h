@@ -239,16 +239,15 @@ int32_t castforge_hip_int4g_from_planes(const void *planes_codes, const uint16_t
                                         uint32_t *codes, uint16_t *scales_f16, uint32_t *zeros, void *stream,
                                         char **out_error);
 
-/* castforge_hip_gemv_w4a16_batched at M = 1..8 over GEMV planes (codes / scales_f16 / zeros of
+/* castforge_hip_gemv_w4a16_batched at M = 1..16 over GEMV planes (codes / scales_f16 / zeros of
  * each problem point at its planes; group 128, k % 128 == 0, x [m, k] and codes 16-byte
  * aligned, y [m, n]): the decode GEMV of `castforge.fused_qmatmul` (codegen/eval.rs:1145-1179,
- * eval_matmul_2d eval.rs:1465-1507) in one launch of one workgroup per CU.  Every finite bf16 x
- * is handled exactly (a power-of-two pre-scale per row and 128 activations, undone on the f32
- * partial); a non-finite x gives NaN or inf in the rows it reaches.  M = 5..8: a problem whose
- * 8 rows of x do not fit the kernel's LDS runs as two problems of 4 rows, each streaming the
- * planes.  A problem's activations must fit the kernel's LDS (about 2.1 * rows * k bytes plus
- * 1, 4 or 4 KB per 16 rows a workgroup takes: rows * k up to about 65536 for the shapes of a
- * decoder); M > 8 runs on the canonical layout (castforge_hip_gemv_w4a16_batched). */
+ * eval_matmul_2d eval.rs:1465-1507) in one launch of one workgroup per CU, every matrix's planes
+ * streamed once.  Every finite bf16 x is handled exactly (a power-of-two pre-scale per row and
+ * 128 activations, undone on the f32 partial); a non-finite x gives NaN or inf in the rows it
+ * reaches.  M = 1: a problem's activations must fit the kernel's LDS (about 2.1 * k bytes; k up
+ * to about 65536).  M = 2..16: any k; a workgroup's partials (4 to 8 KB per 16 rows it takes)
+ * must fit LDS, which a matrix that would exceed it meets by taking more workgroups. */
 int32_t castforge_hip_gemv_w4a16_planes_batched(const cfh_w4a16_problem_t *problems, int32_t count,
                                                 int64_t m, int32_t y_dtype, void *stream, char **out_error);
 

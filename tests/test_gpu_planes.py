@@ -1,4 +1,4 @@
-"""GEMV planes: the INT4 g128 layout the decode kernel (M = 1..8) streams, and that kernel.
+"""GEMV planes: the INT4 g128 layout the decode kernels (M = 1..16) stream, and those kernels.
 
 * The planes equal a numpy construction from the canonical arrays and convert back bit for bit.
 * y matches the oracle's evaluator semantics (dequantize, then eval_matmul_2d, eval.rs:1465-1507)
@@ -77,7 +77,7 @@ def test_planes_layout_and_round_trip(cuda, n, k):
     assert np.array_equal(back.zeros.cpu().numpy().view(np.uint32), zeros)
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 8, 9, 12, 16])
 @pytest.mark.parametrize("n,k", [(48, 256), (100, 1024), (7, 128), (4097, 4096), (64, 11008), (4096, 4096)])
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
 def test_planes_gemv_matches_oracle(cuda, m, n, k, out):
@@ -93,7 +93,7 @@ def test_planes_gemv_matches_oracle(cuda, m, n, k, out):
     _close(y, ref)
 
 
-@pytest.mark.parametrize("m", [1, 4, 5, 8])
+@pytest.mark.parametrize("m", [1, 4, 5, 8, 16])
 @pytest.mark.parametrize("shared_x", [True, False])
 def test_planes_llama_block_batched(cuda, shared_x, m):
     """The 7 projections of a LLaMA-7B block in one launch (x shared by q/k/v and by gate/up as in
@@ -126,7 +126,7 @@ def test_planes_llama_block_batched(cuda, shared_x, m):
         assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("m", [1, 3, 7])
+@pytest.mark.parametrize("m", [1, 3, 7, 12])
 def test_planes_power_of_two_scale_invariance(cuda, m):
     """y(2^e x) == 2^e y(x) bit for bit for every row, e in -100..100: each chunk of x is brought
     to the same f16 values whatever its power-of-two scale.  e >= 16 puts |x| beyond f16's
@@ -174,7 +174,7 @@ def test_planes_large_and_tiny_activations_vs_oracle(cuda):
     assert np.all(np.abs(y - exact) <= ATOL + RTOL * np.abs(exact) + ref_err)
 
 
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
 def test_planes_exact_cancellation(cuda, m):
     """x = [v, -v] with |v| up to 6e4 against weights whose two K halves are equal: the exact
     answer is 0 for every row, reached only through partial sums of order 1e4.  The oracle's
@@ -198,6 +198,39 @@ def test_planes_exact_cancellation(cuda, m):
     assert np.abs(y).max() <= np.abs(ref).max()
 
 
+@pytest.mark.parametrize("m,k", [(2, 40960), (4, 40960), (16, 40960)])
+def test_planes_long_rows_vs_oracle(cuda, m, k):
+    """x of M = 2..4 rows too long for the LDS-staged kernel (about 2.1 M k bytes) runs on the
+    kernel that keeps x in registers, as M = 5..16 does at any K."""
+    n = 40
+    w = synth.weight(71, 1, n, k)
+    p, (codes, scales, zeros) = _packed(w, cuda)
+    pl = ops.int4g_to_planes(p)
+    xb = synth.activations_bf16(72, 7, m, k)
+    y = ops.gemv_w4a16_planes(_xdev(xb, cuda), pl, torch.float32)
+    _close(y, O.gemm_w4a16(xb, codes, scales, zeros, n, k, 128))
+
+
+@pytest.mark.parametrize("m", [3, 8, 16])
+def test_planes_nonfinite_row_stays_in_its_row(cuda, m):
+    """An inf in one row of x makes that row's outputs non-finite and leaves the other rows'
+    outputs finite and equal to the oracle's (each row has its own per-chunk power of two)."""
+    n, k = 64, 1024
+    w = synth.weight(73, 1, n, k)
+    p, (codes, scales, zeros) = _packed(w, cuda)
+    pl = ops.int4g_to_planes(p)
+    xb = synth.activations_bf16(74, 7, m, k)
+    bad = m - 2
+    x = O.bf16_bits_to_f32(xb).reshape(m, k).copy()
+    x[bad, 300] = np.inf
+    xb = O.f32_to_bf16_bits(x)
+    y = ops.gemv_w4a16_planes(_xdev(xb, cuda), pl, torch.float32).cpu().numpy()
+    assert not np.isfinite(y[bad]).any()
+    ok = [r for r in range(m) if r != bad]
+    ref = O.gemm_w4a16(xb, codes, scales, zeros, n, k, 128).reshape(m, n)
+    _close(torch.from_numpy(y[ok]), ref[ok])
+
+
 def test_planes_nonfinite_x_gives_nonfinite_rows(cuda):
     n, k = 32, 256
     w = synth.weight(69, 1, n, k)
@@ -218,10 +251,10 @@ def test_planes_rejects_bad_arguments(cuda):
     arr = (ffi.W4A16Problem * 1)()
     arr[0] = ffi.W4A16Problem(x.data_ptr(), pl.codes.data_ptr(), pl.scales.data_ptr(), pl.zeros.data_ptr(),
                               y.data_ptr(), 32, 256, 128)
-    with pytest.raises(ffi.CastForgeHipError, match="M = 1..8"):
-        ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 9, ffi.DTYPE_F32, None)
-    with pytest.raises(ValueError, match="1..8 rows"):
-        ops.gemv_w4a16_planes(torch.zeros((9, 256), dtype=torch.bfloat16, device=cuda), pl)
+    with pytest.raises(ffi.CastForgeHipError, match="M = 1..16"):
+        ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 17, ffi.DTYPE_F32, None)
+    with pytest.raises(ValueError, match="1..16 rows"):
+        ops.gemv_w4a16_planes(torch.zeros((17, 256), dtype=torch.bfloat16, device=cuda), pl)
     arr[0].group = 64
     with pytest.raises(ffi.CastForgeHipError, match="groups of 128"):
         ffi.call("castforge_hip_gemv_w4a16_planes_batched", arr, 1, 1, ffi.DTYPE_F32, None)
