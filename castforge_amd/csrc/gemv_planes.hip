@@ -692,6 +692,9 @@ constexpr int kNf4Depth = CFH_NF4_PLANES_DEPTH;
 #define CFH_PLANES_I4_DEPTH 2  // the INT4 kind of the kernel below (M = 1 over INT4 GEMV planes)
 #endif
 constexpr int kI4Depth = CFH_PLANES_I4_DEPTH;
+#ifndef CFH_PLANES_M1_SPLIT
+#define CFH_PLANES_M1_SPLIT 1  // M = 1 INT4 work split: 1 whole tiles, least largest share; 0 by bytes, 8-row units
+#endif
 #ifndef CFH_PLANES_XR_FROM
 #define CFH_PLANES_XR_FROM 5  // M from which planes_xr_kernel serves every batch (2..5)
 #endif
@@ -713,7 +716,8 @@ struct NProblem {
     const uint8_t *zeros;  // INT4: zero-point planes
     const uint16_t *x;     // bf16 [1, K]
     void *y;
-    int32_t n, G, units, wg0, wgs, pad;
+    int32_t n, G, units, wg0, wgs;
+    int32_t ush;  // a unit is 8 << ush rows (0: half tiles, 1: whole tiles)
 };
 static_assert(sizeof(NProblem) == 64, "one problem record, 64 bytes");
 
@@ -762,8 +766,9 @@ void planes_m1_kernel(NBatch b) {
     const int G = P.G, local = w - P.wg0;
     const int u0 = static_cast<int>(static_cast<uint32_t>(local * P.units) / static_cast<uint32_t>(P.wgs));
     const int u1 = static_cast<int>(static_cast<uint32_t>((local + 1) * P.units) / static_cast<uint32_t>(P.wgs));
-    const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
-    const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
+    const int r0 = u0 << (3 + P.ush), r1 = u1 << (3 + P.ush);
+    const int rlo = r0, rhi = min(r1, P.n);
+    const int t0 = r0 >> 4, t1 = u1 > u0 ? (r1 + 15) >> 4 : t0;
     const int ntiles = t1 - t0, npos = ntiles * G;
     const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2);
     constexpr uint32_t xoff = KIND == kKindNf4 ? kNf4LutBytes : 0u;
@@ -1047,10 +1052,10 @@ void planes_m1_kernel(NBatch b) {
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kI8ChunkX = 512;
 constexpr uint32_t kI8ChunkRec = 16;
-// positions a wave loads into registers of their own ahead of the ring, after its x has landed
-// (x first: weight loads issued together with x delay every CU's x behind the others' weight
-// traffic).  More in flight per CU is slower: E = 1 / 4 / 6 / 8 over D = 2 measured 20.22 /
-// 20.46 / 20.85 / 21.18 us.
+// positions a wave loads into registers of their own ahead of the ring.  The E + D positions
+// are issued right behind the wave's x loads, before x is awaited (19.87 against 20.00 us with
+// x awaited first); more in flight per CU is slower: E = 1 / 4 / 6 / 8 over D = 2 measured
+// 20.22 / 20.46 / 20.85 / 21.18 us with x awaited first, and D = 3 20.48 against 19.87 us.
 constexpr int kI8Pre = 1;
 
 template <int NW, int D>
@@ -1071,8 +1076,9 @@ void planes_i8_kernel(NBatch b) {
     const int G = P.G, local = w - P.wg0;
     const int u0 = static_cast<int>(static_cast<uint32_t>(local * P.units) / static_cast<uint32_t>(P.wgs));
     const int u1 = static_cast<int>(static_cast<uint32_t>((local + 1) * P.units) / static_cast<uint32_t>(P.wgs));
-    const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
-    const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
+    const int r0 = u0 << (3 + P.ush), r1 = u1 << (3 + P.ush);
+    const int rlo = r0, rhi = min(r1, P.n);
+    const int t0 = r0 >> 4, t1 = u1 > u0 ? (r1 + 15) >> 4 : t0;
     const int ntiles = t1 - t0, npos = ntiles * G;
     const uint32_t rowb = static_cast<uint32_t>(G) * (kGroup * 2);
     const uint32_t soff = static_cast<uint32_t>(G) * kI8ChunkX;
@@ -1080,7 +1086,7 @@ void planes_i8_kernel(NBatch b) {
     float *const accs = reinterpret_cast<float *>(lds + aoff);
 
     // x first (straight into registers, 16 bytes a lane: wave load i holds chunks 4 i .. 4 i + 3,
-    // lane (c4, j) elements 8 j .. 8 j + 7 of chunk 4 i + c4); the weight loads once it has landed
+    // lane (c4, j) elements 8 j .. 8 j + 7 of chunk 4 i + c4), then the weight ring
     const int nxl = (G + 3) >> 2;
     const rsrc_t rx = make_rsrc(P.x, rowb);
     uint4 xr[kXRegs];
@@ -1091,7 +1097,6 @@ void planes_i8_kernel(NBatch b) {
                                               rx, (xl < nxl ? 0u : kOob) | (lane * 16u), static_cast<uint32_t>(xl) * 1024u, 0));
     });
 
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0) & ~(15 << 8));  // see kI8Pre
     const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
     const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
     const rsrc_t rscale = make_rsrc(P.absmax, chunks * 32u);
@@ -1562,6 +1567,54 @@ std::vector<int> workgroups_balanced(const std::vector<int64_t> &bytes, const st
     return wgs;
 }
 
+// Whole tiles per workgroup, the largest number of 1 KB positions a workgroup streams made as
+// small as W workgroups allow: the least L with sum ceil(tiles[i] / floor(L / groups[i])) <= W,
+// then the remaining workgroups one at a time to the problem whose workgroups stream most.  (A
+// workgroup's time follows the positions it touches, and a tile split between two workgroups
+// costs each of them a full position per chunk.)
+std::vector<int> workgroups_whole_tiles(const std::vector<int64_t> &tiles, const std::vector<int64_t> &groups, int W) {
+    const size_t n = tiles.size();
+    auto need = [&](int64_t L) {
+        int64_t t = 0;
+        for (size_t i = 0; i < n; ++i) {
+            const int64_t per = L / groups[i];
+            if (per < 1) return int64_t(W) + 1;
+            t += (tiles[i] + per - 1) / per;
+        }
+        return t;
+    };
+    int64_t lo = 1, hi = 1;
+    for (size_t i = 0; i < n; ++i) hi = std::max(hi, tiles[i] * groups[i]);
+    while (lo < hi) {  // least L with need(L) <= W (need(hi) = count <= W)
+        const int64_t mid = (lo + hi) / 2;
+        if (need(mid) <= W) hi = mid;
+        else lo = mid + 1;
+    }
+    std::vector<int> wgs(n);
+    int used = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const int64_t per = lo / groups[i];
+        wgs[i] = static_cast<int>((tiles[i] + per - 1) / per);
+        used += wgs[i];
+    }
+    while (used < W) {
+        size_t best = n;
+        int64_t most = -1;
+        for (size_t i = 0; i < n; ++i) {
+            if (wgs[i] >= tiles[i]) continue;
+            const int64_t pos = (tiles[i] + wgs[i] - 1) / wgs[i] * groups[i];
+            if (pos > most) {
+                most = pos;
+                best = i;
+            }
+        }
+        if (best == n) break;
+        ++wgs[best];
+        ++used;
+    }
+    return wgs;
+}
+
 // tiles one workgroup of a problem spans at most, for `units` 8-row units over `wgs` workgroups
 int64_t planes_tiles(int64_t units, int64_t wgs) { return (units + wgs - 1) / wgs / 2 + 2; }
 
@@ -1662,12 +1715,24 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
         return;
     }
     if (m == 1 && CFH_PLANES_M1_GENERIC) {
-        std::vector<int64_t> bytes, units;
+        std::vector<int64_t> bytes, units, tiles, groups;
         for (int i = 0; i < count; ++i) {
             bytes.push_back(((problems[i].n + 15) / 16) * (problems[i].k / kGroup) * 1024);
             units.push_back((problems[i].n + 7) / 8);
+            tiles.push_back((problems[i].n + 15) / 16);
+            groups.push_back(problems[i].k / kGroup);
         }
-        const std::vector<int> wgs = workgroups_per_problem(bytes, units, W);
+        std::vector<int> wgs;
+        std::vector<int> ush(static_cast<size_t>(count), 0);
+        if (CFH_PLANES_M1_SPLIT == 1) {
+            wgs = workgroups_whole_tiles(tiles, groups, W);
+            for (int i = 0; i < count; ++i) {
+                units[static_cast<size_t>(i)] = tiles[static_cast<size_t>(i)];
+                ush[static_cast<size_t>(i)] = 1;
+            }
+        } else {
+            wgs = workgroups_per_problem(bytes, units, W);
+        }
         NBatch nb{};
         int64_t need_max = 0, need_i8 = 0, ngrid = 0;
         for (int j = 0; j < count; ++j) {
@@ -1683,9 +1748,10 @@ void planes_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t 
             P.units = static_cast<int32_t>(units[static_cast<size_t>(j)]);
             P.wg0 = static_cast<int32_t>(ngrid);
             P.wgs = wgs[static_cast<size_t>(j)];
+            P.ush = ush[static_cast<size_t>(j)];
             require(static_cast<int64_t>(P.wgs) * P.units < (int64_t(1) << 31), "too many rows for one launch");
             ngrid += P.wgs;
-            const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / 2 + 2;
+            const int64_t tiles = (P.units + P.wgs - 1) / P.wgs / (2 - P.ush) + 2;
             need_max = std::max<int64_t>(need_max, int64_t(P.G) * 256 + (int64_t(P.G) * 4 + 15) / 16 * 16 +
                                                        tiles * kWaves * 64);
             need_i8 = std::max<int64_t>(need_i8, int64_t(P.G) * (kI8ChunkX + kI8ChunkRec) + tiles * kWaves * 64);
