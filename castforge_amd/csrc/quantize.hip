@@ -807,6 +807,75 @@ __device__ __forceinline__ void hadamard16_lanes_fast(float (&x)[16], int rot_b,
     for (int i = 0; i < 16; ++i) x[i] *= f;
 }
 
+// One row's group scales, codes and zero words from each thread's 16 values x (pre-scaled and
+// rotated already): min/max over the group's lanes, f16 scale, codes x / s + z packed 8 per word.
+template <int GROUP>
+__device__ __forceinline__ void int4g16_row(float (&x)[16], int64_t row, int par, uint32_t *__restrict__ rcodes,
+                                            uint16_t *__restrict__ rscales, uint32_t *__restrict__ zeros, uint32_t G,
+                                            uint32_t ZW, uint32_t zw, int t, bool task_ok, uint32_t w0, bool ok0,
+                                            bool ok1, uint32_t (&zpart)[2][kBlock / 64]) {
+    constexpr int TPG = GROUP / 16;  // threads per group
+    constexpr int T = 8 * TPG;       // threads per task
+    float mx = -INFINITY, mn = INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (h == 0 ? ok0 : ok1) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, x[8 * h + i]); mn = fminf(mn, x[8 * h + i]); }
+        }
+    }
+    mx = group_reduce_max<TPG>(mx);
+    mn = group_reduce_min<TPG>(mn);
+    const uint16_t hs = int4_scale_bits(mx, mn);
+    const float s = f16_to_f32(hs);
+    float zf = rintf(-mn / s);
+    if (zf != zf) zf = 0.0f;
+    zf = fminf(fmaxf(zf, 0.0f), 15.0f);
+    const float y = 1.0f / s;
+    const int gi = t / TPG;  // group within the task
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        if (h == 0 ? ok0 : ok1) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float r = rintf(div_by_scale(x[8 * h + i], s, y, 64.0f));
+                if (r != r) r = 0.0f;
+                const float qf = fminf(fmaxf(r + zf, 0.0f), 15.0f);
+                word |= static_cast<uint32_t>(qf) << (4 * i);
+            }
+            rcodes[w0 + h] = word;
+        }
+    }
+    uint32_t zn = 0;
+    if (t % TPG == 0) {
+        if (ok0) {
+            rscales[zw * 8 + gi] = hs;
+            zn = static_cast<uint32_t>(zf) << (4 * gi);
+        } else if (task_ok && zw * 8 + gi >= G) {
+            rscales[zw * 8 + gi] = 0;  // pad scale slots of the last 8-group block
+        }
+    }
+    if constexpr (T <= 64) {
+        zn = wave_or<T>(zn);
+        if (t == 0 && task_ok) zeros[row * ZW + zw] = zn;
+    } else {
+        // alternate buffers: a row's readers finish before the barrier of the next row,
+        // which comes before the row after it overwrites their buffer
+        uint32_t *zp = zpart[par];
+        zn = wave_or<64>(zn);
+        if ((threadIdx.x & 63) == 0) zp[threadIdx.x >> 6] = zn;
+        __syncthreads();
+        if (t == 0 && task_ok) {
+            uint32_t z = 0;
+            const int w0i = (threadIdx.x >> 6);
+#pragma unroll
+            for (int i = 0; i < T / 64; ++i) z |= zp[w0i + i];
+            zeros[row * ZW + zw] = z;
+        }
+    }
+}
+
 // R rows per grid row (R > 1 when every matrix of the launch has a multiple of R rows): the
 // AWQ pre-scale of the thread's 16 columns is loaded once and serves all R rows.
 template <int GROUP, int R>
@@ -877,70 +946,13 @@ __global__ __launch_bounds__(kBlock) void int4g_quant16_kernel(RowSets<float> se
         uint32_t *rcodes = codes + row * KW;
         uint16_t *rscales = scales + row * GP;
         float (&x)[16] = xr[rr];
-        float mx = -INFINITY, mn = INFINITY;
         if (in_scale) {  // uniform
 #pragma unroll
             for (int i = 0; i < 16; ++i) x[i] *= sc[i];  // 0 * 1 outside the row
         }
         if (fast_rot) hadamard16_lanes_fast(x, rot_b, rot_norm, static_cast<int>(threadIdx.x));  // uniform
         else if (rot_b > 1) hadamard16_lanes(x, rot_b, rot_norm);  // uniform: every lane takes part
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (h == 0 ? ok0 : ok1) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) { mx = fmaxf(mx, x[8 * h + i]); mn = fminf(mn, x[8 * h + i]); }
-            }
-        }
-        mx = group_reduce_max<TPG>(mx);
-        mn = group_reduce_min<TPG>(mn);
-        const uint16_t hs = int4_scale_bits(mx, mn);
-        const float s = f16_to_f32(hs);
-        float zf = rintf(-mn / s);
-        if (zf != zf) zf = 0.0f;
-        zf = fminf(fmaxf(zf, 0.0f), 15.0f);
-        const float y = 1.0f / s;
-        const int gi = t / TPG;  // group within the task
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (h == 0 ? ok0 : ok1) {
-                uint32_t word = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    float r = rintf(div_by_scale(x[8 * h + i], s, y, 64.0f));
-                    if (r != r) r = 0.0f;
-                    const float qf = fminf(fmaxf(r + zf, 0.0f), 15.0f);
-                    word |= static_cast<uint32_t>(qf) << (4 * i);
-                }
-                rcodes[w0 + h] = word;
-            }
-        }
-        uint32_t zn = 0;
-        if (t % TPG == 0) {
-            if (ok0) {
-                rscales[zw * 8 + gi] = hs;
-                zn = static_cast<uint32_t>(zf) << (4 * gi);
-            } else if (task_ok && zw * 8 + gi >= G) {
-                rscales[zw * 8 + gi] = 0;  // pad scale slots of the last 8-group block
-            }
-        }
-        if constexpr (T <= 64) {
-            zn = wave_or<T>(zn);
-            if (t == 0 && task_ok) zeros[row * ZW + zw] = zn;
-        } else {
-            // alternate buffers: a row's readers finish before the barrier of the next row,
-            // which comes before the row after it overwrites their buffer
-            uint32_t *zp = zpart[rr & 1];
-            zn = wave_or<64>(zn);
-            if ((threadIdx.x & 63) == 0) zp[threadIdx.x >> 6] = zn;
-            __syncthreads();
-            if (t == 0 && task_ok) {
-                uint32_t z = 0;
-                const int w0i = (threadIdx.x >> 6);
-#pragma unroll
-                for (int i = 0; i < T / 64; ++i) z |= zp[w0i + i];
-                zeros[row * ZW + zw] = z;
-            }
-        }
+        int4g16_row<GROUP>(x, row, rr & 1, rcodes, rscales, zeros, G, ZW, zw, t, task_ok, w0, ok0, ok1, zpart);
     }
 }
 
