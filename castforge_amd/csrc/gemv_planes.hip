@@ -429,8 +429,14 @@ void planes_kernel(PBatch<CFH_MAX_BATCH> b) {
 #ifndef CFH_PLANES_XR_DEPTH16
 #define CFH_PLANES_XR_DEPTH16 4
 #endif
+// the cost of converting one x value in streamed bytes, for the work split (MR = 4, 8 / MR = 16;
+// measured at M = 8: 1.0 best of 1..3; at M = 16: 39.3 / 37.3 / 36.7 / 36.6 us for 1 / 1.5 / 2 /
+// 2.5)
 #ifndef CFH_PLANES_XR_XCOST
 #define CFH_PLANES_XR_XCOST 1.0
+#endif
+#ifndef CFH_PLANES_XR_XCOST16
+#define CFH_PLANES_XR_XCOST16 2.0
 #endif
 #ifndef CFH_PLANES_XR_TILES
 #define CFH_PLANES_XR_TILES 1
@@ -1527,21 +1533,25 @@ void launch_planes_xr(const PBatch<CFH_MAX_BATCH> &b, int64_t grid, int64_t lds,
 }
 
 // workgroups per problem such that bytes[i] / wgs[i] + fixed[i] is about equal over the problems
-// (fixed: work every workgroup of problem i does whatever its share), at most units[i] each and W
-// in total (at least one each): the level T solves sum bytes[i] / (T - fixed[i]) = W, the shares
-// are rounded by largest remainder.  All fixed equal to 0 is workgroups_per_problem's split.
+// (fixed: work every workgroup of problem i does whatever its share), at least lo[i] (>= 1) and
+// at most units[i] each and W in total: the level T solves sum max(lo[i], bytes[i] / (T -
+// fixed[i])) = W, the shares are rounded by largest remainder.  All fixed equal to 0 and lo to 1
+// is workgroups_per_problem's split.
 std::vector<int> workgroups_balanced(const std::vector<int64_t> &bytes, const std::vector<int64_t> &fixed,
-                                     const std::vector<int64_t> &units, int W) {
+                                     const std::vector<int64_t> &lo_wgs, const std::vector<int64_t> &units, int W) {
     const size_t n = bytes.size();
     double fmax = 0.0;
     for (int64_t f : fixed) fmax = std::max(fmax, static_cast<double>(f));
+    auto share = [&](size_t i, double T) {
+        return std::max(static_cast<double>(lo_wgs[i]), static_cast<double>(bytes[i]) / (T - static_cast<double>(fixed[i])));
+    };
     auto total = [&](double T) {
         double t = 0.0;
-        for (size_t i = 0; i < n; ++i) t += static_cast<double>(bytes[i]) / (T - static_cast<double>(fixed[i]));
+        for (size_t i = 0; i < n; ++i) t += share(i, T);
         return t;
     };
     double lo = fmax, hi = fmax + 1.0;
-    while (total(hi) > W) hi = fmax + 2.0 * (hi - fmax);
+    for (int it = 0; it < 200 && total(hi) > W; ++it) hi = fmax + 2.0 * (hi - fmax);
     for (int it = 0; it < 100; ++it) {
         const double mid = 0.5 * (lo + hi);
         if (mid <= fmax || total(mid) > W) lo = mid;
@@ -1551,10 +1561,10 @@ std::vector<int> workgroups_balanced(const std::vector<int64_t> &bytes, const st
     int used = 0;
     std::vector<std::pair<double, size_t>> rem;
     for (size_t i = 0; i < n; ++i) {
-        const double share = static_cast<double>(bytes[i]) / (hi - static_cast<double>(fixed[i]));
-        wgs[i] = static_cast<int>(std::min<int64_t>(std::max(1, static_cast<int>(share)), units[i]));
+        const double sh = share(i, hi);
+        wgs[i] = static_cast<int>(std::min<int64_t>(std::max<int64_t>(lo_wgs[i], static_cast<int64_t>(sh)), units[i]));
         used += wgs[i];
-        rem.push_back({share - static_cast<double>(wgs[i]), i});
+        rem.push_back({sh - static_cast<double>(wgs[i]), i});
     }
     std::sort(rem.begin(), rem.end(), [](const auto &a, const auto &c) { return a.first > c.first; });
     for (size_t j = 0; used < W && j < rem.size(); ++j) {
@@ -1615,8 +1625,9 @@ std::vector<int> workgroups_whole_tiles(const std::vector<int64_t> &tiles, const
     return wgs;
 }
 
-// tiles one workgroup of a problem spans at most, for `units` 8-row units over `wgs` workgroups
-int64_t planes_tiles(int64_t units, int64_t wgs) { return (units + wgs - 1) / wgs / 2 + 2; }
+// tiles one workgroup of a problem spans at most, for `units` 8-row units over `wgs` workgroups:
+// U = ceil(units / wgs) units starting at an odd unit touch floor(U / 2) + 1 tiles
+int64_t planes_tiles(int64_t units, int64_t wgs) { return (units + wgs - 1) / wgs / 2 + 1; }
 
 // M = 2..16 on planes_xr_kernel: every problem's planes streamed once, each problem's share of
 // the CUs by its bytes; a problem whose workgroups would span more tiles than their slots fit in
@@ -1628,6 +1639,7 @@ void planes_xr_launch(const cfh_w4a16_problem_t *problems, int32_t count, int64_
     const int64_t slot_bytes = int64_t(NW) * 64 * MR;          // one tile's slots
     const int64_t x_bytes = int64_t(NW) * (int64_t(MR) * 256 + 64);  // the waves' x areas
     const int64_t max_tiles = (kLdsMax / kWgPerCu - x_bytes) / slot_bytes;
+    static_assert((kLdsMax / kWgPerCu - NW * (MR * 256 + 64)) / (NW * 64 * MR) >= 2, "room for two tiles' slots");
     std::vector<int64_t> bytes, units;
     for (int i = 0; i < count; ++i) {
         const cfh_w4a16_problem_t &q = problems[i];
@@ -1637,17 +1649,22 @@ void planes_xr_launch(const cfh_w4a16_problem_t *problems, int32_t count, int64_
     }
     // every workgroup converts its problem's whole x (M x K values) besides streaming its share of
     // the planes: the split equalises bytes / wgs + c M K over the problems (c: the cost of
-    // converting one value in bytes streamed)
-    std::vector<int64_t> xcost;
-    for (int i = 0; i < count; ++i) xcost.push_back(static_cast<int64_t>(CFH_PLANES_XR_XCOST * m * problems[i].k));
-    std::vector<int> wgs = workgroups_balanced(bytes, xcost, units, cu_count() * kWgPerCu);
+    // converting one value in bytes streamed), each problem taking at least the workgroups that
+    // keep its tiles' slots within LDS
+    std::vector<int64_t> xcost, lo_wgs;
+    const double c = MR == 16 ? CFH_PLANES_XR_XCOST16 : CFH_PLANES_XR_XCOST;
+    for (int i = 0; i < count; ++i) {
+        xcost.push_back(static_cast<int64_t>(c * static_cast<double>(m * problems[i].k)));
+        lo_wgs.push_back(std::max<int64_t>(1, (units[static_cast<size_t>(i)] + 2 * (max_tiles - 1) - 1) / (2 * (max_tiles - 1))));
+    }
+    std::vector<int> wgs = workgroups_balanced(bytes, xcost, lo_wgs, units, cu_count() * kWgPerCu);
     PBatch<CFH_MAX_BATCH> b{};
     int64_t lds = 0, grid = 0;
     for (int j = 0; j < count; ++j) {
         const cfh_w4a16_problem_t &q = problems[j];
         int64_t wj = wgs[static_cast<size_t>(j)];
         const int64_t u = units[static_cast<size_t>(j)];
-        if (planes_tiles(u, wj) > max_tiles) wj = std::min<int64_t>(u, (u + 2 * (max_tiles - 2) - 1) / (2 * (max_tiles - 2)));
+        if (planes_tiles(u, wj) > max_tiles) wj = std::min<int64_t>(u, (u + 2 * (max_tiles - 1) - 1) / (2 * (max_tiles - 1)));
         require(planes_tiles(u, wj) <= max_tiles, "a problem's rows exceed the GEMV planes kernel's LDS");
         PProblem &P = b.p[j];
         P.codes = reinterpret_cast<const uint8_t *>(q.codes);
