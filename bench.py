@@ -181,7 +181,7 @@ def main():
     def ev():
         return torch.cuda.Event(enable_timing=True)
 
-    def time_steps(fn, steps, warmup, min_ms=0.0, replays=1, stream=None):
+    def time_steps(fn, steps, warmup, min_ms=20.0, replays=3, stream=None):
         """Milliseconds per step.  `warmup` eager calls of fn(i), then `steps` calls captured
         into one HIP graph (fn enqueues on torch's current stream, which is the capture stream
         during capture), replayed once untimed (graph upload), then replayed at least
