@@ -438,23 +438,16 @@ void planes_kernel(PBatch<CFH_MAX_BATCH> b) {
 #ifndef CFH_PLANES_XR_XCOST16
 #define CFH_PLANES_XR_XCOST16 2.0
 #endif
-#ifndef CFH_PLANES_XR_TILES
-#define CFH_PLANES_XR_TILES 1
-#endif
-#ifndef CFH_PLANES_XR_ROT
-#define CFH_PLANES_XR_ROT 0
-#endif
-
-// one ring stage: TP tiles of one chunk (their codes, scales and zero points) and, when they are
-// the chunk's first, the chunk's x fragment
-template <int TP, int MR>
+// one ring stage: one position's codes, scale and zero point and, when it is its chunk's last
+// tile, the next chunk's x
+template <int MR>
 struct XStage {
-    uint32_t w[TP][4];
-    uint32_t sc[TP], zb[TP];
+    uint32_t w[4];
+    uint32_t sc, zb;
     uint4 x[MR / 4];
 };
 
-template <int NW, int D, int MR, int TP>
+template <int NW, int D, int MR>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW * kWgPerCu / 4)))
 void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
     // a chunk's partial is rounded on its own before it is added (no contraction into an fma):
@@ -478,9 +471,8 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
     const int rlo = 8 * u0, rhi = min(8 * u1, P.n);
     const int t0 = u0 >> 1, t1 = u1 > u0 ? (u1 + 1) >> 1 : t0;
     const int ntiles = t1 - t0;
-    const int ngrp = (ntiles + TP - 1) / TP;  // steps per chunk: TP tiles each (the last may hold dead tiles)
-    constexpr int kSlot = 16 * MR;             // floats of one (tile, wave) slot
-    const bool out_lane = lane < 4 * MR;       // lanes holding D rows 0..MR-1
+    constexpr int kSlot = 16 * MR;        // floats of one (tile, wave) slot
+    const bool out_lane = lane < 4 * MR;  // lanes holding D rows 0..MR-1
     float *const accs = reinterpret_cast<float *>(lds);
     float *const mine = accs + wave * kSlot + 4 * lane;  // slot (t, wave) at mine + t * NW * kSlot
     // this wave's x area after the slots: MR rows of a chunk as f16 (256 bytes each), then their
@@ -491,7 +483,7 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
         if (out_lane) *reinterpret_cast<floatx4 *>(mine + t * NW * kSlot) = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int nc = G > wave ? (G - wave + NW - 1) / NW : 0;  // chunks of this wave
-    const int nsteps = nc * ngrp;
+    const int nsteps = nc * ntiles;
     const uint32_t chunks = static_cast<uint32_t>(((P.n + 15) >> 4) * G);
     const rsrc_t rcode = make_rsrc(P.codes, chunks * 1024u);
     const rsrc_t rscale = make_rsrc(P.scales, chunks * 32u);
@@ -501,7 +493,7 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
     // a chunk's x: load i brings rows 4 i .. 4 i + 3 (clamped to M - 1), 16 bytes a lane
     auto xrow = [&](int i) __attribute__((always_inline)) { return min(4 * i + part, M - 1); };
 
-    int lc = 0, lg = 0;  // load cursor: the wave's chunk index, tile group
+    int lc = 0, lt = 0;  // load cursor: the wave's chunk index, tile (relative to t0)
     auto load_x = [&](uint4 (&xr)[MR / 4], int c) __attribute__((always_inline)) {
         const uint32_t xo = c < nc ? static_cast<uint32_t>(wave + c * NW) * (kGroup * 2) + static_cast<uint32_t>(r16) * 16u : kOob;
         static_for<MR / 4>([&](auto jj) __attribute__((always_inline)) {
@@ -510,30 +502,26 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
                                                   rx, xo + static_cast<uint32_t>(xrow(j)) * rowb, 0, 0));
         });
     };
-    auto load = [&](XStage<TP, MR> &st) __attribute__((always_inline)) {
+    auto load = [&](XStage<MR> &st) __attribute__((always_inline)) {
         const uint32_t g = static_cast<uint32_t>(wave + lc * NW);
-        if (lg == ngrp - 1) load_x(st.x, lc + 1);  // the chunk's last tiles: the next chunk's x first
-        static_for<TP>([&](auto uu) __attribute__((always_inline)) {
-            constexpr int u = decltype(uu)::value;
-            const int lt = lg * TP + u;
-            // rows outside [rlo, rhi), tiles past the workgroup's and chunks past the wave's read
-            // zeros (offsets pushed out of range) and add nothing
-            const int row = (t0 + lt) * 16 + r16;
-            const uint32_t m = lc < nc && lt < ntiles && row >= rlo && row < rhi ? 0u : kOob;
-            const uint32_t chunk = static_cast<uint32_t>(t0 + lt) * static_cast<uint32_t>(G) + g;
-            const uint4 v = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, ((static_cast<uint32_t>(lane) * 16u) | m) + chunk * 1024u,
-                                                             0, CFH_PLANES_CPOL));
-            st.w[u][0] = v.x;
-            st.w[u][1] = v.y;
-            st.w[u][2] = v.z;
-            st.w[u][3] = v.w;
-            st.sc[u] = __builtin_amdgcn_raw_buffer_load_b16(
-                rscale, ((static_cast<uint32_t>(r16) * 2u) | (out_lane ? m : kOob)) + chunk * 32u, 0, 0);
-            st.zb[u] = __builtin_amdgcn_raw_buffer_load_b8(rzero, (static_cast<uint32_t>(r16 >> 1) | m) + chunk * 8u, 0, 0);
-        });
-        if (++lg == ngrp) {
-            lg = 0;
+        if (lt == ntiles - 1) load_x(st.x, lc + 1);  // the chunk's last tile: the next chunk's x first
+        // rows outside [rlo, rhi) and chunks past the wave's read zeros (offsets pushed out of
+        // range) and add nothing
+        const int row = (t0 + lt) * 16 + r16;
+        const uint32_t m = lc < nc && row >= rlo && row < rhi ? 0u : kOob;
+        const uint32_t chunk = static_cast<uint32_t>(t0 + lt) * static_cast<uint32_t>(G) + g;
+        const uint4 v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rcode, ((static_cast<uint32_t>(lane) * 16u) | m) + chunk * 1024u, 0,
+                                                         CFH_PLANES_CPOL));
+        st.w[0] = v.x;
+        st.w[1] = v.y;
+        st.w[2] = v.z;
+        st.w[3] = v.w;
+        st.sc = __builtin_amdgcn_raw_buffer_load_b16(
+            rscale, ((static_cast<uint32_t>(r16) * 2u) | (out_lane ? m : kOob)) + chunk * 32u, 0, 0);
+        st.zb = __builtin_amdgcn_raw_buffer_load_b8(rzero, (static_cast<uint32_t>(r16 >> 1) | m) + chunk * 8u, 0, 0);
+        if (++lt == ntiles) {
+            lt = 0;
             ++lc;
         }
     };
@@ -592,7 +580,7 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
     // the next stage's loads)
     uint4 x0[MR / 4];
     load_x(x0, 0);
-    XStage<TP, MR> st[D];
+    XStage<MR> st[D];
     static_for<D>([&](auto i) __attribute__((always_inline)) {
         load(st[i]);
         __builtin_amdgcn_sched_barrier(0);
@@ -600,19 +588,17 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
     convert(x0);
 
     const uint32_t LO = vgpr_const(0x000F000Fu), HI = vgpr_const(0x00F000F0u), MG = vgpr_const(0x64006400u);
-    int pc = 0, pg = 0;  // process cursor
+    int pc = 0, pt = 0;  // process cursor: the wave's chunk index, tile
     const int steps = (nsteps + D - 1) / D * D;
     for (int k = 0; k < steps; k += D) {
         static_for<D>([&](auto ii) __attribute__((always_inline)) {
             constexpr int i = decltype(ii)::value;
-            XStage<TP, MR> &s = st[i];
-            static_for<TP>([&](auto uu) __attribute__((always_inline)) {
-                constexpr int u = decltype(uu)::value;
-                const int pt = pg * TP + u;
-                const uint32_t w0 = s.w[u][0], w1 = s.w[u][1], w2 = s.w[u][2], w3 = s.w[u][3];
+            XStage<MR> &s = st[i];
+            {
+                const uint32_t w0 = s.w[0], w1 = s.w[1], w2 = s.w[2], w3 = s.w[3];
                 const uint32_t w08 = w0 >> 8, w18 = w1 >> 8, w28 = w2 >> 8, w38 = w3 >> 8;
-                const uint32_t zi = (s.zb[u] >> (4 * (r16 & 1))) & 15u;
-                const float sc = f16_to_f32(static_cast<uint16_t>(s.sc[u]));
+                const uint32_t zi = (s.zb >> (4 * (r16 & 1))) & 15u;
+                const float sc = f16_to_f32(static_cast<uint16_t>(s.sc));
                 // (1024 + q) - (1024 + z) and (1024 + 16 q) / 16 - (64 + z): exact small integers
                 const half2_t zc1024 = as_h2((0xE400u + zi) * 0x00010001u);
                 const half2_t zc64 = as_h2((0xD400u + (zi << 4)) * 0x00010001u);
@@ -627,15 +613,15 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
                 pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1], dec(w1, w18), pb, 0, 0, 0);
                 pa = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2], dec(w2, w28), pa, 0, 0, 0);
                 pb = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[3], dec(w3, w38), pb, 0, 0, 0);
-                if (pc < nc && pt < ntiles && out_lane) {
+                if (pc < nc && out_lane) {
                     floatx4 *dst = reinterpret_cast<floatx4 *>(mine + pt * NW * kSlot);
                     floatx4 a = *dst;
 #pragma unroll
                     for (int q = 0; q < 4; ++q) a[q] = a[q] + (pa[q] + pb[q]) * (sc * post[q]);
                     *dst = a;
                 }
-            });
-            const bool last = pg == ngrp - 1;
+            }
+            const bool last = pt == ntiles - 1;
             // the next chunk's x moved out of the stage (opaque copies: the refill may then load
             // into the stage's own registers, none rotate between iterations)
             uint4 xn[MR / 4];
@@ -649,8 +635,8 @@ void planes_xr_kernel(PBatch<CFH_MAX_BATCH> b) {
                     asm volatile("v_mov_b32 %0, %1" : "=v"(xn[j].w) : "v"(e));
                 }
             }
-            if (++pg == ngrp) {
-                pg = 0;
+            if (++pt == ntiles) {
+                pt = 0;
                 ++pc;
             }
             load(s);
@@ -1512,7 +1498,7 @@ void launch_planes(const PBatch<CFH_MAX_BATCH> &b, int64_t grid, int64_t lds, hi
 }
 
 
-template <int NW, int D, int MR, int TP>
+template <int NW, int D, int MR>
 void launch_planes_xr(const PBatch<CFH_MAX_BATCH> &b, int64_t grid, int64_t lds, hipStream_t st) {
     static std::mutex mu;
     static std::map<int, bool> attr_set;  // per device
@@ -1521,13 +1507,13 @@ void launch_planes_xr(const PBatch<CFH_MAX_BATCH> &b, int64_t grid, int64_t lds,
     {
         std::lock_guard<std::mutex> g(mu);
         if (!attr_set[dev]) {
-            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_xr_kernel<NW, D, MR, TP>),
+            check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(&planes_xr_kernel<NW, D, MR>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax),
                       "hipFuncSetAttribute");
             attr_set[dev] = true;
         }
     }
-    planes_xr_kernel<NW, D, MR, TP>
+    planes_xr_kernel<NW, D, MR>
         <<<dim3(static_cast<unsigned>(grid)), dim3(64 * NW), static_cast<size_t>(lds), st>>>(b);
     check_launch("planes_xr_kernel");
 }
@@ -1635,7 +1621,6 @@ int64_t planes_tiles(int64_t units, int64_t wgs) { return (units + wgs - 1) / wg
 template <int NW, int D, int MR>
 void planes_xr_launch(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
                       hipStream_t st) {
-    constexpr int TP = CFH_PLANES_XR_TILES;
     const int64_t slot_bytes = int64_t(NW) * 64 * MR;          // one tile's slots
     const int64_t x_bytes = int64_t(NW) * (int64_t(MR) * 256 + 64);  // the waves' x areas
     const int64_t max_tiles = (kLdsMax / kWgPerCu - x_bytes) / slot_bytes;
@@ -1684,7 +1669,7 @@ void planes_xr_launch(const cfh_w4a16_problem_t *problems, int32_t count, int64_
     }
     b.count = count;
     b.y_bf16 = y_dtype == CFH_DTYPE_BF16;
-    launch_planes_xr<NW, D, MR, TP>(b, grid, std::max<int64_t>(lds, kLdsFloor), st);
+    launch_planes_xr<NW, D, MR>(b, grid, std::max<int64_t>(lds, kLdsFloor), st);
 }
 
 void planes_xr_batched(const cfh_w4a16_problem_t *problems, int32_t count, int64_t m, int32_t y_dtype,
