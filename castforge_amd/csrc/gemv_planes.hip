@@ -1046,9 +1046,9 @@ constexpr uint32_t kI8ChunkX = 512;
 constexpr uint32_t kI8ChunkRec = 16;
 // positions a wave loads into registers of their own ahead of the ring.  The E + D positions
 // are issued right behind the wave's x loads, before x is awaited (19.87 against 20.00 us with
-// x awaited first); more in flight per CU is slower: E = 1 / 4 / 6 / 8 over D = 2 measured
-// 20.22 / 20.46 / 20.85 / 21.18 us with x awaited first, and D = 3 20.48 against 19.87 us.
-constexpr int kI8Pre = 1;
+// x awaited first).  E = 1 / 2 / 3 over D = 2 that way: 19.85 / 19.72 / 19.97 us (with x
+// awaited first, E = 1 / 4 / 6 / 8: 20.22 / 20.46 / 20.85 / 21.18 us); D = 3: 20.48 us.
+constexpr int kI8Pre = 2;
 
 template <int NW, int D>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4)))
