@@ -291,6 +291,21 @@ def test_fp8_rows_bf16_special_values(cuda):
     assert np.array_equal(codes.cpu().numpy(), c_ref)
 
 
+@pytest.mark.parametrize("c", [1024, 4096, 16384])
+def test_fp8_rows_bf16_finite_rows_beside_special_ones(cuda, c):
+    """Finite rows (the kernel's fast path) next to rows holding an infinity or a NaN (rows 4
+    and 9, its general path) and an all-zero last row, 11 rows in all: every row's bytes and
+    scale equal the oracle's, whichever path its neighbours take."""
+    x = synth.activations_bf16(44, 1, 11, c).copy()
+    x[4, 3] = O.f32_to_bf16_bits(np.array([np.inf], np.float32))[0]
+    x[9, c - 1] = O.f32_to_bf16_bits(np.array([np.nan], np.float32))[0]
+    x[10, :] = O.f32_to_bf16_bits(np.zeros(c, np.float32))
+    c_ref, s_ref = O.quantize_fp8_rows(x)
+    codes, scales = ops.quantize_fp8(torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(cuda))
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(codes.cpu().numpy(), c_ref)
+
+
 # ------------------------------------------------------------- BASELINE block shapes ----
 @pytest.mark.parametrize("name,n,k", synth.LLAMA7B_BLOCK)
 def test_block_int8_channel_and_int4g128_full_size(cuda, name, n, k):
